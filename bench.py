@@ -1,0 +1,244 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X attention hot path (one GPU).
+
+Prints ONE JSON line.  The headline workload is BASELINE.json configs[1]:
+causal GQA prefill, batch 1, S=1371, 16 query / 8 KV heads, head_dim 128,
+bf16 ~ N(0,1) seeded; metric TFLOP/s with the causal FLOP count
+4*S^2*Hq*D/2.  A step is one prefill over that input (one
+toyinfer_flash_attention_v1_bf16 call); W untimed steps, then exactly K
+timed steps between two device synchronisations, timed with HIP events on
+the stream the kernel runs on.
+
+The same line carries, under "components", the other hot-path workloads
+the north-star targets name, each with its own roofline block:
+  * prefill_fused_s8192: configs[3], S=8192, 32/8, QK-RMSNorm + RoPE fused
+    in front (toyinfer_prefill_qknorm_rope_attention_bf16), MFMA-bound;
+  * decode_b8_l4096: configs[2], split-K decode over 128 MiB of KV, HBM-bound;
+  * decode_b1_l32768: the north-star 32k-token decode, 128 MiB of KV.
+Decode steps rotate over 4 independent KV sets (512 MiB) so every step reads
+KV that is not resident in the 256 MB Infinity Cache.
+
+cpu_baseline: the CPU oracle (oracle/, the restated host reference of the
+reference's tests) timed on this host's cores on a bounded sample of the
+headline workload, and used there as the checker of the GPU output.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+METRIC = "prefill attn TFLOP/s + decode attn HBM GB/s (% MI355X roofline), Qwen3 GQA"
+PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
+PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
+SEED = 2026
+
+
+def causal_flops(s, hq, d):
+    return 4.0 * s * s * hq * d / 2.0
+
+
+def parse():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--no-components", action="store_true",
+                    help="only the headline workload")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the cpu_baseline leg")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0,
+                    help="target CPU time of the cpu_baseline sample")
+    return ap.parse_args()
+
+
+def to_dev(bits, dev):
+    import numpy as np
+    import torch
+
+    return torch.from_numpy(np.ascontiguousarray(bits).view(np.int16)).view(torch.bfloat16).to(dev)
+
+
+def to_host(t):
+    import numpy as np
+    import torch
+
+    return t.detach().cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
+
+
+def time_steps(fn, steps, warmup, stream):
+    """Mean ms per step of `fn(i)` over `steps` launches, HIP events on `stream`."""
+    import torch
+
+    with torch.cuda.stream(stream):
+        for i in range(warmup):
+            fn(i)
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    with torch.cuda.stream(stream):
+        for i in range(steps):
+            fn(i)
+    end.record(stream)
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps
+
+
+def roofline(bound, achieved, peak, unit, traffic=None):
+    return {"bound": bound, "achieved": round(achieved, 3), "peak": peak, "unit": unit,
+            "frac": round(achieved / peak, 4), "traffic": traffic}
+
+
+# ------------------------------------------------------------------ prefill
+
+def prefill_inputs(s, hq, hkv, d, dev, seed=SEED):
+    from toyinfer_amd import synth
+
+    qb = synth.normal_bf16(seed, "q", (s, hq, d))
+    kb = synth.normal_bf16(seed, "k", (s, hkv, d))
+    vb = synth.normal_bf16(seed, "v", (s, hkv, d))
+    return (qb, kb, vb), (to_dev(qb, dev), to_dev(kb, dev), to_dev(vb, dev))
+
+
+def bench_prefill(dev, stream, steps, warmup, s=1371, hq=16, hkv=8, d=128):
+    import torch
+
+    from toyinfer_amd import attn
+
+    host, (q, k, v) = prefill_inputs(s, hq, hkv, d, dev)
+    o = torch.empty((s, hq, d), dtype=torch.bfloat16, device=dev)
+    ms = time_steps(lambda i: attn.flash_attention_v1_bf16(q, k, v, o, hq, hkv, d, s, stream),
+                    steps, warmup, stream)
+    tflops = causal_flops(s, hq, d) / (ms * 1e-3) / 1e12
+    return ms, tflops, host, to_host(o)
+
+
+def bench_prefill_fused(dev, stream, steps, warmup, s=8192, hq=32, hkv=8, d=128):
+    import torch
+
+    from toyinfer_amd import attn, synth
+
+    _, (q, k, v) = prefill_inputs(s, hq, hkv, d, dev, seed=SEED + 4)
+    gq = to_dev(synth.uniform_bf16(SEED + 4, "gamma_q", (d,), 0.9, 1.1), dev)
+    gk = to_dev(synth.uniform_bf16(SEED + 4, "gamma_k", (d,), 0.9, 1.1), dev)
+    f = torch.empty(d // 2, dtype=torch.float32, device=dev)
+    attn.precompute_freq_f32(f, d, 1e6, stream)
+    o = torch.empty((s, hq, d), dtype=torch.bfloat16, device=dev)
+    k_out = torch.empty_like(k)
+    ms = time_steps(lambda i: attn.prefill_qknorm_rope_attention_bf16(
+        q, k, v, o, k_out, gq, gk, f, 1e-6, hq, hkv, d, s, stream), steps, warmup, stream)
+    tflops = causal_flops(s, hq, d) / (ms * 1e-3) / 1e12
+    return {"workload": "prefill_fused_qknorm_rope_s8192_hq32_hkv8_d128",
+            "entry": "toyinfer_prefill_qknorm_rope_attention_bf16", "steps": steps,
+            "ms_per_step": round(ms, 5), "value": round(tflops, 2), "unit": "TFLOP/s",
+            "note": "time includes the K norm+RoPE pre-pass; FLOPs count attention only",
+            "roofline": roofline("mfma", tflops, PEAK_BF16_TFLOPS, "TFLOP/s")}
+
+
+# ------------------------------------------------------------------- decode
+
+def bench_decode(dev, stream, steps, warmup, b, L, hq=32, hkv=8, d=128, sets=4):
+    import torch
+
+    from toyinfer_amd import attn, synth
+
+    kv = []
+    for r in range(sets):
+        kb = synth.normal_bf16(SEED + 10 + r, "k", (b, L, hkv, d))
+        vb = synth.normal_bf16(SEED + 10 + r, "v", (b, L, hkv, d))
+        kv.append((to_dev(kb, dev), to_dev(vb, dev)))
+    q = to_dev(synth.normal_bf16(SEED + 10, "q", (b, hq, d)), dev)
+    o = torch.empty((b, hq, d), dtype=torch.bfloat16, device=dev)
+    splits = attn.decode_default_splits(b, hq, hkv, d, L)
+    ws = torch.empty(attn.decode_workspace_bytes(b, hq, d, splits), dtype=torch.uint8,
+                     device=dev)
+
+    def step(i):
+        kc, vc = kv[i % sets]
+        attn.decode_attention_bf16(q, kc, vc, o, b, hq, hkv, d, None, L, L * hkv * d, splits, ws,
+                                   stream)
+
+    ms = time_steps(step, steps, warmup, stream)
+    kv_bytes = 2.0 * b * L * hkv * d * 2
+    gbs = kv_bytes / (ms * 1e-3) / 1e9
+    return {"workload": f"decode_b{b}_l{L}_hq{hq}_hkv{hkv}_d{d}",
+            "entry": "toyinfer_decode_attention_bf16", "splits": splits, "steps": steps,
+            "ms_per_step": round(ms, 5), "value": round(gbs, 1), "unit": "GB/s",
+            "note": "KV bytes read per step / step time (split + combine kernels); "
+                    f"{sets} rotating KV sets defeat the Infinity Cache",
+            "roofline": roofline("hbm", gbs, PEAK_HBM_GBS, "GB/s")}
+
+
+# ------------------------------------------------------------- CPU baseline
+
+def cpu_baseline(host_inputs, gpu_out, budget_s, s=1371, hq=16, d=128):
+    """Oracle on this host's cores over the full headline workload, repeated
+    until ~budget_s of CPU time; its output also checks the GPU output."""
+    import numpy as np
+
+    import oracle
+
+    threads = len(os.sched_getaffinity(0))
+    qb, kb, vb = host_inputs
+    t0 = time.perf_counter()
+    ref = oracle.flash_reference(qb, kb, vb, nthreads=threads)
+    reps, elapsed = 1, time.perf_counter() - t0
+    while elapsed < budget_s and reps < 64:
+        oracle.flash_reference(qb, kb, vb, nthreads=threads)
+        reps += 1
+        elapsed = time.perf_counter() - t0
+    tflops = causal_flops(s, hq, d) * reps / elapsed / 1e12
+    exp = oracle.round_bf16(ref)
+    got = (gpu_out.astype(np.uint32) << 16).view(np.float32)
+    diff = np.abs(got - exp)
+    return {"value": round(tflops, 6), "unit": "TFLOP/s", "cores": threads, "kind": "port",
+            "sample": f"full headline workload (S={s}, {hq}/8 heads, D={d}) x {reps} runs "
+                      f"of the oracle (fp64 scores/softmax, fp32 P.V), {elapsed:.1f} s, "
+                      f"{threads} OpenMP threads",
+            "parity_vs_gpu": {"max_abs": float(diff.max()), "mean_abs": float(diff.mean())}}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU only: bench.py --gpus 1 "
+                                   "(sharding across GPUs is described in DESIGN.md, not run)"}))
+        sys.exit(2)
+    import torch
+
+    from toyinfer_amd import attn  # noqa: F401  (fails loudly if the HIP library is missing)
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    stream = torch.cuda.Stream(device=dev)
+
+    ms, tflops, host_inputs, gpu_out = bench_prefill(dev, stream, args.steps, args.warmup)
+    line = {
+        "metric": METRIC, "value": round(tflops, 2), "unit": "TFLOP/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 5),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic: bf16 N(0,1) from seed 2026 (SplitMix64 + Box-Muller)",
+        "config": {"workload": "prefill_causal_gqa_s1371_hq16_hkv8_d128", "batch": 1,
+                   "seq_len": 1371, "num_q_heads": 16, "num_kv_heads": 8, "head_dim": 128,
+                   "flops_per_step": causal_flops(1371, 16, 128), "accumulate": "fp32",
+                   "parallelism": "single GPU"},
+        "roofline": roofline("mfma", tflops, PEAK_BF16_TFLOPS, "TFLOP/s"),
+    }
+    if not args.no_components:
+        comps = [bench_prefill_fused(dev, stream, max(10, args.steps // 4), 3)]
+        comps.append(bench_decode(dev, stream, max(50, args.steps * 2), 10, b=8, L=4096))
+        comps.append(bench_decode(dev, stream, max(50, args.steps * 2), 10, b=1, L=32768))
+        line["components"] = comps
+    if not args.no_cpu:
+        line["cpu_baseline"] = cpu_baseline(host_inputs, gpu_out, args.cpu_seconds)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

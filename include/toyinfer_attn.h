@@ -1,0 +1,144 @@
+/*
+ * C ABI of the MI355X (gfx950) attention path for ToyInfer.
+ *
+ * Plain pointers, sizes and an opaque stream (a hipStream_t, NULL = the
+ * legacy default stream, as in the reference).  Every entry point validates
+ * its arguments on the host before touching the GPU and returns a status
+ * code; none of them allocates, frees or synchronises, so all are safe to
+ * enqueue while a stream is being captured into a HIP graph.  bf16 tensors
+ * are 2-byte IEEE bfloat16 values (layout of __nv_bfloat16 / __hip_bfloat16).
+ *
+ * Citations name the reference launcher each function replaces
+ * (paths are into the wiketool/ToyInfer tree).
+ */
+#ifndef TOYINFER_ATTN_H_
+#define TOYINFER_ATTN_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define TOYINFER_ABI_VERSION 1u
+
+/* Status codes. */
+#define TOYINFER_OK 0
+#define TOYINFER_ERR_INVALID_ARGUMENT 1 /* shape, pointer or alignment precondition failed */
+#define TOYINFER_ERR_UNSUPPORTED 2      /* valid in principle, not implemented (e.g. head_dim) */
+#define TOYINFER_ERR_WORKSPACE 3        /* caller workspace too small */
+#define TOYINFER_ERR_HIP 4              /* a HIP call failed; see toyinfer_last_hip_error() */
+
+const char* toyinfer_status_string(int status);
+/* hipError_t of the most recent TOYINFER_ERR_HIP returned on this thread. */
+int toyinfer_last_hip_error(void);
+uint32_t toyinfer_abi_version(void);
+
+/* ---------------------------------------------------------------- prefill */
+
+/* Causal GQA prefill attention.  Replaces toyinfer::flash_attention_v1_bf16
+ * <Bc, Br, HEAD_DIM> (include/kernel_warpper.h:128-135; src/prefill.cu:381-395).
+ * Qs [S][Hq][D], Ks/Vs [S][Hkv][D], Os [S][Hq][D], bf16, token-major,
+ * positions 0..S-1.  D in {64, 128}; Hq % Hkv == 0; S >= 1.
+ * Pointers 16-byte aligned.  Writes Os[0..S) only. */
+int toyinfer_flash_attention_v1_bf16(const void* Qs, const void* Ks, const void* Vs, void* Os,
+                                     uint32_t num_q_heads, uint32_t num_kv_heads,
+                                     uint32_t heads_dim, uint32_t seq_len, void* stream);
+
+/* Prefill with Qwen3's pre-attention ops fused in front: per-head RMSNorm of
+ * Q and K (eps, gamma [D]) -> bf16 -> RoPE at position = token index with
+ * inv_freq [D/2] -> bf16, then causal GQA attention.  Equivalent to
+ * batch_multi_rmsnorm_bf16 + batch_rope_bf16 on Q and K followed by
+ * flash_attention_v1_bf16, as src/transformer.cpp:380-404 sequences them.
+ * Q_raw is read only (normalised and rotated on load); the normalised and
+ * rotated K is written to K_out [S][Hkv][D] (may alias K_raw; typically the
+ * layer's KV-cache slot), then used as the attention's K. */
+int toyinfer_prefill_qknorm_rope_attention_bf16(
+    const void* Q_raw, const void* K_raw, const void* Vs, void* Os, void* K_out,
+    const void* q_gamma, const void* k_gamma, const float* inv_freq, float rms_norm_eps,
+    uint32_t num_q_heads, uint32_t num_kv_heads, uint32_t heads_dim, uint32_t seq_len,
+    void* stream);
+
+/* ----------------------------------------------------------------- decode */
+
+/* Single-token decode attention over one sequence's KV cache, reference
+ * contract.  Replaces toyinfer::attention_bf16<NUM_THREADS, TILE_SEQ>
+ * (include/kernel_warpper.h:98-105; src/decode.cu:665-701).
+ * Q [Hq][D]; Ks/Vs [max_seq_len][Hkv][D] (rows 0..pos used); D in {64, 128}.
+ * Outputs as the reference leaves them: score [Hq][max_seq_len] = softmax
+ * probabilities for t <= pos and 0 for t > pos; O_buffer [Hq][D] = fp32
+ * output; O [Hq][D] = bf16(O_buffer).  score and O_buffer also serve as the
+ * split-K workspace, so no other memory is used. */
+int toyinfer_attention_bf16(const void* Q, const void* Ks, const void* Vs, float* score,
+                            float* O_buffer, void* O, uint32_t num_q_heads,
+                            uint32_t num_kv_heads, uint32_t heads_dim, uint32_t pos,
+                            uint32_t max_seq_len, void* stream);
+
+/* Same, with pos read on the device from *pos_d when the kernels run, so the
+ * call can be captured once into a graph and replayed for every position.
+ * Replaces toyinfer::attention_bf16_graph<NUM_THREADS, TILE_SEQ>
+ * (include/kernel_warpper.h:107-114; src/decode.cu:703-744).  A device pos
+ * >= max_seq_len is clamped to max_seq_len - 1. */
+int toyinfer_attention_bf16_graph(const void* Q, const void* Ks, const void* Vs, float* score,
+                                  float* O_buffer, void* O, uint32_t num_q_heads,
+                                  uint32_t num_kv_heads, uint32_t heads_dim,
+                                  const uint32_t* pos_d, uint32_t max_seq_len, void* stream);
+
+/* Batched split-K decode attention (extension; the reference runs one
+ * sequence per attention_bf16 call).  Only O is produced.
+ * q [B][Hq][D]; sequence b's cache rows at k_cache/v_cache + b*kv_batch_stride
+ * elements, row t of KV head h at + (t*Hkv + h)*D; o [B][Hq][D].
+ * Lengths: seq_lens_d (device, [B], each in 1..seq_len) or, if NULL, every
+ * sequence has length seq_len.  num_splits = 0 picks a default; the
+ * workspace must hold toyinfer_decode_workspace_bytes(B, Hq, D, splits)
+ * bytes (256-byte aligned) for the split count used. */
+int toyinfer_decode_attention_bf16(const void* q, const void* k_cache, const void* v_cache,
+                                   void* o, uint32_t batch, uint32_t num_q_heads,
+                                   uint32_t num_kv_heads, uint32_t heads_dim,
+                                   const uint32_t* seq_lens_d, uint32_t seq_len,
+                                   uint64_t kv_batch_stride, uint32_t num_splits,
+                                   void* workspace, size_t workspace_bytes, void* stream);
+/* Split count num_splits = 0 resolves to for these shapes. */
+uint32_t toyinfer_decode_default_splits(uint32_t batch, uint32_t num_q_heads,
+                                        uint32_t num_kv_heads, uint32_t heads_dim,
+                                        uint32_t seq_len);
+size_t toyinfer_decode_workspace_bytes(uint32_t batch, uint32_t num_q_heads, uint32_t heads_dim,
+                                       uint32_t num_splits);
+
+/* --------------------------------------------- Qwen3 pre-attention ops */
+
+/* inv_freq[i] = 1 / powf(theta, 2i/D), i < D/2.  Replaces
+ * toyinfer::precompute_freq_f32 (include/kernel_warpper.h:23; src/decode.cu:35-50). */
+int toyinfer_precompute_freq_f32(float* inv_freq, int head_dim, float theta, void* stream);
+
+/* Per-head RMSNorm, y = bf16(x / sqrt(mean(x^2) + eps) * w), rows of D.
+ * input may equal output.  Replaces toyinfer::multi_rmsnorm_bf16
+ * (include/kernel_warpper.h:39-42; src/decode.cu:144-199). */
+int toyinfer_multi_rmsnorm_bf16(const void* input, const void* weight, void* output,
+                                float rms_norm_eps, uint32_t nums_head, uint32_t head_dim,
+                                void* stream);
+/* Replaces toyinfer::batch_multi_rmsnorm_bf16 (include/kernel_warpper.h:45-50;
+ * src/prefill.cu:114-122): the same over num_tokens * nums_head rows. */
+int toyinfer_batch_multi_rmsnorm_bf16(const void* input, const void* weight, void* output,
+                                      float rms_norm_eps, uint32_t num_tokens,
+                                      uint32_t nums_head, uint32_t head_dim, void* stream);
+
+/* Rotate-half RoPE in place, angle = token * inv_freq[i] for token
+ * 0..num_tokens-1, pairs (i, i + D/2), outputs rounded to bf16.  Replaces
+ * toyinfer::batch_rope_bf16 (include/kernel_warpper.h:88-90; src/prefill.cu:185-218). */
+int toyinfer_batch_rope_bf16(void* qk, const float* inv_freq, uint32_t num_tokens,
+                             uint32_t nums_head, uint32_t head_dim, void* stream);
+
+/* Fused per-head RMSNorm -> bf16 -> RoPE(position = token) -> bf16 in one
+ * pass (extension: batch_multi_rmsnorm_bf16 then batch_rope_bf16 in one
+ * kernel).  input may equal output. */
+int toyinfer_qk_norm_rope_bf16(const void* input, const void* weight, void* output,
+                               const float* inv_freq, float rms_norm_eps, uint32_t num_tokens,
+                               uint32_t nums_head, uint32_t head_dim, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TOYINFER_ATTN_H_ */

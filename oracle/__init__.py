@@ -1,0 +1,279 @@
+"""Python view of the CPU oracle (``oracle/attn_oracle.c``).
+
+TEST INFRASTRUCTURE ONLY: the checker for the HIP attention path.  Only
+``tests/``, ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of
+``bench.py`` may import this module.  Nothing under ``toyinfer_amd/`` uses it.
+
+Every function restates one host reference of the reference's tests; the
+C file's header lists them with file:line citations, and
+``tests/test_oracle.py`` pins each against fixtures, closed forms and
+invariants.  Arrays are numpy: bf16 tensors travel as ``uint16`` bit
+patterns, everything else as ``float32``.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from typing import Optional, Sequence
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "liboracle.so")
+
+_f32p = np.ctypeslib.ndpointer(dtype=np.float32, flags="C_CONTIGUOUS")
+_u16p = np.ctypeslib.ndpointer(dtype=np.uint16, flags="C_CONTIGUOUS")
+_u32 = ctypes.c_uint32
+_f32 = ctypes.c_float
+_vp = ctypes.c_void_p
+
+
+def build() -> None:
+    """Compile liboracle.so with the committed Makefile."""
+    import subprocess
+
+    subprocess.run(["make", "-s", "-C", _HERE, "-B", "liboracle.so"], check=True)
+
+
+def _load() -> ctypes.CDLL:
+    if not os.path.exists(_LIB_PATH):
+        raise RuntimeError(
+            f"{_LIB_PATH} is missing: build it with `make -C oracle` "
+            "(or __graft_entry__.build())")
+    lib = ctypes.CDLL(_LIB_PATH)
+    sig = {
+        "or_f32_to_bf16_array": (None, [_f32p, _u16p, ctypes.c_int64]),
+        "or_bf16_to_f32_array": (None, [_u16p, _f32p, ctypes.c_int64]),
+        "or_make_flash_case": (None, [_u32, _u32, _u32, _u32, _f32, _f32, _f32, _f32, _f32,
+                                      _f32p, _f32p, _f32p]),
+        "or_make_causal_focus_case": (None, [_f32p, _f32p, _f32p]),
+        "or_make_attention_case": (None, [_u32, _u32, _u32, _u32, _f32, _f32,
+                                          _f32p, _f32p, _f32p]),
+        "or_make_rmsnorm_case": (None, [_u32, _u32, _u32, _f32, _f32, _f32p, _f32p]),
+        "or_make_batch_rmsnorm_case": (None, [_u32, _u32, _u32, _f32, _f32, _f32p, _f32p]),
+        "or_make_rope_case": (None, [_u32, _u32, _u32, _f32, _f32, _f32p, _f32p]),
+        "or_flash_reference_f32": (None, [_f32p, _f32p, _f32p, _f32p, _u32, _u32, _u32, _u32,
+                                          _vp, _u32, ctypes.c_int]),
+        "or_flash_reference_bf16": (None, [_u16p, _u16p, _u16p, _f32p, _u32, _u32, _u32, _u32,
+                                           _vp, _u32, ctypes.c_int]),
+        "or_decode_qk_scores": (None, [_f32p, _f32p, _f32p, _u32, _u32, _u32, _u32, _u32]),
+        "or_decode_softmax": (None, [_f32p, _u32, _u32, _u32]),
+        "or_decode_apply": (None, [_f32p, _f32p, _f32p, _u32, _u32, _u32, _u32, _u32]),
+        "or_decode_attention_f32": (None, [_f32p, _f32p, _f32p, _f32p, _f32p, _vp, _u32, _u32,
+                                           _u32, _u32, _u32]),
+        "or_decode_batched_bf16": (None, [_u16p, _u16p, _u16p, _f32p, _u32, _u32, _u32, _u32,
+                                          _vp, ctypes.c_int64, ctypes.c_int]),
+        "or_multi_rmsnorm": (None, [_f32p, _f32p, _f32p, _u32, _u32, _f32]),
+        "or_rope": (None, [_f32p, _f32p, _u32, _u32, _u32, _u32]),
+        "or_inv_freq": (None, [_f32p, ctypes.c_int, _f32]),
+        "or_qk_norm_rope": (None, [_f32p, _f32p, _f32p, _u32, _u32, _u32, _f32]),
+    }
+    for name, (res, args) in sig.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    return lib
+
+
+_lib: Optional[ctypes.CDLL] = None
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        _lib = _load()
+    return _lib
+
+
+def _c32(a) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+# ------------------------------------------------------------------ bf16
+
+def f32_to_bf16(x) -> np.ndarray:
+    """float32 -> bf16 bit patterns (RNE, quiet NaN)."""
+    x = _c32(x)
+    out = np.empty(x.shape, np.uint16)
+    lib().or_f32_to_bf16_array(x.reshape(-1), out.reshape(-1), x.size)
+    return out
+
+
+def bf16_to_f32(h) -> np.ndarray:
+    h = np.ascontiguousarray(h, dtype=np.uint16)
+    out = np.empty(h.shape, np.float32)
+    lib().or_bf16_to_f32_array(h.reshape(-1), out.reshape(-1), h.size)
+    return out
+
+
+def round_bf16(x) -> np.ndarray:
+    return bf16_to_f32(f32_to_bf16(x))
+
+
+# ------------------------------------------------------- case generators
+
+def make_flash_case(hq, hkv, d, s, q_phase, kv_phase, q_scale=1.0, k_scale=1.0, v_scale=1.0):
+    """tests/flash_attention_test_common.h:25-85 -> float (q, k, v)."""
+    q = np.empty((s, hq, d), np.float32)
+    k = np.empty((s, hkv, d), np.float32)
+    v = np.empty((s, hkv, d), np.float32)
+    lib().or_make_flash_case(hq, hkv, d, s, q_phase, kv_phase, q_scale, k_scale, v_scale,
+                             q.reshape(-1), k.reshape(-1), v.reshape(-1))
+    return q, k, v
+
+
+def make_causal_focus_case():
+    """tests/test_flash_attention_v1_bf16.cu:11-45 -> (q, k, v), Hq2 Hkv1 D64 S6."""
+    q = np.empty((6, 2, 64), np.float32)
+    k = np.empty((6, 1, 64), np.float32)
+    v = np.empty((6, 1, 64), np.float32)
+    lib().or_make_causal_focus_case(q.reshape(-1), k.reshape(-1), v.reshape(-1))
+    return q, k, v
+
+
+def make_attention_case(hq, hkv, d, max_seq_len, q_phase, kv_phase):
+    """tests/attention_test_common.h:40-85 -> float (q [Hq][D], k, v [MSL][Hkv][D])."""
+    q = np.empty((hq, d), np.float32)
+    k = np.empty((max_seq_len, hkv, d), np.float32)
+    v = np.empty((max_seq_len, hkv, d), np.float32)
+    lib().or_make_attention_case(hq, hkv, d, max_seq_len, q_phase, kv_phase,
+                                 q.reshape(-1), k.reshape(-1), v.reshape(-1))
+    return q, k, v
+
+
+def make_rmsnorm_case(num_heads, d, buffer_size, input_phase, weight_phase):
+    x = np.empty(buffer_size, np.float32)
+    w = np.empty(d, np.float32)
+    lib().or_make_rmsnorm_case(num_heads, d, buffer_size, input_phase, weight_phase, x, w)
+    return x, w
+
+
+def make_batch_rmsnorm_case(batch, num_heads, d, input_phase, weight_phase):
+    x = np.empty((batch, num_heads, d), np.float32)
+    w = np.empty(d, np.float32)
+    lib().or_make_batch_rmsnorm_case(batch, num_heads, d, input_phase, weight_phase,
+                                     x.reshape(-1), w)
+    return x, w
+
+
+def make_rope_case(num_heads, d, buffer_size, qk_phase, freq_scale):
+    qk = np.empty(buffer_size, np.float32)
+    f = np.empty(d // 2, np.float32)
+    lib().or_make_rope_case(num_heads, d, buffer_size, qk_phase, freq_scale, qk, f)
+    return qk, f
+
+
+# ----------------------------------------------------------- references
+
+def _rows_arg(rows):
+    if rows is None:
+        return None, 0, None
+    r = np.ascontiguousarray(rows, dtype=np.uint32)
+    return r.ctypes.data_as(_vp), r.size, r
+
+
+def flash_reference(q, k, v, rows: Optional[Sequence[int]] = None, nthreads: int = 0):
+    """Causal GQA prefill reference (flash_attention_test_common.h:87-136).
+
+    q [S][Hq][D], k/v [S][Hkv][D]: uint16 bf16 bits or float32 (already
+    bf16-valued).  Returns float32 [S][Hq][D] before the final bf16 rounding;
+    rows not in ``rows`` are NaN.
+    """
+    s, hq, d = q.shape
+    hkv = k.shape[1]
+    out = np.full((s, hq, d), np.nan, np.float32)
+    rp, nr, keep = _rows_arg(rows)
+    if q.dtype == np.uint16:
+        lib().or_flash_reference_bf16(np.ascontiguousarray(q).reshape(-1),
+                                      np.ascontiguousarray(k).reshape(-1),
+                                      np.ascontiguousarray(v).reshape(-1), out.reshape(-1),
+                                      hq, hkv, d, s, rp, nr, nthreads)
+    else:
+        lib().or_flash_reference_f32(_c32(q).reshape(-1), _c32(k).reshape(-1),
+                                     _c32(v).reshape(-1), out.reshape(-1),
+                                     hq, hkv, d, s, rp, nr, nthreads)
+    del keep
+    return out
+
+
+def decode_qk_scores(q, k, init_score, pos, max_seq_len):
+    hq, d = q.shape
+    hkv = k.shape[1]
+    sc = _c32(init_score).copy().reshape(-1)
+    lib().or_decode_qk_scores(_c32(q).reshape(-1), _c32(k).reshape(-1), sc, hq, hkv, d, pos,
+                              max_seq_len)
+    return sc.reshape(hq, max_seq_len)
+
+
+def decode_softmax(score, pos):
+    hq, msl = score.shape
+    sc = _c32(score).copy()
+    lib().or_decode_softmax(sc.reshape(-1), hq, pos, msl)
+    return sc
+
+
+def decode_apply(score, v, init_o, pos):
+    hq, msl = score.shape
+    hkv, d = v.shape[1], v.shape[2]
+    o = _c32(init_o).copy()
+    lib().or_decode_apply(_c32(score).reshape(-1), _c32(v).reshape(-1), o.reshape(-1), hq, hkv,
+                          d, pos, msl)
+    return o
+
+
+def decode_attention(q, k, v, pos, max_seq_len):
+    """Single-sequence decode reference -> (score [Hq][MSL], o_buffer [Hq][D] f32,
+    o [Hq][D] bf16 bits).  q/k/v float32, already bf16-valued."""
+    hq, d = q.shape
+    hkv = k.shape[1]
+    score = np.empty((hq, max_seq_len), np.float32)
+    ob = np.empty((hq, d), np.float32)
+    o = np.empty((hq, d), np.uint16)
+    lib().or_decode_attention_f32(_c32(q).reshape(-1), _c32(k).reshape(-1), _c32(v).reshape(-1),
+                                  score.reshape(-1), ob.reshape(-1),
+                                  o.ctypes.data_as(_vp), hq, hkv, d, pos, max_seq_len)
+    return score, ob, o
+
+
+def decode_batched(q, k, v, lens, nthreads: int = 0):
+    """Batched decode on bf16 bits: q [B][Hq][D], k/v [B][Lcap][Hkv][D]
+    -> o_buffer float32 [B][Hq][D]."""
+    b, hq, d = q.shape
+    hkv = k.shape[2]
+    stride = k.shape[1] * hkv * d
+    lens_a = np.ascontiguousarray(lens, dtype=np.uint32)
+    out = np.empty((b, hq, d), np.float32)
+    lib().or_decode_batched_bf16(np.ascontiguousarray(q).reshape(-1),
+                                 np.ascontiguousarray(k).reshape(-1),
+                                 np.ascontiguousarray(v).reshape(-1), out.reshape(-1),
+                                 b, hq, hkv, d, lens_a.ctypes.data_as(_vp), stride, nthreads)
+    return out
+
+
+def multi_rmsnorm(x, w, d, eps):
+    """Per-head RMSNorm of x (float, rows of D) -> float holding bf16 values."""
+    x = _c32(x)
+    out = np.empty_like(x)
+    rows = x.size // d
+    lib().or_multi_rmsnorm(x.reshape(-1), _c32(w), out.reshape(-1), rows, d, eps)
+    return out
+
+
+def rope(qk, inv_freq, num_tokens, num_heads, d, pos0=0):
+    out = _c32(qk).copy()
+    lib().or_rope(out.reshape(-1), _c32(inv_freq), num_tokens, num_heads, d, pos0)
+    return out
+
+
+def inv_freq(d, theta):
+    out = np.empty(d // 2, np.float32)
+    lib().or_inv_freq(out, d, theta)
+    return out
+
+
+def qk_norm_rope(x, gamma, inv_freq_arr, eps):
+    """x float [T][H][D] -> norm -> bf16 -> RoPE(pos = token) -> bf16."""
+    t, h, d = x.shape
+    out = _c32(x).copy()
+    lib().or_qk_norm_rope(out.reshape(-1), _c32(gamma), _c32(inv_freq_arr), t, h, d, eps)
+    return out

@@ -1,0 +1,136 @@
+"""Prefill parity: the HIP kernel through the C ABI vs the CPU oracle.
+
+Cases follow tests/test_flash_attention_v1_bf16.cu:108-131 (deterministic
+sin/cos inputs, its tolerances), then seeded N(0,1) inputs at the benchmark
+shapes, ragged lengths, every GQA ratio the reference exercises, and
+invariants that hold at any size.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from tests import helpers as H
+from toyinfer_amd import attn, synth
+
+pytestmark = pytest.mark.gpu
+
+
+def run_prefill(q_bits, k_bits, v_bits, dev):
+    s, hq, d = q_bits.shape
+    hkv = k_bits.shape[1]
+    q = H.to_dev_bf16(q_bits, dev)
+    k = H.to_dev_bf16(k_bits, dev)
+    v = H.to_dev_bf16(v_bits, dev)
+    o = torch.full((s, hq, d), -3.0, dtype=torch.bfloat16, device=dev)
+    attn.flash_attention_v1_bf16(q, k, v, o, hq, hkv, d, s)
+    H.sync()
+    return H.from_dev_bf16(o)
+
+
+# tests/test_flash_attention_v1_bf16.cu:113-131: (label, Hq, Hkv, D, S,
+# q_phase, kv_phase, scales, atol=rtol)
+REF_CASES = [
+    ("seq1 gqa", 2, 1, 64, 1, 0.07, 0.03, (1.0, 1.0, 1.0), 7e-2),
+    ("exact-kv-tile", 4, 4, 64, 32, 0.05, 0.021, (1.0, 1.0, 1.0), 7e-2),
+    ("gqa tail-tiles", 8, 2, 128, 37, 0.033, 0.017, (1.0, 1.0, 1.0), 7e-2),
+    ("multi-kv-tile", 6, 3, 128, 65, 0.028, 0.019, (1.0, 1.0, 1.0), 7e-2),
+    ("large-magnitude", 4, 2, 64, 19, 0.061, 0.027, (12.0, 10.0, 1.7), 1.2),
+]
+
+
+@pytest.mark.parametrize("case", REF_CASES, ids=[c[0] for c in REF_CASES])
+def test_reference_cases(dev, case):
+    label, hq, hkv, d, s, qp, kvp, (qs, ks_, vs), tol = case
+    print(f"[prefill] reference case {label}", flush=True)
+    q, k, v = oracle.make_flash_case(hq, hkv, d, s, qp, kvp, qs, ks_, vs)
+    qb, kb, vb = oracle.f32_to_bf16(q), oracle.f32_to_bf16(k), oracle.f32_to_bf16(v)
+    exp = oracle.round_bf16(oracle.flash_reference(qb, kb, vb))
+    got = H.bf16_bits_to_f32(run_prefill(qb, kb, vb, dev))
+    H.check_close(got, exp, tol, tol, label)
+    H.check_bar(got, exp, label)
+
+
+def test_causal_focus_case(dev):
+    """tests/test_flash_attention_v1_bf16.cu:11-45, tolerance 9e-2."""
+    q, k, v = oracle.make_causal_focus_case()
+    qb, kb, vb = oracle.f32_to_bf16(q), oracle.f32_to_bf16(k), oracle.f32_to_bf16(v)
+    exp = oracle.round_bf16(oracle.flash_reference(qb, kb, vb))
+    got = H.bf16_bits_to_f32(run_prefill(qb, kb, vb, dev))
+    H.check_close(got, exp, 9e-2, 9e-2, "causal-focus")
+    H.check_bar(got, exp, "causal-focus")
+
+
+def seeded(seed, s, hq, hkv, d):
+    return (synth.normal_bf16(seed, "q", (s, hq, d)), synth.normal_bf16(seed, "k", (s, hkv, d)),
+            synth.normal_bf16(seed, "v", (s, hkv, d)))
+
+
+@pytest.mark.parametrize("d", [64, 128])
+@pytest.mark.parametrize("hq,hkv", [(2, 1), (4, 4), (6, 3), (8, 2), (6, 2)])
+@pytest.mark.parametrize("s", [1, 2, 31, 63, 64, 65, 127, 129, 200])
+def test_ragged_shapes(dev, s, hq, hkv, d):
+    print(f"[prefill] ragged S={s} Hq={hq} Hkv={hkv} D={d}", flush=True)
+    qb, kb, vb = seeded(11 + s, s, hq, hkv, d)
+    exp = oracle.round_bf16(oracle.flash_reference(qb, kb, vb))
+    got = H.bf16_bits_to_f32(run_prefill(qb, kb, vb, dev))
+    H.check_bar(got, exp, f"S={s} {hq}/{hkv} D={d}")
+
+
+def test_config1_seeded(dev):
+    """Config 1 shape (S=128, 16/8, D=128), seeded N(0,1), vs oracle."""
+    qb, kb, vb = seeded(1, 128, 16, 8, 128)
+    exp = oracle.round_bf16(oracle.flash_reference(qb, kb, vb))
+    got = H.bf16_bits_to_f32(run_prefill(qb, kb, vb, dev))
+    H.check_bar(got, exp, "config1")
+
+
+def test_config2_full(dev):
+    """Config 2 (S=1371, 16/8, D=128): every output element vs the oracle."""
+    print("[prefill] config2 S=1371", flush=True)
+    qb, kb, vb = seeded(2, 1371, 16, 8, 128)
+    exp = oracle.round_bf16(oracle.flash_reference(qb, kb, vb))
+    got = H.bf16_bits_to_f32(run_prefill(qb, kb, vb, dev))
+    mx, mn = H.check_bar(got, exp, "config2")
+    print(f"[prefill] config2 max-abs {mx:.3g} mean-abs {mn:.3g}", flush=True)
+
+
+def test_deterministic(dev):
+    qb, kb, vb = seeded(5, 700, 8, 2, 128)
+    a = run_prefill(qb, kb, vb, dev)
+    b = run_prefill(qb, kb, vb, dev)
+    assert np.array_equal(a, b)
+
+
+def test_gqa_equals_mha_with_repeated_kv(dev):
+    """GQA output == MHA output on K/V heads repeated G times (bitwise)."""
+    qb, kb, vb = seeded(6, 300, 8, 2, 128)
+    gqa = run_prefill(qb, kb, vb, dev)
+    mha = run_prefill(qb, np.repeat(kb, 4, axis=1), np.repeat(vb, 4, axis=1), dev)
+    assert np.array_equal(gqa, mha)
+
+
+def test_row0_is_v_row0(dev):
+    """Causal row 0 attends only to key 0: O[0] == V[0] exactly."""
+    qb, kb, vb = seeded(7, 96, 4, 2, 64)
+    got = run_prefill(qb, kb, vb, dev)
+    assert np.array_equal(got[0], np.repeat(vb[0], 2, axis=0))
+
+
+def test_prefix_independence(dev):
+    """Causality: rows < S' of a length-S run equal a length-S' run."""
+    qb, kb, vb = seeded(8, 400, 8, 2, 128)
+    full = run_prefill(qb, kb, vb, dev)
+    part = run_prefill(qb[:257].copy(), kb[:257].copy(), vb[:257].copy(), dev)
+    assert np.array_equal(full[:257], part)
+
+
+def test_rejects_bad_arguments(dev):
+    q = torch.zeros((4, 4, 128), dtype=torch.bfloat16, device=dev)
+    k = torch.zeros((4, 3, 128), dtype=torch.bfloat16, device=dev)
+    with pytest.raises(attn.ToyInferError) as e:
+        attn.flash_attention_v1_bf16(q, k, k, q, 4, 3, 128, 4)
+    assert e.value.status == attn.ERR_INVALID_ARGUMENT
+    with pytest.raises(attn.ToyInferError) as e:
+        attn.flash_attention_v1_bf16(q, k, k, q, 4, 4, 96, 4)
+    assert e.value.status == attn.ERR_UNSUPPORTED

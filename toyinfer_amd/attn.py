@@ -1,0 +1,212 @@
+"""Python host side of the MI355X attention path, over the C ABI.
+
+Mirrors the reference's launch-wrapper API (include/kernel_warpper.h) with
+the same names, argument meaning and order; device buffers are torch tensors
+on a ROCm device (PyTorch is only the allocator and stream provider here).
+Every call goes through ``toyinfer_amd/lib/libtoyinfer_attn.so``; there is no
+CPU fallback: if the library is missing, loading this module fails loudly.
+
+Errors: the C ABI returns a status; a non-zero status raises
+``ToyInferError`` (the reference instead prints and calls exit(EXIT_FAILURE),
+src/kernel_common.cuh:11-20; the C++ drop-in header keeps that behaviour).
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from typing import Optional
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "lib", "libtoyinfer_attn.so")
+
+OK = 0
+ERR_INVALID_ARGUMENT = 1
+ERR_UNSUPPORTED = 2
+ERR_WORKSPACE = 3
+ERR_HIP = 4
+
+# Every entry point of include/toyinfer_attn.h, with its ctypes signature.
+_vp, _u32, _u64, _f32, _i32, _sz = (ctypes.c_void_p, ctypes.c_uint32, ctypes.c_uint64,
+                                    ctypes.c_float, ctypes.c_int, ctypes.c_size_t)
+SIGNATURES = {
+    "toyinfer_status_string": (ctypes.c_char_p, [_i32]),
+    "toyinfer_last_hip_error": (_i32, []),
+    "toyinfer_abi_version": (_u32, []),
+    "toyinfer_flash_attention_v1_bf16": (_i32, [_vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _vp]),
+    "toyinfer_prefill_qknorm_rope_attention_bf16": (
+        _i32, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _f32, _u32, _u32, _u32, _u32, _vp]),
+    "toyinfer_attention_bf16": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32,
+                                       _u32, _vp]),
+    "toyinfer_attention_bf16_graph": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32, _vp,
+                                             _u32, _vp]),
+    "toyinfer_decode_attention_bf16": (_i32, [_vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _vp,
+                                              _u32, _u64, _u32, _vp, _sz, _vp]),
+    "toyinfer_decode_default_splits": (_u32, [_u32, _u32, _u32, _u32, _u32]),
+    "toyinfer_decode_workspace_bytes": (_sz, [_u32, _u32, _u32, _u32]),
+    "toyinfer_precompute_freq_f32": (_i32, [_vp, _i32, _f32, _vp]),
+    "toyinfer_multi_rmsnorm_bf16": (_i32, [_vp, _vp, _vp, _f32, _u32, _u32, _vp]),
+    "toyinfer_batch_multi_rmsnorm_bf16": (_i32, [_vp, _vp, _vp, _f32, _u32, _u32, _u32, _vp]),
+    "toyinfer_batch_rope_bf16": (_i32, [_vp, _vp, _u32, _u32, _u32, _vp]),
+    "toyinfer_qk_norm_rope_bf16": (_i32, [_vp, _vp, _vp, _vp, _f32, _u32, _u32, _u32, _vp]),
+}
+
+
+class ToyInferError(RuntimeError):
+    def __init__(self, fn: str, status: int, hip_error: int = 0):
+        self.status = status
+        self.hip_error = hip_error
+        msg = f"{fn}: {status_string(status)} (status {status})"
+        if status == ERR_HIP:
+            msg += f", hipError {hip_error}"
+        super().__init__(msg)
+
+
+def _load() -> ctypes.CDLL:
+    if not os.path.exists(LIB_PATH):
+        raise ImportError(
+            f"{LIB_PATH} not found: build the HIP library first "
+            "(python -m toyinfer_amd.build, or __graft_entry__.build())")
+    lib = ctypes.CDLL(LIB_PATH)
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    return lib
+
+
+LIB = _load()
+
+
+def status_string(status: int) -> str:
+    return LIB.toyinfer_status_string(status).decode()
+
+
+def _check(fn: str, status: int) -> None:
+    if status != OK:
+        raise ToyInferError(fn, status, LIB.toyinfer_last_hip_error() if status == ERR_HIP else 0)
+
+
+# ------------------------------------------------------------ tensor glue
+
+def _ptr(t) -> Optional[int]:
+    """Device address of a torch tensor (None passes a null pointer)."""
+    if t is None:
+        return None
+    return int(t.data_ptr())
+
+
+def _stream(stream) -> Optional[int]:
+    """hipStream_t handle: an int, a torch.cuda.Stream, or None for torch's
+    current stream on the current device."""
+    if isinstance(stream, int):
+        return stream
+    import torch
+
+    if stream is None:
+        stream = torch.cuda.current_stream()
+    return int(stream.cuda_stream)
+
+
+# ---------------------------------------------------------------- prefill
+
+def flash_attention_v1_bf16(Qs, Ks, Vs, Os, num_q_heads: int, num_kv_heads: int, heads_dim: int,
+                            seq_len: int, stream=None) -> None:
+    """Causal GQA prefill (include/kernel_warpper.h:128-135).
+    Qs [S][Hq][D], Ks/Vs [S][Hkv][D], Os [S][Hq][D]: bf16 device tensors."""
+    _check("flash_attention_v1_bf16",
+           LIB.toyinfer_flash_attention_v1_bf16(_ptr(Qs), _ptr(Ks), _ptr(Vs), _ptr(Os),
+                                                num_q_heads, num_kv_heads, heads_dim, seq_len,
+                                                _stream(stream)))
+
+
+def prefill_qknorm_rope_attention_bf16(Q_raw, K_raw, Vs, Os, K_out, q_gamma, k_gamma, inv_freq,
+                                       rms_norm_eps: float, num_q_heads: int, num_kv_heads: int,
+                                       heads_dim: int, seq_len: int, stream=None) -> None:
+    """QK-RMSNorm + RoPE fused in front of causal GQA prefill."""
+    _check("prefill_qknorm_rope_attention_bf16",
+           LIB.toyinfer_prefill_qknorm_rope_attention_bf16(
+               _ptr(Q_raw), _ptr(K_raw), _ptr(Vs), _ptr(Os), _ptr(K_out), _ptr(q_gamma),
+               _ptr(k_gamma), _ptr(inv_freq), rms_norm_eps, num_q_heads, num_kv_heads, heads_dim,
+               seq_len, _stream(stream)))
+
+
+# ----------------------------------------------------------------- decode
+
+def attention_bf16(Q, Ks, Vs, score, O_buffer, O, num_q_heads: int, num_kv_heads: int,
+                   heads_dim: int, pos: int, max_seq_len: int, stream=None) -> None:
+    """Single-sequence decode, reference contract (include/kernel_warpper.h:98-105)."""
+    _check("attention_bf16",
+           LIB.toyinfer_attention_bf16(_ptr(Q), _ptr(Ks), _ptr(Vs), _ptr(score), _ptr(O_buffer),
+                                       _ptr(O), num_q_heads, num_kv_heads, heads_dim, pos,
+                                       max_seq_len, _stream(stream)))
+
+
+def attention_bf16_graph(Q, Ks, Vs, score, O_buffer, O, num_q_heads: int, num_kv_heads: int,
+                         heads_dim: int, pos_d, max_seq_len: int, stream=None) -> None:
+    """Decode with pos read on the device (include/kernel_warpper.h:107-114)."""
+    _check("attention_bf16_graph",
+           LIB.toyinfer_attention_bf16_graph(_ptr(Q), _ptr(Ks), _ptr(Vs), _ptr(score),
+                                             _ptr(O_buffer), _ptr(O), num_q_heads, num_kv_heads,
+                                             heads_dim, _ptr(pos_d), max_seq_len,
+                                             _stream(stream)))
+
+
+def decode_default_splits(batch: int, num_q_heads: int, num_kv_heads: int, heads_dim: int,
+                          seq_len: int) -> int:
+    return int(LIB.toyinfer_decode_default_splits(batch, num_q_heads, num_kv_heads, heads_dim,
+                                                  seq_len))
+
+
+def decode_workspace_bytes(batch: int, num_q_heads: int, heads_dim: int, num_splits: int) -> int:
+    return int(LIB.toyinfer_decode_workspace_bytes(batch, num_q_heads, heads_dim, num_splits))
+
+
+def decode_attention_bf16(q, k_cache, v_cache, o, batch: int, num_q_heads: int,
+                          num_kv_heads: int, heads_dim: int, seq_lens_d, seq_len: int,
+                          kv_batch_stride: int, num_splits: int, workspace,
+                          stream=None) -> None:
+    """Batched split-K decode; workspace is a device tensor (any dtype)."""
+    ws_bytes = workspace.numel() * workspace.element_size()
+    _check("decode_attention_bf16",
+           LIB.toyinfer_decode_attention_bf16(_ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(o), batch,
+                                              num_q_heads, num_kv_heads, heads_dim,
+                                              _ptr(seq_lens_d), seq_len, kv_batch_stride,
+                                              num_splits, _ptr(workspace), ws_bytes,
+                                              _stream(stream)))
+
+
+# ------------------------------------------------------------ prologue ops
+
+def precompute_freq_f32(inv_freq, head_dim: int, theta: float, stream=None) -> None:
+    _check("precompute_freq_f32",
+           LIB.toyinfer_precompute_freq_f32(_ptr(inv_freq), head_dim, theta, _stream(stream)))
+
+
+def multi_rmsnorm_bf16(input, weight, output, rms_norm_eps: float, nums_head: int,
+                       head_dim: int, stream=None) -> None:
+    _check("multi_rmsnorm_bf16",
+           LIB.toyinfer_multi_rmsnorm_bf16(_ptr(input), _ptr(weight), _ptr(output), rms_norm_eps,
+                                           nums_head, head_dim, _stream(stream)))
+
+
+def batch_multi_rmsnorm_bf16(input, weight, output, rms_norm_eps: float, num_tokens: int,
+                             nums_head: int, head_dim: int, stream=None) -> None:
+    _check("batch_multi_rmsnorm_bf16",
+           LIB.toyinfer_batch_multi_rmsnorm_bf16(_ptr(input), _ptr(weight), _ptr(output),
+                                                 rms_norm_eps, num_tokens, nums_head, head_dim,
+                                                 _stream(stream)))
+
+
+def batch_rope_bf16(qk, inv_freq, num_tokens: int, nums_head: int, head_dim: int,
+                    stream=None) -> None:
+    _check("batch_rope_bf16",
+           LIB.toyinfer_batch_rope_bf16(_ptr(qk), _ptr(inv_freq), num_tokens, nums_head, head_dim,
+                                        _stream(stream)))
+
+
+def qk_norm_rope_bf16(input, weight, output, inv_freq, rms_norm_eps: float, num_tokens: int,
+                      nums_head: int, head_dim: int, stream=None) -> None:
+    _check("qk_norm_rope_bf16",
+           LIB.toyinfer_qk_norm_rope_bf16(_ptr(input), _ptr(weight), _ptr(output), _ptr(inv_freq),
+                                          rms_norm_eps, num_tokens, nums_head, head_dim,
+                                          _stream(stream)))

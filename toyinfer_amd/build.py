@@ -1,0 +1,81 @@
+"""Build the gfx950 attention library in-tree.
+
+``python -m toyinfer_amd.build`` (or ``__graft_entry__.build()``) compiles
+every HIP source under ``toyinfer_amd/csrc`` with hipcc into
+``toyinfer_amd/lib/libtoyinfer_attn.so``.  Packed-FP32 VALU forms are
+disabled on purpose: some of their encodings have produced silently wrong
+results on the target machines, and the kernels do not depend on them.
+"""
+from __future__ import annotations
+
+import glob
+import os
+import shutil
+import subprocess
+import sys
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(HERE)
+CSRC = os.path.join(HERE, "csrc")
+LIB_DIR = os.path.join(HERE, "lib")
+LIB_PATH = os.path.join(LIB_DIR, "libtoyinfer_attn.so")
+SYNTH_PATH = os.path.join(LIB_DIR, "libtoyinfer_synth.so")
+ARCH = "gfx950"
+
+HIP_FLAGS = [
+    f"--offload-arch={ARCH}",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    "-Wall",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-I", os.path.join(ROOT, "include"),
+]
+
+
+def hipcc() -> str:
+    path = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+    if not os.path.exists(path):
+        raise RuntimeError("hipcc not found: the ROCm toolchain is required to build")
+    return path
+
+
+def sources() -> list:
+    return sorted(glob.glob(os.path.join(CSRC, "*.hip")))
+
+
+def build_synth(verbose: bool = False) -> str:
+    """Host-only synthetic-input generator (same bits as synth.py's numpy code)."""
+    os.makedirs(LIB_DIR, exist_ok=True)
+    tmp = SYNTH_PATH + ".tmp"
+    cmd = ["gcc", "-O3", "-march=x86-64-v3", "-ffp-contract=off", "-fno-fast-math", "-fopenmp",
+           "-fPIC", "-shared", "-std=c11", "-Wall", "-o", tmp,
+           os.path.join(CSRC, "synth.c"), "-lm"]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    subprocess.run(cmd, check=True)
+    os.replace(tmp, SYNTH_PATH)
+    return SYNTH_PATH
+
+
+def build_library(verbose: bool = False) -> str:
+    os.makedirs(LIB_DIR, exist_ok=True)
+    tmp = LIB_PATH + ".tmp"
+    cmd = [hipcc(), *HIP_FLAGS, "-shared", "-o", tmp, *sources()]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        sys.stderr.write(res.stdout + res.stderr)
+        raise RuntimeError("hipcc failed building libtoyinfer_attn.so")
+    os.replace(tmp, LIB_PATH)
+    return LIB_PATH
+
+
+def build_all(verbose: bool = False) -> None:
+    build_library(verbose)
+    build_synth(verbose)
+
+
+if __name__ == "__main__":
+    build_all(verbose=True)

@@ -1,0 +1,331 @@
+// C ABI of the attention path (declared in include/toyinfer_attn.h).
+//
+// Every entry point checks its arguments on the host and returns a status
+// before any HIP call, so argument errors are testable without a GPU.  The
+// entry points only enqueue kernels: no allocation, no memset node, no
+// synchronisation, which keeps them legal inside stream capture.
+#include <stdint.h>
+
+#include "../../include/toyinfer_attn.h"
+#include "kernels.hpp"
+
+using namespace tiattn;
+
+namespace {
+
+thread_local int g_last_hip_error = 0;
+
+int from_hip(hipError_t e) {
+    if (e == hipSuccess) return TOYINFER_OK;
+    g_last_hip_error = (int)e;
+    return TOYINFER_ERR_HIP;
+}
+
+bool aligned(const void* p, uintptr_t a) { return ((uintptr_t)p & (a - 1)) == 0; }
+
+// Shared shape checks.  head_dim outside {64, 128} is "unsupported" rather
+// than "invalid": the reference instantiates exactly these two
+// (src/prefill.cu:433-452, src/transformer.cpp:26-38).
+int check_heads(uint32_t hq, uint32_t hkv, uint32_t d) {
+    if (hq == 0 || hkv == 0 || hq % hkv != 0) return TOYINFER_ERR_INVALID_ARGUMENT;
+    if (hq > 65535u) return TOYINFER_ERR_INVALID_ARGUMENT;
+    if (d != 64 && d != 128) return TOYINFER_ERR_UNSUPPORTED;
+    return TOYINFER_OK;
+}
+
+hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
+
+// Where the reference-contract decode keeps its split partials: in score
+// rows when they are long enough (mode B), else in O_buffer/O rows with a
+// single split (mode A).  Either way each head's partials live only in that
+// head's rows, which the finaliser reads before it overwrites them.
+void compat_partials(uint32_t hq, uint32_t hkv, uint32_t d, uint32_t sizing_len, uint32_t msl,
+                     float* score, float* o_buffer, void* o, uint32_t* splits,
+                     DecodePartials* part) {
+    uint32_t s = decode_default_splits(1, hq, hkv, d, sizing_len);
+    const uint32_t cap = msl / (d + 2);
+    if (s >= 2 && cap >= 2) {
+        if (s > cap) s = cap;
+        *splits = s;
+        part->ml = score;
+        part->ml_head = msl;
+        part->o = score + 2 * (size_t)s;
+        part->o_head = msl;
+        part->o_split = d;
+        return;
+    }
+    *splits = 1;
+    part->ml = reinterpret_cast<float*>(o);  // 8 bytes at the head of O row h (D*2 bytes)
+    part->ml_head = d / 2;
+    part->o = o_buffer;
+    part->o_head = d;
+    part->o_split = d;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* toyinfer_status_string(int status) {
+    switch (status) {
+        case TOYINFER_OK: return "ok";
+        case TOYINFER_ERR_INVALID_ARGUMENT: return "invalid argument";
+        case TOYINFER_ERR_UNSUPPORTED: return "unsupported configuration";
+        case TOYINFER_ERR_WORKSPACE: return "workspace too small";
+        case TOYINFER_ERR_HIP: return "HIP error";
+        default: return "unknown status";
+    }
+}
+
+int toyinfer_last_hip_error(void) { return g_last_hip_error; }
+
+uint32_t toyinfer_abi_version(void) { return TOYINFER_ABI_VERSION; }
+
+// ------------------------------------------------------------------ prefill
+
+int toyinfer_flash_attention_v1_bf16(const void* Qs, const void* Ks, const void* Vs, void* Os,
+                                     uint32_t num_q_heads, uint32_t num_kv_heads,
+                                     uint32_t heads_dim, uint32_t seq_len, void* stream) {
+    if (int st = check_heads(num_q_heads, num_kv_heads, heads_dim)) return st;
+    if (seq_len == 0) return TOYINFER_ERR_INVALID_ARGUMENT;
+    if (!Qs || !Ks || !Vs || !Os) return TOYINFER_ERR_INVALID_ARGUMENT;
+    if (!aligned(Qs, 16) || !aligned(Ks, 16) || !aligned(Vs, 16) || !aligned(Os, 16))
+        return TOYINFER_ERR_INVALID_ARGUMENT;
+    if ((uint64_t)((seq_len + 127) / 128) * num_q_heads > 0x7fffffffull)
+        return TOYINFER_ERR_INVALID_ARGUMENT;
+    PrefillProblem p{};
+    p.q = static_cast<const uint16_t*>(Qs);
+    p.k = static_cast<const uint16_t*>(Ks);
+    p.v = static_cast<const uint16_t*>(Vs);
+    p.o = static_cast<uint16_t*>(Os);
+    p.s = seq_len;
+    p.hq = num_q_heads;
+    p.hkv = num_kv_heads;
+    p.d = heads_dim;
+    p.fused_q = false;
+    return from_hip(launch_prefill(p, as_stream(stream)));
+}
+
+int toyinfer_prefill_qknorm_rope_attention_bf16(
+    const void* Q_raw, const void* K_raw, const void* Vs, void* Os, void* K_out,
+    const void* q_gamma, const void* k_gamma, const float* inv_freq, float rms_norm_eps,
+    uint32_t num_q_heads, uint32_t num_kv_heads, uint32_t heads_dim, uint32_t seq_len,
+    void* stream) {
+    if (int st = check_heads(num_q_heads, num_kv_heads, heads_dim)) return st;
+    if (seq_len == 0) return TOYINFER_ERR_INVALID_ARGUMENT;
+    if (!Q_raw || !K_raw || !Vs || !Os || !K_out || !q_gamma || !k_gamma || !inv_freq)
+        return TOYINFER_ERR_INVALID_ARGUMENT;
+    if (!aligned(Q_raw, 16) || !aligned(Vs, 16) || !aligned(Os, 16) || !aligned(K_out, 16) ||
+        !aligned(q_gamma, 16) || !aligned(K_raw, 2) || !aligned(k_gamma, 2) ||
+        !aligned(inv_freq, 4))
+        return TOYINFER_ERR_INVALID_ARGUMENT;
+    if ((uint64_t)((seq_len + 127) / 128) * num_q_heads > 0x7fffffffull)
+        return TOYINFER_ERR_INVALID_ARGUMENT;
+    hipStream_t st = as_stream(stream);
+    hipError_t e = launch_row_norm_rope(static_cast<const uint16_t*>(K_raw),
+                                        static_cast<uint16_t*>(K_out),
+                                        static_cast<const uint16_t*>(k_gamma), inv_freq,
+                                        rms_norm_eps, seq_len, num_kv_heads, heads_dim,
+                                        kRowNorm | kRowRope, st);
+    if (e != hipSuccess) return from_hip(e);
+    PrefillProblem p{};
+    p.q = static_cast<const uint16_t*>(Q_raw);
+    p.k = static_cast<const uint16_t*>(K_out);
+    p.v = static_cast<const uint16_t*>(Vs);
+    p.o = static_cast<uint16_t*>(Os);
+    p.s = seq_len;
+    p.hq = num_q_heads;
+    p.hkv = num_kv_heads;
+    p.d = heads_dim;
+    p.fused_q = true;
+    p.q_gamma = static_cast<const uint16_t*>(q_gamma);
+    p.inv_freq = inv_freq;
+    p.eps = rms_norm_eps;
+    return from_hip(launch_prefill(p, st));
+}
+
+// ------------------------------------------------------------------- decode
+
+static int decode_common_checks(const void* Q, const void* Ks, const void* Vs, float* score,
+                                float* O_buffer, void* O, uint32_t hq, uint32_t hkv, uint32_t d,
+                                uint32_t msl) {
+    if (int st = check_heads(hq, hkv, d)) return st;
+    if (msl == 0) return TOYINFER_ERR_INVALID_ARGUMENT;
+    if (!Q || !Ks || !Vs || !score || !O_buffer || !O) return TOYINFER_ERR_INVALID_ARGUMENT;
+    if (!aligned(Q, 16) || !aligned(Ks, 16) || !aligned(Vs, 16) || !aligned(O, 8) ||
+        !aligned(score, 4) || !aligned(O_buffer, 4))
+        return TOYINFER_ERR_INVALID_ARGUMENT;
+    return TOYINFER_OK;
+}
+
+static int decode_compat(const void* Q, const void* Ks, const void* Vs, float* score,
+                         float* O_buffer, void* O, uint32_t hq, uint32_t hkv, uint32_t d,
+                         int len_mode, const uint32_t* pos_d, uint32_t pos, uint32_t msl,
+                         void* stream) {
+    DecodeProblem p{};
+    p.q = static_cast<const uint16_t*>(Q);
+    p.k = static_cast<const uint16_t*>(Ks);
+    p.v = static_cast<const uint16_t*>(Vs);
+    p.kv_stride = 0;
+    p.batch = 1;
+    p.hq = hq;
+    p.hkv = hkv;
+    p.d = d;
+    p.len_mode = len_mode;
+    p.len_dev = pos_d;
+    p.len_host = pos + 1;
+    p.len_cap = msl;
+    DecodePartials part{};
+    const uint32_t sizing = len_mode == kLenHost ? pos + 1 : msl;
+    compat_partials(hq, hkv, d, sizing, msl, score, O_buffer, O, &p.splits, &part);
+    hipStream_t st = as_stream(stream);
+    hipError_t e = launch_decode_split(p, part, st);
+    if (e != hipSuccess) return from_hip(e);
+    return from_hip(launch_decode_finalize_compat(p, part, score, msl, O_buffer,
+                                                  static_cast<uint16_t*>(O), st));
+}
+
+int toyinfer_attention_bf16(const void* Q, const void* Ks, const void* Vs, float* score,
+                            float* O_buffer, void* O, uint32_t num_q_heads,
+                            uint32_t num_kv_heads, uint32_t heads_dim, uint32_t pos,
+                            uint32_t max_seq_len, void* stream) {
+    if (int st = decode_common_checks(Q, Ks, Vs, score, O_buffer, O, num_q_heads, num_kv_heads,
+                                      heads_dim, max_seq_len))
+        return st;
+    if (pos >= max_seq_len) return TOYINFER_ERR_INVALID_ARGUMENT;
+    return decode_compat(Q, Ks, Vs, score, O_buffer, O, num_q_heads, num_kv_heads, heads_dim,
+                         kLenHost, nullptr, pos, max_seq_len, stream);
+}
+
+int toyinfer_attention_bf16_graph(const void* Q, const void* Ks, const void* Vs, float* score,
+                                  float* O_buffer, void* O, uint32_t num_q_heads,
+                                  uint32_t num_kv_heads, uint32_t heads_dim,
+                                  const uint32_t* pos_d, uint32_t max_seq_len, void* stream) {
+    if (int st = decode_common_checks(Q, Ks, Vs, score, O_buffer, O, num_q_heads, num_kv_heads,
+                                      heads_dim, max_seq_len))
+        return st;
+    if (!pos_d || !aligned(pos_d, 4)) return TOYINFER_ERR_INVALID_ARGUMENT;
+    return decode_compat(Q, Ks, Vs, score, O_buffer, O, num_q_heads, num_kv_heads, heads_dim,
+                         kLenDevicePos, pos_d, 0, max_seq_len, stream);
+}
+
+uint32_t toyinfer_decode_default_splits(uint32_t batch, uint32_t num_q_heads,
+                                        uint32_t num_kv_heads, uint32_t heads_dim,
+                                        uint32_t seq_len) {
+    if (batch == 0 || num_kv_heads == 0 || num_q_heads % num_kv_heads != 0 || seq_len == 0)
+        return 1;
+    return decode_default_splits(batch, num_q_heads, num_kv_heads, heads_dim, seq_len);
+}
+
+size_t toyinfer_decode_workspace_bytes(uint32_t batch, uint32_t num_q_heads, uint32_t heads_dim,
+                                       uint32_t num_splits) {
+    const size_t heads = (size_t)batch * num_q_heads;
+    return align_up(heads * num_splits * 2 * sizeof(float), 256) +
+           heads * num_splits * heads_dim * sizeof(float);
+}
+
+int toyinfer_decode_attention_bf16(const void* q, const void* k_cache, const void* v_cache,
+                                   void* o, uint32_t batch, uint32_t num_q_heads,
+                                   uint32_t num_kv_heads, uint32_t heads_dim,
+                                   const uint32_t* seq_lens_d, uint32_t seq_len,
+                                   uint64_t kv_batch_stride, uint32_t num_splits,
+                                   void* workspace, size_t workspace_bytes, void* stream) {
+    if (int st = check_heads(num_q_heads, num_kv_heads, heads_dim)) return st;
+    if (batch == 0 || batch > 65535u || seq_len == 0) return TOYINFER_ERR_INVALID_ARGUMENT;
+    if (!q || !k_cache || !v_cache || !o || !workspace) return TOYINFER_ERR_INVALID_ARGUMENT;
+    if (!aligned(q, 16) || !aligned(k_cache, 16) || !aligned(v_cache, 16) || !aligned(o, 2) ||
+        !aligned(workspace, 256) || (seq_lens_d && !aligned(seq_lens_d, 4)))
+        return TOYINFER_ERR_INVALID_ARGUMENT;
+    if (batch > 1 && kv_batch_stride < (uint64_t)seq_len * num_kv_heads * heads_dim)
+        return TOYINFER_ERR_INVALID_ARGUMENT;
+    if (kv_batch_stride % 8 != 0) return TOYINFER_ERR_INVALID_ARGUMENT;
+    const uint32_t splits =
+        num_splits ? num_splits
+                   : decode_default_splits(batch, num_q_heads, num_kv_heads, heads_dim, seq_len);
+    if (splits > 65535u) return TOYINFER_ERR_INVALID_ARGUMENT;
+    if (workspace_bytes < toyinfer_decode_workspace_bytes(batch, num_q_heads, heads_dim, splits))
+        return TOYINFER_ERR_WORKSPACE;
+    DecodeProblem p{};
+    p.q = static_cast<const uint16_t*>(q);
+    p.k = static_cast<const uint16_t*>(k_cache);
+    p.v = static_cast<const uint16_t*>(v_cache);
+    p.kv_stride = (int64_t)kv_batch_stride;
+    p.batch = batch;
+    p.hq = num_q_heads;
+    p.hkv = num_kv_heads;
+    p.d = heads_dim;
+    p.len_mode = seq_lens_d ? kLenDevice : kLenHost;
+    p.len_dev = seq_lens_d;
+    p.len_host = seq_len;
+    p.len_cap = seq_len;
+    p.splits = splits;
+    const size_t heads = (size_t)batch * num_q_heads;
+    DecodePartials part{};
+    part.ml = static_cast<float*>(workspace);
+    part.ml_head = 2 * (int64_t)splits;
+    part.o = reinterpret_cast<float*>(static_cast<char*>(workspace) +
+                                      align_up(heads * splits * 2 * sizeof(float), 256));
+    part.o_head = (int64_t)splits * heads_dim;
+    part.o_split = heads_dim;
+    hipStream_t st = as_stream(stream);
+    hipError_t e = launch_decode_split(p, part, st);
+    if (e != hipSuccess) return from_hip(e);
+    return from_hip(launch_decode_combine(p, part, static_cast<uint16_t*>(o), st));
+}
+
+// ------------------------------------------------------ prologue operators
+
+int toyinfer_precompute_freq_f32(float* inv_freq, int head_dim, float theta, void* stream) {
+    if (!inv_freq || head_dim < 2 || head_dim % 2 != 0) return TOYINFER_ERR_INVALID_ARGUMENT;
+    return from_hip(launch_precompute_freq(inv_freq, head_dim, theta, as_stream(stream)));
+}
+
+static int row_op(const void* input, const void* weight, void* output, const float* inv_freq,
+                  float eps, uint32_t num_tokens, uint32_t nums_head, uint32_t head_dim, int mode,
+                  void* stream) {
+    if (head_dim != 64 && head_dim != 128) return TOYINFER_ERR_UNSUPPORTED;
+    if (num_tokens == 0 || nums_head == 0) return TOYINFER_ERR_INVALID_ARGUMENT;
+    if ((uint64_t)num_tokens * nums_head > 0xffffffffull) return TOYINFER_ERR_INVALID_ARGUMENT;
+    if (!input || !output) return TOYINFER_ERR_INVALID_ARGUMENT;
+    if ((mode & kRowNorm) && !weight) return TOYINFER_ERR_INVALID_ARGUMENT;
+    if ((mode & kRowRope) && !inv_freq) return TOYINFER_ERR_INVALID_ARGUMENT;
+    if (!aligned(input, 2) || !aligned(output, 2) || (weight && !aligned(weight, 2)) ||
+        (inv_freq && !aligned(inv_freq, 4)))
+        return TOYINFER_ERR_INVALID_ARGUMENT;
+    return from_hip(launch_row_norm_rope(static_cast<const uint16_t*>(input),
+                                         static_cast<uint16_t*>(output),
+                                         static_cast<const uint16_t*>(weight), inv_freq, eps,
+                                         num_tokens, nums_head, head_dim, mode,
+                                         as_stream(stream)));
+}
+
+int toyinfer_multi_rmsnorm_bf16(const void* input, const void* weight, void* output,
+                                float rms_norm_eps, uint32_t nums_head, uint32_t head_dim,
+                                void* stream) {
+    return row_op(input, weight, output, nullptr, rms_norm_eps, 1, nums_head, head_dim, kRowNorm,
+                  stream);
+}
+
+int toyinfer_batch_multi_rmsnorm_bf16(const void* input, const void* weight, void* output,
+                                      float rms_norm_eps, uint32_t num_tokens,
+                                      uint32_t nums_head, uint32_t head_dim, void* stream) {
+    return row_op(input, weight, output, nullptr, rms_norm_eps, num_tokens, nums_head, head_dim,
+                  kRowNorm, stream);
+}
+
+int toyinfer_batch_rope_bf16(void* qk, const float* inv_freq, uint32_t num_tokens,
+                             uint32_t nums_head, uint32_t head_dim, void* stream) {
+    return row_op(qk, nullptr, qk, inv_freq, 0.0f, num_tokens, nums_head, head_dim, kRowRope,
+                  stream);
+}
+
+int toyinfer_qk_norm_rope_bf16(const void* input, const void* weight, void* output,
+                               const float* inv_freq, float rms_norm_eps, uint32_t num_tokens,
+                               uint32_t nums_head, uint32_t head_dim, void* stream) {
+    return row_op(input, weight, output, inv_freq, rms_norm_eps, num_tokens, nums_head, head_dim,
+                  kRowNorm | kRowRope, stream);
+}
+
+}  // extern "C"

@@ -1,0 +1,92 @@
+// Shared device helpers for the gfx950 (CDNA4) attention kernels.
+//
+// Wave64 throughout: cross-lane work uses DPP row operations (16-lane rows),
+// ds_bpermute only for the one lane^32 exchange per tile.  bf16 values move
+// as raw 16-bit patterns; bf16 -> f32 is a shift, f32 -> bf16 is the
+// hardware round-to-nearest-even v_cvt_pk_bf16_f32.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace tiattn {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+
+constexpr float kLog2e = 1.4426950408889634f;
+
+__device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+__device__ __forceinline__ float bf16_to_f32(uint16_t h) { return __uint_as_float(uint32_t(h) << 16); }
+
+// Two floats -> packed bf16x2 (lo = a), round to nearest even.
+__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
+    f32x2_t v = {a, b};
+    bf16x2_t r = __builtin_convertvector(v, bf16x2_t);
+    return __builtin_bit_cast(uint32_t, r);
+}
+__device__ __forceinline__ uint16_t f32_to_bf16(float a) {
+    return uint16_t(pack_bf16x2(a, 0.0f) & 0xffffu);
+}
+
+// DPP move within 16-lane rows (row_mask = bank_mask = 0xf).
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float x) {
+    return __builtin_bit_cast(
+        float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, 0xf, 0xf, false));
+}
+constexpr int kDppXor1 = 0xB1;          // quad_perm [1,0,3,2]
+constexpr int kDppXor2 = 0x4E;          // quad_perm [2,3,0,1]
+constexpr int kDppRowHalfMirror = 0x141;  // lane i <-> 7-i within 8
+constexpr int kDppRowMirror = 0x140;      // lane i <-> 15-i within 16
+
+// Reductions over the 16 lanes of a DPP row; every lane of the row gets the result.
+__device__ __forceinline__ float row16_max(float x) {
+    x = fmaxf(x, dpp_f32<kDppXor1>(x));
+    x = fmaxf(x, dpp_f32<kDppXor2>(x));
+    x = fmaxf(x, dpp_f32<kDppRowHalfMirror>(x));
+    x = fmaxf(x, dpp_f32<kDppRowMirror>(x));
+    return x;
+}
+__device__ __forceinline__ float row16_sum(float x) {
+    x += dpp_f32<kDppXor1>(x);
+    x += dpp_f32<kDppXor2>(x);
+    x += dpp_f32<kDppRowHalfMirror>(x);
+    x += dpp_f32<kDppRowMirror>(x);
+    return x;
+}
+
+// Value held by lane (lane ^ 32).
+__device__ __forceinline__ float xor32(float x) {
+    const int lane = __lane_id();
+    return __builtin_bit_cast(
+        float, __builtin_amdgcn_ds_bpermute((lane ^ 32) << 2, __builtin_bit_cast(int, x)));
+}
+
+// Full wave64 sum (every lane gets the result).
+__device__ __forceinline__ float wave_sum(float x) {
+    x = row16_sum(x);
+    x += __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(((__lane_id() ^ 16) << 2),
+                                                                __builtin_bit_cast(int, x)));
+    x += xor32(x);
+    return x;
+}
+
+__device__ __forceinline__ uint4 ldg16(const void* p) {
+    return *reinterpret_cast<const uint4*>(p);
+}
+
+__device__ __forceinline__ bf16x8_t as_bf16x8(uint4 v) { return __builtin_bit_cast(bf16x8_t, v); }
+
+__device__ __forceinline__ f32x16_t mfma32x32x16(bf16x8_t a, bf16x8_t b, f32x16_t c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x4_t mfma16x16x32(bf16x8_t a, bf16x8_t b, f32x4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+}  // namespace tiattn

@@ -1,0 +1,83 @@
+// Host-side launch interface between the C ABI (capi.hip) and the kernels.
+// Launchers assume their arguments were validated by the caller.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace tiattn {
+
+// ------------------------------------------------------------------ decode
+//
+// Split-K decode writes one partial (m, l, o[D]) per (sequence, q-head,
+// split).  Where partials live is described by base pointers and strides so
+// the same kernels serve the batched workspace layout and the reference
+// contract's score/O_buffer/O buffers.
+struct DecodePartials {
+    float* ml;              // (m, l) pairs: ml + bh*ml_head + s*2
+    float* o;               // o[D]:        o + bh*o_head + s*o_split
+    int64_t ml_head;        // floats between consecutive (seq, q-head)
+    int64_t o_head;
+    int64_t o_split;
+};
+
+enum LenMode : int {
+    kLenHost = 0,        // every sequence has length len_host
+    kLenDevice = 1,      // lengths in len_dev[B]
+    kLenDevicePos = 2,   // one device position: length = *len_dev + 1 (clamped to len_cap)
+};
+
+struct DecodeProblem {
+    const uint16_t* q;   // [B][Hq][D]
+    const uint16_t* k;
+    const uint16_t* v;
+    int64_t kv_stride;   // elements between sequences
+    uint32_t batch, hq, hkv, d;
+    int len_mode;
+    const uint32_t* len_dev;
+    uint32_t len_host;   // kLenHost: the length; otherwise unused
+    uint32_t len_cap;    // upper bound for device lengths (grid sizing, clamping)
+    uint32_t splits;
+};
+
+// Split pass: grid (splits, Hkv * head groups, B).
+hipError_t launch_decode_split(const DecodeProblem& p, const DecodePartials& part,
+                               hipStream_t stream);
+// Combine partials into o [B][Hq][D] bf16.
+hipError_t launch_decode_combine(const DecodeProblem& p, const DecodePartials& part, uint16_t* o,
+                                 hipStream_t stream);
+// Reference-contract finaliser (B == 1): combine partials, write O_buffer
+// (fp32), O (bf16) and score [Hq][msl] (probabilities, zeros past pos).
+hipError_t launch_decode_finalize_compat(const DecodeProblem& p, const DecodePartials& part,
+                                         float* score, uint32_t msl, float* o_buffer,
+                                         uint16_t* o, hipStream_t stream);
+
+uint32_t decode_default_splits(uint32_t batch, uint32_t hq, uint32_t hkv, uint32_t d,
+                               uint32_t seq_len);
+// Workgroups per KV head: query heads are taken two at a time.
+uint32_t decode_head_groups(uint32_t group);
+
+// ----------------------------------------------------------------- prefill
+struct PrefillProblem {
+    const uint16_t* q;   // [S][Hq][D] (raw when fused_q)
+    const uint16_t* k;   // [S][Hkv][D] (already normalised/rotated when fused)
+    const uint16_t* v;
+    uint16_t* o;
+    uint32_t s, hq, hkv, d;
+    bool fused_q;
+    const uint16_t* q_gamma;  // [D] (fused_q)
+    const float* inv_freq;    // [D/2] (fused_q)
+    float eps;
+};
+hipError_t launch_prefill(const PrefillProblem& p, hipStream_t stream);
+
+// ------------------------------------------------------ prologue kernels
+hipError_t launch_precompute_freq(float* inv_freq, int d, float theta, hipStream_t stream);
+// mode bit 1: RMSNorm with weight; bit 2: RoPE at position = row / nums_head.
+enum RowOpMode : int { kRowNorm = 1, kRowRope = 2 };
+hipError_t launch_row_norm_rope(const uint16_t* in, uint16_t* out, const uint16_t* weight,
+                                const float* inv_freq, float eps, uint32_t num_tokens,
+                                uint32_t nums_head, uint32_t d, int mode, hipStream_t stream);
+
+}  // namespace tiattn

@@ -1,0 +1,349 @@
+// Causal GQA prefill attention for gfx950 (bf16 MFMA, fp32 online softmax).
+//
+// Replaces flash_attention_v1_bf16_kernel (src/prefill.cu:224-379), which
+// runs scalar fp32 dots out of LDS, re-reads every K/V tile per query head
+// and visits all ceil(S/32) tiles whatever the causal mask.  Here:
+//
+// * One workgroup = 4 waves = 128 query rows (32 per wave) of one q-head.
+//   Workgroups of the same KV head are launched on the same XCD (block id
+//   % Hkv picks the KV head, and the hardware deals block ids round-robin
+//   over the 8 XCDs), so a K/V tile fetched into one XCD's L2 serves every
+//   q-head of its group; the heaviest (last) query tiles are launched first.
+// * Per 64-key tile: S^T = K Q^T on v_mfma_f32_32x32x16_bf16 (A = K from
+//   LDS, B = Q^T held in registers for the whole kernel).  In the result
+//   lane (q = lane%32, half = lane/32) holds 32 keys of query q, so the row
+//   max and row sum are in-lane plus one lane^32 exchange.
+// * O^T += V^T P^T on the same MFMA: B = P^T is exactly the lane's own
+//   probabilities (converted to bf16 in place); A = V^T is read from a
+//   transposed V tile in LDS with two 8-byte reads per operand.  The output
+//   lane again owns one query row, so the running rescale is in-lane.
+// * The running max is only moved when it grows by more than 2^8 (the sum
+//   and output share the stale max, so the result is exact); fully masked
+//   tiles past the diagonal are never visited.
+// * K and V tiles are double-buffered in LDS: the next tile's global loads
+//   are in flight while the current tile computes.  K rows are stored with
+//   their 16-byte chunks XOR-swizzled by row; V^T rows are padded to 136 B.
+//
+// Optional fused prologue (Qwen3, src/transformer.cpp:380-391): Q rows are
+// RMS-normalised with gamma, rounded to bf16, rotated (RoPE at position =
+// token) and rounded again while they are loaded into registers.
+#include <math.h>
+
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace tiattn {
+namespace {
+
+constexpr int kPfThreads = 256;
+constexpr int kPfBM = 128;  // query rows per workgroup
+constexpr int kPfBN = 64;   // keys per tile
+constexpr float kRescaleThreshold = 8.0f;
+
+template <int D>
+struct PfShape {
+    static constexpr int CPR = D / 8;                       // 16-byte chunks per K row
+    static constexpr int VT_PITCH = kPfBN + 4;              // bf16 per V^T row (136 B)
+    static constexpr int K_ELEMS = kPfBN * D;
+    static constexpr int VT_ELEMS = D * VT_PITCH;
+    static constexpr int K_LOADS = kPfBN * D / 8 / kPfThreads;  // uint4 per thread
+    static constexpr int V_BLOCKS = (kPfBN / 4) * (D / 8);      // 4 keys x 8 dims blocks
+    static constexpr int KSTEPS = D / 16;                   // QK MFMA k-steps
+    static constexpr int DBLK = D / 32;                     // PV output d-blocks
+};
+
+template <int D>
+struct TileRegs {
+    uint4 k[PfShape<D>::K_LOADS];
+    uint4 v[4];
+};
+
+template <int D>
+__device__ __forceinline__ void load_tile(TileRegs<D>& r, const uint16_t* __restrict__ K,
+                                          const uint16_t* __restrict__ V, uint32_t n0, uint32_t S,
+                                          int64_t kv_row, uint32_t kvh) {
+    using P = PfShape<D>;
+    const int tid = threadIdx.x;
+#pragma unroll
+    for (int it = 0; it < P::K_LOADS; ++it) {
+        const int idx = tid + kPfThreads * it;
+        const int row = idx / P::CPR, c = idx % P::CPR;
+        const uint32_t key = n0 + row;
+        const uint32_t kc = key < S ? key : S - 1;
+        uint4 x = ldg16(K + (int64_t)kc * kv_row + (int64_t)kvh * D + c * 8);
+        if (key >= S) x = make_uint4(0, 0, 0, 0);
+        r.k[it] = x;
+    }
+    if (tid < P::V_BLOCKS) {
+        const int dgi = tid % (D / 8), kgi = tid / (D / 8);
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) {
+            const uint32_t key = n0 + 4 * kgi + rr;
+            const uint32_t kc = key < S ? key : S - 1;
+            uint4 x = ldg16(V + (int64_t)kc * kv_row + (int64_t)kvh * D + dgi * 8);
+            if (key >= S) x = make_uint4(0, 0, 0, 0);
+            r.v[rr] = x;
+        }
+    }
+}
+
+__device__ __forceinline__ uint32_t word_of(const uint4& v, int i) {
+    return i == 0 ? v.x : (i == 1 ? v.y : (i == 2 ? v.z : v.w));
+}
+
+template <int D>
+__device__ __forceinline__ void store_tile(const TileRegs<D>& r, uint16_t* sk, uint16_t* svt) {
+    using P = PfShape<D>;
+    const int tid = threadIdx.x;
+#pragma unroll
+    for (int it = 0; it < P::K_LOADS; ++it) {
+        const int idx = tid + kPfThreads * it;
+        const int row = idx / P::CPR, c = idx % P::CPR;
+        const int phys = c ^ (row & (P::CPR - 1));
+        *reinterpret_cast<uint4*>(sk + row * D + phys * 8) = r.k[it];
+    }
+    if (tid < P::V_BLOCKS) {
+        const int dgi = tid % (D / 8), kgi = tid / (D / 8);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const uint32_t w0 = word_of(r.v[0], j / 2), w1 = word_of(r.v[1], j / 2);
+            const uint32_t w2 = word_of(r.v[2], j / 2), w3 = word_of(r.v[3], j / 2);
+            uint2 out;
+            if ((j & 1) == 0) {
+                out.x = (w0 & 0xffffu) | (w1 << 16);
+                out.y = (w2 & 0xffffu) | (w3 << 16);
+            } else {
+                out.x = (w0 >> 16) | (w1 & 0xffff0000u);
+                out.y = (w2 >> 16) | (w3 & 0xffff0000u);
+            }
+            *reinterpret_cast<uint2*>(svt + (dgi * 8 + j) * P::VT_PITCH + 4 * kgi) = out;
+        }
+    }
+}
+
+// Q^T fragment of this lane: query row qq, dims {ks*16 + 8*kg + j}.  With
+// FUSED, applies RMSNorm(gamma) -> bf16 -> RoPE(position qq) -> bf16.
+template <int D, bool FUSED>
+__device__ __forceinline__ void load_q(bf16x8_t (&qf)[PfShape<D>::KSTEPS], const PrefillProblem& p,
+                                       uint32_t qq, uint32_t h, int kg) {
+    constexpr int KS = PfShape<D>::KSTEPS;
+    uint4 raw[KS];
+    const uint32_t qc = qq < p.s ? qq : p.s - 1;
+    const uint16_t* qrow = p.q + ((int64_t)qc * p.hq + h) * D + 8 * kg;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+        uint4 x = ldg16(qrow + ks * 16);
+        if (qq >= p.s) x = make_uint4(0, 0, 0, 0);
+        raw[ks] = x;
+    }
+    if constexpr (!FUSED) {
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) qf[ks] = as_bf16x8(raw[ks]);
+    } else {
+#pragma clang fp contract(off)
+        float ss = 0.0f;
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const uint32_t w = word_of(raw[ks], e);
+                const float a = bf16_lo(w), b = bf16_hi(w);
+                ss += a * a;
+                ss += b * b;
+            }
+        ss += xor32(ss);
+        const float inv = 1.0f / sqrtf(ss / (float)D + p.eps);
+        const float pos = (float)qq;
+        // Chunk ks (dims < D/2) pairs with chunk ks + KS/2 (dims + D/2).
+#pragma unroll
+        for (int ks = 0; ks < KS / 2; ++ks) {
+            const uint4 g_re = ldg16(p.q_gamma + ks * 16 + 8 * kg);
+            const uint4 g_im = ldg16(p.q_gamma + (ks + KS / 2) * 16 + 8 * kg);
+            uint32_t o_re[4], o_im[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const uint32_t xr = word_of(raw[ks], e), xi = word_of(raw[ks + KS / 2], e);
+                const uint32_t gr = word_of(g_re, e), gi = word_of(g_im, e);
+                float r2[2], i2[2];
+#pragma unroll
+                for (int hlf = 0; hlf < 2; ++hlf) {
+                    const float xre = hlf ? bf16_hi(xr) : bf16_lo(xr);
+                    const float xim = hlf ? bf16_hi(xi) : bf16_lo(xi);
+                    const float gre = hlf ? bf16_hi(gr) : bf16_lo(gr);
+                    const float gim = hlf ? bf16_hi(gi) : bf16_lo(gi);
+                    const float re = bf16_lo(pack_bf16x2(xre * inv * gre, 0.0f));
+                    const float im = bf16_lo(pack_bf16x2(xim * inv * gim, 0.0f));
+                    float sn, cs;
+                    sincosf(pos * p.inv_freq[ks * 16 + 8 * kg + 2 * e + hlf], &sn, &cs);
+                    r2[hlf] = cs * re - sn * im;
+                    i2[hlf] = cs * im + sn * re;
+                }
+                o_re[e] = pack_bf16x2(r2[0], r2[1]);
+                o_im[e] = pack_bf16x2(i2[0], i2[1]);
+            }
+            qf[ks] = as_bf16x8(make_uint4(o_re[0], o_re[1], o_re[2], o_re[3]));
+            qf[ks + KS / 2] = as_bf16x8(make_uint4(o_im[0], o_im[1], o_im[2], o_im[3]));
+        }
+    }
+}
+
+template <int D, bool FUSED>
+__global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(PrefillProblem p, float scale_log2) {
+    using P = PfShape<D>;
+    __shared__ __align__(16) uint16_t s_k[2][P::K_ELEMS];
+    __shared__ __align__(16) uint16_t s_vt[2][P::VT_ELEMS];
+
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int ql = lane & 31, kg = lane >> 5;
+    const uint32_t group = p.hq / p.hkv;
+    const uint32_t n_qtiles = (p.s + kPfBM - 1) / kPfBM;
+    const uint32_t bid = blockIdx.x;
+    const uint32_t kvh = bid % p.hkv;
+    const uint32_t r = bid / p.hkv;
+    const uint32_t h = kvh * group + r % group;
+    const uint32_t qt = n_qtiles - 1 - r / group;
+
+    const uint32_t q_end = min(p.s, (qt + 1) * kPfBM);
+    const uint32_t n_tiles = (q_end + kPfBN - 1) / kPfBN;
+    const uint32_t q0 = qt * kPfBM + wave * 32;
+    const uint32_t qq = q0 + ql;
+    const uint32_t wave_tiles = q0 < p.s ? (min(q0 + 31, p.s - 1) / kPfBN + 1) : 0;
+    const int64_t kv_row = (int64_t)p.hkv * D;
+
+    bf16x8_t qf[P::KSTEPS];
+    load_q<D, FUSED>(qf, p, qq, h, kg);
+
+    TileRegs<D> regs;
+    load_tile<D>(regs, p.k, p.v, 0, p.s, kv_row, kvh);
+
+    f32x16_t oacc[P::DBLK];
+#pragma unroll
+    for (int db = 0; db < P::DBLK; ++db)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) oacc[db][i] = 0.0f;
+    float m_run = -INFINITY, l_run = 0.0f;
+
+    store_tile<D>(regs, s_k[0], s_vt[0]);
+    __syncthreads();
+
+    for (uint32_t t = 0; t < n_tiles; ++t) {
+        const int buf = t & 1;
+        if (t + 1 < n_tiles) load_tile<D>(regs, p.k, p.v, (t + 1) * kPfBN, p.s, kv_row, kvh);
+
+        if (t < wave_tiles) {
+            const uint32_t n0 = t * kPfBN;
+            const uint16_t* kb = s_k[buf];
+            const uint16_t* vb = s_vt[buf];
+            f32x16_t st0, st1;
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                st0[i] = 0.0f;
+                st1[i] = 0.0f;
+            }
+            const int sw = ql & (P::CPR - 1);
+#pragma unroll
+            for (int ks = 0; ks < P::KSTEPS; ++ks) {
+                const int phys = (ks * 2 + kg) ^ sw;
+                const uint4 a0 = *reinterpret_cast<const uint4*>(kb + ql * D + phys * 8);
+                const uint4 a1 = *reinterpret_cast<const uint4*>(kb + (32 + ql) * D + phys * 8);
+                st0 = mfma32x32x16(as_bf16x8(a0), qf[ks], st0);
+                st1 = mfma32x32x16(as_bf16x8(a1), qf[ks], st1);
+            }
+            // Causal mask: lane holds keys n0 + 32*blk + 8*(i/4) + 4*kg + i%4.
+            if (n0 + kPfBN - 1 > q0) {
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    const uint32_t key = n0 + 8 * (i / 4) + 4 * kg + (i % 4);
+                    if (key > qq) st0[i] = -INFINITY;
+                    if (key + 32 > qq) st1[i] = -INFINITY;
+                }
+            }
+            float mx = fmaxf(st0[0], st1[0]);
+#pragma unroll
+            for (int i = 1; i < 16; ++i) mx = fmaxf(mx, fmaxf(st0[i], st1[i]));
+            mx = fmaxf(mx, xor32(mx));
+            const float mt = mx * scale_log2;
+            const bool need = mt > m_run + kRescaleThreshold;
+            if (__any(need)) {
+                float alpha = 1.0f;
+                if (need) {
+                    alpha = exp2f(m_run - mt);
+                    m_run = mt;
+                }
+                l_run *= alpha;
+#pragma unroll
+                for (int db = 0; db < P::DBLK; ++db)
+#pragma unroll
+                    for (int i = 0; i < 16; ++i) oacc[db][i] *= alpha;
+            }
+            const float mref = m_run == -INFINITY ? 0.0f : m_run;
+            float rs = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                st0[i] = exp2f(fmaf(st0[i], scale_log2, -mref));
+                st1[i] = exp2f(fmaf(st1[i], scale_log2, -mref));
+                rs += st0[i] + st1[i];
+            }
+            l_run += rs;
+            bf16x8_t pf[4];
+#pragma unroll
+            for (int tt = 0; tt < 4; ++tt) {
+                const f32x16_t& src = tt < 2 ? st0 : st1;
+                const int o8 = 8 * (tt & 1);
+                uint4 w;
+                w.x = pack_bf16x2(src[o8 + 0], src[o8 + 1]);
+                w.y = pack_bf16x2(src[o8 + 2], src[o8 + 3]);
+                w.z = pack_bf16x2(src[o8 + 4], src[o8 + 5]);
+                w.w = pack_bf16x2(src[o8 + 6], src[o8 + 7]);
+                pf[tt] = as_bf16x8(w);
+            }
+#pragma unroll
+            for (int db = 0; db < P::DBLK; ++db) {
+                const uint16_t* vrow = vb + (db * 32 + ql) * P::VT_PITCH + 4 * kg;
+#pragma unroll
+                for (int tt = 0; tt < 4; ++tt) {
+                    const uint2 x0 = *reinterpret_cast<const uint2*>(vrow + 16 * tt);
+                    const uint2 x1 = *reinterpret_cast<const uint2*>(vrow + 16 * tt + 8);
+                    const uint4 a = make_uint4(x0.x, x0.y, x1.x, x1.y);
+                    oacc[db] = mfma32x32x16(as_bf16x8(a), pf[tt], oacc[db]);
+                }
+            }
+        }
+
+        if (t + 1 < n_tiles) store_tile<D>(regs, s_k[buf ^ 1], s_vt[buf ^ 1]);
+        __syncthreads();
+    }
+
+    const float l_tot = l_run + xor32(l_run);  // all lanes take part in the exchange
+    if (qq < p.s) {
+        const float inv = 1.0f / l_tot;
+        uint16_t* orow = p.o + ((int64_t)qq * p.hq + h) * D;
+#pragma unroll
+        for (int db = 0; db < P::DBLK; ++db)
+#pragma unroll
+            for (int i4 = 0; i4 < 4; ++i4) {
+                uint2 w;
+                w.x = pack_bf16x2(oacc[db][4 * i4] * inv, oacc[db][4 * i4 + 1] * inv);
+                w.y = pack_bf16x2(oacc[db][4 * i4 + 2] * inv, oacc[db][4 * i4 + 3] * inv);
+                *reinterpret_cast<uint2*>(orow + db * 32 + 8 * i4 + 4 * kg) = w;
+            }
+    }
+}
+
+template <int D, bool FUSED>
+hipError_t launch_t(const PrefillProblem& p, hipStream_t st) {
+    const uint32_t n_qtiles = (p.s + kPfBM - 1) / kPfBM;
+    const dim3 grid(n_qtiles * p.hq);
+    const float sl2 = kLog2e / sqrtf((float)D);
+    hipLaunchKernelGGL((prefill_kernel<D, FUSED>), grid, dim3(kPfThreads), 0, st, p, sl2);
+    return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_prefill(const PrefillProblem& p, hipStream_t stream) {
+    if (p.d == 64) return p.fused_q ? launch_t<64, true>(p, stream) : launch_t<64, false>(p, stream);
+    return p.fused_q ? launch_t<128, true>(p, stream) : launch_t<128, false>(p, stream);
+}
+
+}  // namespace tiattn

@@ -90,9 +90,10 @@ int toyinfer_attention_bf16_graph(const void* Q, const void* Ks, const void* Vs,
  * q [B][Hq][D]; sequence b's cache rows at k_cache/v_cache + b*kv_batch_stride
  * elements, row t of KV head h at + (t*Hkv + h)*D; o [B][Hq][D].
  * Lengths: seq_lens_d (device, [B], each in 1..seq_len) or, if NULL, every
- * sequence has length seq_len.  num_splits = 0 picks a default; the
- * workspace must hold toyinfer_decode_workspace_bytes(B, Hq, D, splits)
- * bytes (256-byte aligned) for the split count used. */
+ * sequence has length seq_len.  num_splits = 0 picks a default (at most
+ * 1024 splits are accepted); the workspace must hold
+ * toyinfer_decode_workspace_bytes(B, Hq, D, splits) bytes (256-byte
+ * aligned) for the split count used. */
 int toyinfer_decode_attention_bf16(const void* q, const void* k_cache, const void* v_cache,
                                    void* o, uint32_t batch, uint32_t num_q_heads,
                                    uint32_t num_kv_heads, uint32_t heads_dim,

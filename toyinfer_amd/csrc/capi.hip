@@ -45,7 +45,8 @@ void compat_partials(uint32_t hq, uint32_t hkv, uint32_t d, uint32_t sizing_len,
                      float* score, float* o_buffer, void* o, uint32_t* splits,
                      DecodePartials* part) {
     uint32_t s = decode_default_splits(1, hq, hkv, d, sizing_len);
-    const uint32_t cap = msl / (d + 2);
+    uint32_t cap = msl / (d + 2);
+    if (cap > decode_max_splits()) cap = decode_max_splits();
     if (s >= 2 && cap >= 2) {
         if (s > cap) s = cap;
         *splits = s;
@@ -244,7 +245,7 @@ int toyinfer_decode_attention_bf16(const void* q, const void* k_cache, const voi
     const uint32_t splits =
         num_splits ? num_splits
                    : decode_default_splits(batch, num_q_heads, num_kv_heads, heads_dim, seq_len);
-    if (splits > 65535u) return TOYINFER_ERR_INVALID_ARGUMENT;
+    if (splits > decode_max_splits()) return TOYINFER_ERR_INVALID_ARGUMENT;
     if (workspace_bytes < toyinfer_decode_workspace_bytes(batch, num_q_heads, heads_dim, splits))
         return TOYINFER_ERR_WORKSPACE;
     DecodeProblem p{};

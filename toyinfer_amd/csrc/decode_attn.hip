@@ -3,24 +3,33 @@
 // Replaces the reference's three-kernel decode pipeline
 // (gqa_qk_gemv_bf16 -> softmax_f32 -> apply_score2v_f32 + convert,
 // src/decode.cu:399-744) with one streaming pass over the KV cache plus a
-// small combine.  Work unit: one workgroup = (sequence, KV head, group of up
-// to 4 query heads, slice of the cached positions).  Each K/V row is read
-// from HBM once and used by every query head of its GQA group.
+// small combine.  Work unit: one workgroup = (sequence, KV head, slice of
+// the cached positions) for all query heads of the GQA group (up to 16), so
+// each K/V row is read from HBM exactly once.
 //
-// Per 16-position tile a wave issues, per lane, 4 (D=128) 16-byte loads of K
-// and of V: lane (n = lane%16, g = lane/16) reads row t0+n, dims [g*D/4,
-// (g+1)*D/4).  Scores come from v_mfma_f32_16x16x32_bf16 with K as the B
-// operand (column n = position) and Q as the A operand with row m holding
-// head (m % HG) of the workgroup's head group, so lane (n, g) receives its
-// heads' scores of its own position and needs no shuffles.  A workgroup
-// takes at most two query heads (HG <= 2: 64 fp32 accumulators per lane);
-// the split count is a multiple of 8 whenever a KV head has several head
-// groups, so the workgroups of one (sequence, KV head, split) differ in
-// block id by a multiple of 8, run on the same XCD, and the second read of
-// each K/V row is served by that XCD's L2.  Softmax is online across
-// 128-position iterations in the log2 domain; P.V runs as fp32 FMAs on the
-// lane's own V slice.  Partials (m, l, o[D]) are merged across the 4 waves
-// in LDS and written once per workgroup; the combine kernel merges splits.
+// Per iteration a wave takes 32 positions (two 16-row tiles):
+// * K: lane (n = lane%16, g = lane/16) loads rows t0+n and t0+16+n with
+//   16-byte loads, directly in the A-operand layout of
+//   v_mfma_f32_16x16x32_bf16; B = Q^T (column n = head n of the group).
+//   Load i of lane (n, g) takes dims [32i + 8g, 32i + 8g + 8): the k-order
+//   of a dot product is free as long as Q uses the same one, and this order
+//   makes each load instruction read 64 contiguous bytes per row.  The next
+//   iteration's K/V loads are issued as soon as this iteration's registers
+//   are consumed, so they overlap the softmax and P.V.
+//   The result S^T leaves lane (head n, g) holding positions
+//   {4g..4g+3, 16+4g..16+4g+3} of its head: softmax is in-lane plus two
+//   shuffles across the four lanes of a head.
+// * Those eight probabilities, as bf16, are exactly the B operand (P^T) of
+//   O^T += V^T P^T.  V goes registers -> the wave's own LDS tile (row-major,
+//   16-byte chunks XOR-swizzled by row), and the A operand V^T comes back
+//   with ds_read_b64_tr_b16, which transposes 16-bit elements across each
+//   16-lane group: source lane s points at row p(g, s/4), column
+//   16*db + 4*(s%4), and lane i receives rows p(g, 0..3) of column 16*db + i.
+// * O^T accumulates in lane (head n, g) as d = 16*db + 4g + r: 32 fp32
+//   accumulators per lane for D = 128, nothing to reduce across lanes.
+// Softmax is online in the log2 domain; each wave keeps its own (m, l, O)
+// and the four waves are merged in LDS into one partial (m, l, o[D]) per
+// head and workgroup; the combine kernel merges the splits.
 #include <math.h>
 
 #include "common.hpp"
@@ -29,9 +38,12 @@
 namespace tiattn {
 namespace {
 
+typedef short v4i16_t __attribute__((ext_vector_type(4)));
+
 constexpr int kDecWaves = 4;
-constexpr int kDecTilesPerWave = 2;
-constexpr int kDecIterRows = kDecWaves * kDecTilesPerWave * 16;  // 128 positions
+constexpr int kDecWaveRows = 32;                          // positions per wave-iteration
+constexpr int kDecIterRows = kDecWaves * kDecWaveRows;    // 128 positions
+constexpr int kDecMaxHeads = 16;                          // MFMA columns = query heads
 
 __device__ __forceinline__ uint32_t seq_length(const DecodeProblem& p, uint32_t b) {
     if (p.len_mode == kLenHost) return p.len_host;
@@ -52,21 +64,44 @@ __device__ __forceinline__ void split_range(uint32_t L, uint32_t splits, uint32_
     *end = (uint64_t)*begin + per < L ? *begin + per : L;
 }
 
-template <int D, int HG>
-__global__ __launch_bounds__(256, 2) void decode_split_kernel(DecodeProblem p, DecodePartials part,
+// Row-major V tile of one wave in LDS: element (row, col) at
+// row*D + 8*((col/8) ^ swz(row)) + col%8.
+template <int D>
+__device__ __forceinline__ int vt_swz(int row) {
+    return (2 * row) & (D / 8 - 1);
+}
+
+__device__ __forceinline__ v4i16_t ds_read_tr16(const uint16_t* p) {
+    return __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (__attribute__((address_space(3))) v4i16_t*)(p));
+}
+
+__device__ __forceinline__ float shfl_xor_f(float x, int m) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(((__lane_id() ^ m) << 2),
+                                                                   __builtin_bit_cast(int, x)));
+}
+
+template <int D>
+__global__ __launch_bounds__(256, 3) void decode_split_kernel(DecodeProblem p, DecodePartials part,
                                                               float scale_log2) {
-    constexpr int DG = D / 4;    // dims per lane group
-    constexpr int NLD = DG / 8;  // 16-byte loads per row slice == MFMA k-steps
-    constexpr int TPW = kDecTilesPerWave;
-    constexpr int STEP = kDecIterRows;
+    constexpr int NLD = D / 32;  // 16-byte loads per row and lane == QK k-steps
+    constexpr int NDB = D / 16;  // PV output blocks of 16 dims
+    constexpr int V_ELEMS = kDecWaveRows * D;
+    // LDS: per-wave V tiles during the loop, the cross-wave merge afterwards.
+    constexpr int LDS_BYTES_V = kDecWaves * V_ELEMS * 2;
+    constexpr int LDS_BYTES_O = kDecWaves * kDecMaxHeads * D * 4;
+    __shared__ __align__(16) unsigned char s_raw[LDS_BYTES_V > LDS_BYTES_O ? LDS_BYTES_V
+                                                                            : LDS_BYTES_O];
+    __shared__ float s_ml[kDecWaves][kDecMaxHeads][2];
+
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int n = lane & 15, g = lane >> 4;
     const uint32_t group = p.hq / p.hkv;
-    const uint32_t n_hg = (group + HG - 1) / HG;
+    const uint32_t n_hg = (group + kDecMaxHeads - 1) / kDecMaxHeads;
     const uint32_t kvh = blockIdx.y / n_hg, hgi = blockIdx.y % n_hg;
     const uint32_t b = blockIdx.z;
-    const uint32_t h0 = kvh * group + hgi * HG;
-    const uint32_t nh = min((uint32_t)HG, group - hgi * HG);
+    const uint32_t h0 = kvh * group + hgi * kDecMaxHeads;
+    const uint32_t nh = min((uint32_t)kDecMaxHeads, group - hgi * kDecMaxHeads);
     const int64_t bh0 = (int64_t)b * p.hq + h0;
 
     const uint32_t L = seq_length(p, b);
@@ -81,138 +116,150 @@ __global__ __launch_bounds__(256, 2) void decode_split_kernel(DecodeProblem p, D
         return;
     }
 
-    // A operand: row m = n of the 16x32 tile holds head slot m % HG, so
-    // result row 4g + r (lane (n, g), value r) is head slot r % HG.
-    const uint32_t slot_a = n % HG;
-    const uint32_t qh = h0 + (slot_a < nh ? slot_a : 0);
-    const uint16_t* qrow = p.q + ((int64_t)b * p.hq + qh) * D + DG * g;
-    bf16x8_t qa[NLD];
+    // B operand Q^T: column n = head h0 + n (zero beyond the group).
+    bf16x8_t qb[NLD];
+    {
+        const bool has = (uint32_t)n < nh;
+        const uint16_t* qrow = p.q + (bh0 + (has ? n : 0)) * D + 8 * g;
 #pragma unroll
-    for (int i = 0; i < NLD; ++i) qa[i] = as_bf16x8(ldg16(qrow + 8 * i));
-
-    const int64_t row_stride = (int64_t)p.hkv * D;
-    const uint16_t* kbase = p.k + (int64_t)b * p.kv_stride + (int64_t)kvh * D + DG * g;
-    const uint16_t* vbase = p.v + (int64_t)b * p.kv_stride + (int64_t)kvh * D + DG * g;
-
-    float m_run[HG], l_run[HG], acc[HG][DG];
-#pragma unroll
-    for (int s = 0; s < HG; ++s) {
-        m_run[s] = -INFINITY;
-        l_run[s] = 0.0f;
-#pragma unroll
-        for (int d = 0; d < DG; ++d) acc[s][d] = 0.0f;
+        for (int i = 0; i < NLD; ++i) {
+            uint4 x = ldg16(qrow + 32 * i);
+            if (!has) x = make_uint4(0, 0, 0, 0);
+            qb[i] = as_bf16x8(x);
+        }
     }
 
-    for (uint32_t base = t_begin; base < t_end; base += STEP) {
-        uint4 kr[TPW][NLD], vr[TPW][NLD];
-        bool valid[TPW];
+    const int64_t row_stride = (int64_t)p.hkv * D;
+    const uint16_t* kbase = p.k + (int64_t)b * p.kv_stride + (int64_t)kvh * D + 8 * g;
+    const uint16_t* vbase = p.v + (int64_t)b * p.kv_stride + (int64_t)kvh * D + 8 * g;
+    uint16_t* vs = reinterpret_cast<uint16_t*>(s_raw) + wave * V_ELEMS;
+
+    f32x4_t acc[NDB];
 #pragma unroll
-        for (int j = 0; j < TPW; ++j) {
-            const uint32_t t = base + (wave * TPW + j) * 16 + n;
-            valid[j] = t < t_end;
-            const uint32_t tc = valid[j] ? t : t_end - 1;
+    for (int db = 0; db < NDB; ++db) acc[db] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    float m_run = -INFINITY, l_run = 0.0f;
+
+    // tr16 read addresses (element offsets) of this lane for both halves.
+    int tr_off[2][NDB];
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) {
+        const int row = 16 * hh + 4 * g + (n >> 2);
+#pragma unroll
+        for (int db = 0; db < NDB; ++db) {
+            const int col = 16 * db + 4 * (n & 3);
+            tr_off[hh][db] = row * D + 8 * ((col >> 3) ^ vt_swz<D>(row)) + (col & 7);
+        }
+    }
+
+    uint4 kr[2][NLD], vr[2][NLD];
+    auto load_kv = [&](uint32_t bb) {
+        const uint32_t tb = bb + wave * kDecWaveRows;
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt) {
+            const uint32_t t = tb + 16 * tt + n;
+            const uint32_t tc = t < t_end ? t : t_end - 1;
             const uint16_t* kp = kbase + (int64_t)tc * row_stride;
             const uint16_t* vp = vbase + (int64_t)tc * row_stride;
 #pragma unroll
-            for (int i = 0; i < NLD; ++i) kr[j][i] = ldg16(kp + 8 * i);
+            for (int i = 0; i < NLD; ++i) kr[tt][i] = ldg16(kp + 32 * i);
 #pragma unroll
-            for (int i = 0; i < NLD; ++i) vr[j][i] = ldg16(vp + 8 * i);
+            for (int i = 0; i < NLD; ++i) vr[tt][i] = ldg16(vp + 32 * i);
         }
-
-        // Scores: lane (n, g) value r = head slot r % HG at position n.
-        float s[TPW][HG];
+    };
+    load_kv(t_begin);
+    for (uint32_t base = t_begin; base < t_end; base += kDecIterRows) {
+        const uint32_t t0 = base + wave * kDecWaveRows;
+        // V -> this wave's LDS tile (row 16*tt + n, 16-byte chunk 4i + g).
 #pragma unroll
-        for (int j = 0; j < TPW; ++j) {
-            f32x4_t c = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-            for (int i = 0; i < NLD; ++i) c = mfma16x16x32(qa[i], as_bf16x8(kr[j][i]), c);
-#pragma unroll
-            for (int sl = 0; sl < HG; ++sl) s[j][sl] = valid[j] ? c[sl] : -INFINITY;
-        }
-
-        // Online softmax; the running max is made wave-uniform (row 0's value).
-#pragma unroll
-        for (int sl = 0; sl < HG; ++sl) {
-            float cm = s[0][sl];
-#pragma unroll
-            for (int j = 1; j < TPW; ++j) cm = fmaxf(cm, s[j][sl]);
-            cm = row16_max(cm);
-            cm = __builtin_bit_cast(float,
-                                    __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, cm)));
-            const float m_new = fmaxf(m_run[sl], cm * scale_log2);
-            if (m_new > m_run[sl]) {
-                const float alpha = exp2f(m_run[sl] - m_new);
-                l_run[sl] *= alpha;
-#pragma unroll
-                for (int d = 0; d < DG; ++d) acc[sl][d] *= alpha;
-                m_run[sl] = m_new;
-            }
-        }
-
-#pragma unroll
-        for (int j = 0; j < TPW; ++j) {
-            float pj[HG];
-#pragma unroll
-            for (int sl = 0; sl < HG; ++sl) {
-                const float mref = m_run[sl] == -INFINITY ? 0.0f : m_run[sl];
-                pj[sl] = exp2f(fmaf(s[j][sl], scale_log2, -mref));
-                l_run[sl] += pj[sl];
-            }
+        for (int tt = 0; tt < 2; ++tt) {
+            const int row = 16 * tt + n;
 #pragma unroll
             for (int i = 0; i < NLD; ++i) {
-                const uint32_t w[4] = {vr[j][i].x, vr[j][i].y, vr[j][i].z, vr[j][i].w};
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const float v0 = bf16_lo(w[e]), v1 = bf16_hi(w[e]);
-#pragma unroll
-                    for (int sl = 0; sl < HG; ++sl) {
-                        acc[sl][8 * i + 2 * e] = fmaf(pj[sl], v0, acc[sl][8 * i + 2 * e]);
-                        acc[sl][8 * i + 2 * e + 1] = fmaf(pj[sl], v1, acc[sl][8 * i + 2 * e + 1]);
-                    }
-                }
+                const int chunk = 4 * i + g;
+                *reinterpret_cast<uint4*>(vs + row * D + 8 * (chunk ^ vt_swz<D>(row))) = vr[tt][i];
             }
+        }
+        // S^T: lane (head n, g) value r of tile tt = position t0 + 16*tt + 4g + r.
+        f32x4_t st[2];
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt) {
+            st[tt] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int i = 0; i < NLD; ++i) st[tt] = mfma16x16x32(as_bf16x8(kr[tt][i]), qb[i], st[tt]);
+        }
+        if (base + kDecIterRows < t_end) load_kv(base + kDecIterRows);
+        float mx = -INFINITY;
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const uint32_t t = t0 + 16 * tt + 4 * g + r;
+                if (t >= t_end) st[tt][r] = -INFINITY;
+                mx = fmaxf(mx, st[tt][r]);
+            }
+        mx = fmaxf(mx, shfl_xor_f(mx, 16));
+        mx = fmaxf(mx, shfl_xor_f(mx, 32));
+        const float m_new = fmaxf(m_run, mx * scale_log2);
+        if (m_new > m_run) {
+            const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+            l_run *= alpha;
+#pragma unroll
+            for (int db = 0; db < NDB; ++db) acc[db] *= alpha;
+            m_run = m_new;
+        }
+        const float mref = m_run == -INFINITY ? 0.0f : m_run;
+        float pr[8];
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                pr[4 * tt + r] = __builtin_amdgcn_exp2f(fmaf(st[tt][r], scale_log2, -mref));
+                l_run += pr[4 * tt + r];
+            }
+        const bf16x8_t pb = as_bf16x8(make_uint4(pack_bf16x2(pr[0], pr[1]), pack_bf16x2(pr[2], pr[3]),
+                                                 pack_bf16x2(pr[4], pr[5]), pack_bf16x2(pr[6], pr[7])));
+#pragma unroll
+        for (int db = 0; db < NDB; ++db) {
+            const v4i16_t lo = ds_read_tr16(vs + tr_off[0][db]);
+            const v4i16_t hi = ds_read_tr16(vs + tr_off[1][db]);
+            const uint4 a = make_uint4(__builtin_bit_cast(uint2, lo).x, __builtin_bit_cast(uint2, lo).y,
+                                       __builtin_bit_cast(uint2, hi).x, __builtin_bit_cast(uint2, hi).y);
+            acc[db] = mfma16x16x32(as_bf16x8(a), pb, acc[db]);
         }
     }
 
-    // Sum over the 16 positions held by each row, then merge the 4 waves.
+    // Merge the four waves: per head n, l summed over the 4 lanes of the head.
+    l_run += shfl_xor_f(l_run, 16);
+    l_run += shfl_xor_f(l_run, 32);
+    __syncthreads();  // every wave is done with its V tile; s_raw becomes s_o
+    float* s_o = reinterpret_cast<float*>(s_raw);  // [wave][head][D]
+    if ((uint32_t)n < nh) {
 #pragma unroll
-    for (int sl = 0; sl < HG; ++sl) {
-        l_run[sl] = row16_sum(l_run[sl]);
+        for (int db = 0; db < NDB; ++db)
 #pragma unroll
-        for (int d = 0; d < DG; ++d) acc[sl][d] = row16_sum(acc[sl][d]);
-    }
-    __shared__ float s_o[kDecWaves][HG][D];
-    __shared__ float s_ml[kDecWaves][HG][2];
-    if (n == 0) {
-#pragma unroll
-        for (int sl = 0; sl < HG; ++sl)
-#pragma unroll
-            for (int d = 0; d < DG; ++d) s_o[wave][sl][DG * g + d] = acc[sl][d];
-    }
-    if (lane == 0) {
-#pragma unroll
-        for (int sl = 0; sl < HG; ++sl) {
-            s_ml[wave][sl][0] = m_run[sl];
-            s_ml[wave][sl][1] = l_run[sl];
+            for (int r = 0; r < 4; ++r)
+                s_o[(wave * kDecMaxHeads + n) * D + 16 * db + 4 * g + r] = acc[db][r];
+        if (g == 0) {
+            s_ml[wave][n][0] = m_run;
+            s_ml[wave][n][1] = l_run;
         }
     }
     __syncthreads();
-    for (int e = threadIdx.x; e < HG * D; e += blockDim.x) {
-        const int sl = e / D, d = e % D;
-        if (sl >= (int)nh) continue;
+    for (int e = threadIdx.x; e < (int)nh * D; e += blockDim.x) {
+        const int hs = e / D, d = e % D;
         float M = -INFINITY;
 #pragma unroll
-        for (int w = 0; w < kDecWaves; ++w) M = fmaxf(M, s_ml[w][sl][0]);
+        for (int w = 0; w < kDecWaves; ++w) M = fmaxf(M, s_ml[w][hs][0]);
         float o = 0.0f, l = 0.0f;
 #pragma unroll
         for (int w = 0; w < kDecWaves; ++w) {
-            const float mw = s_ml[w][sl][0];
+            const float mw = s_ml[w][hs][0];
             if (mw == -INFINITY) continue;
-            const float sc = exp2f(mw - M);
-            o = fmaf(sc, s_o[w][sl][d], o);
-            l = fmaf(sc, s_ml[w][sl][1], l);
+            const float sc = __builtin_amdgcn_exp2f(mw - M);
+            o = fmaf(sc, s_o[(w * kDecMaxHeads + hs) * D + d], o);
+            l = fmaf(sc, s_ml[w][hs][1], l);
         }
-        const int64_t bh = bh0 + sl;
+        const int64_t bh = bh0 + hs;
         part.o[bh * part.o_head + (int64_t)blockIdx.x * part.o_split + d] = o;
         if (d == 0) {
             float* ml = part.ml + bh * part.ml_head + blockIdx.x * 2;
@@ -222,38 +269,78 @@ __global__ __launch_bounds__(256, 2) void decode_split_kernel(DecodeProblem p, D
     }
 }
 
-// Merge the splits of one (sequence, q-head): thread d produces o[d].
+// Merge the splits of one (sequence, q-head) in a 256-thread block.  The
+// per-split weights 2^(m_s - M) go to LDS first, so the pass over the
+// partial outputs is a set of independent loads.  Empty splits (m = -inf)
+// get weight 0 and their never-written o is not used.
+constexpr int kCombineThreads = 256;
+constexpr int kMaxSplits = 1024;
+
+__device__ __forceinline__ float block_reduce(float x, bool is_max, float* s_red) {
+    x = is_max ? fmaxf(x, dpp_f32<kDppXor1>(x)) : x + dpp_f32<kDppXor1>(x);
+    x = is_max ? fmaxf(x, dpp_f32<kDppXor2>(x)) : x + dpp_f32<kDppXor2>(x);
+    x = is_max ? fmaxf(x, dpp_f32<kDppRowHalfMirror>(x)) : x + dpp_f32<kDppRowHalfMirror>(x);
+    x = is_max ? fmaxf(x, dpp_f32<kDppRowMirror>(x)) : x + dpp_f32<kDppRowMirror>(x);
+    x = is_max ? fmaxf(x, shfl_xor_f(x, 16)) : x + shfl_xor_f(x, 16);
+    x = is_max ? fmaxf(x, shfl_xor_f(x, 32)) : x + shfl_xor_f(x, 32);
+    const int wave = threadIdx.x >> 6;
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) s_red[wave] = x;
+    __syncthreads();
+    float r = s_red[0];
+    for (int w = 1; w < kCombineThreads / 64; ++w) r = is_max ? fmaxf(r, s_red[w]) : r + s_red[w];
+    return r;
+}
+
+// Returns o[d] for d = threadIdx.x % D (valid in threads < D); M and the
+// softmax denominator in *m_out / *l_out (all threads).
 template <int D>
-__device__ __forceinline__ void merge_splits(const DecodePartials& part, int64_t bh,
-                                             uint32_t splits, int d, float* out, float* m_out,
-                                             float* l_out) {
+__device__ float merge_splits(const DecodePartials& part, int64_t bh, uint32_t splits,
+                              float* m_out, float* l_out) {
+    __shared__ float s_w[kMaxSplits];
+    __shared__ float s_red[kCombineThreads / 64];
+    __shared__ float s_part[kCombineThreads];
     const float* ml = part.ml + bh * part.ml_head;
     const float* po = part.o + bh * part.o_head;
-    float M = -INFINITY;
-    for (uint32_t s = 0; s < splits; ++s) M = fmaxf(M, ml[2 * s]);
-    float num = 0.0f, den = 0.0f;
-    if (M != -INFINITY) {
-        for (uint32_t s = 0; s < splits; ++s) {
-            const float ms = ml[2 * s];
-            if (ms == -INFINITY) continue;
-            const float w = exp2f(ms - M);
-            num = fmaf(w, po[(int64_t)s * part.o_split + d], num);
-            den = fmaf(w, ml[2 * s + 1], den);
-        }
+    const int tid = threadIdx.x;
+    float mloc = -INFINITY;
+    for (uint32_t s = tid; s < splits; s += kCombineThreads) mloc = fmaxf(mloc, ml[2 * s]);
+    const float M = block_reduce(mloc, true, s_red);
+    float lloc = 0.0f;
+    for (uint32_t s = tid; s < splits; s += kCombineThreads) {
+        const float ms = ml[2 * s];
+        const float w = ms == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(ms - M);
+        s_w[s] = w;
+        lloc = fmaf(w, ml[2 * s + 1], lloc);
     }
-    *out = den > 0.0f ? num / den : 0.0f;
+    const float den = block_reduce(lloc, false, s_red);  // also orders the s_w writes
+    constexpr int NPART = kCombineThreads / D;
+    const int d = tid % D, q = tid / D;
+    float num = 0.0f;
+#pragma unroll 8
+    for (uint32_t s = q; s < splits; s += NPART) {
+        const float w = s_w[s];
+        const float o = po[(int64_t)s * part.o_split + d];
+        num += w != 0.0f ? w * o : 0.0f;
+    }
+    s_part[tid] = num;
+    __syncthreads();
+    float tot = 0.0f;
+    if (tid < D)
+        for (int k = 0; k < NPART; ++k) tot += s_part[k * D + tid];
     *m_out = M;
     *l_out = den;
+    return den > 0.0f ? tot / den : 0.0f;
 }
 
 template <int D>
-__global__ __launch_bounds__(D) void decode_combine_kernel(DecodePartials part, uint32_t splits,
-                                                           uint16_t* o) {
+__global__ __launch_bounds__(kCombineThreads) void decode_combine_kernel(DecodePartials part,
+                                                                         uint32_t splits,
+                                                                         uint16_t* o) {
     const int64_t bh = blockIdx.x;
-    const int d = threadIdx.x;
-    float r, m, l;
-    merge_splits<D>(part, bh, splits, d, &r, &m, &l);
-    o[bh * D + d] = f32_to_bf16(r);
+    float m, l;
+    const float r = merge_splits<D>(part, bh, splits, &m, &l);
+    if (threadIdx.x < D) o[bh * D + threadIdx.x] = f32_to_bf16(r);
 }
 
 // Reference-contract finaliser for one sequence: block h merges head h's
@@ -262,31 +349,20 @@ __global__ __launch_bounds__(D) void decode_combine_kernel(DecodePartials part, 
 // block only touches its own head's rows, and reads every partial before
 // the barrier, so partials may live inside score/O_buffer/O rows of head h.
 template <int D>
-__global__ __launch_bounds__(256) void decode_finalize_compat_kernel(DecodeProblem p,
-                                                                     DecodePartials part,
-                                                                     float* score, uint32_t msl,
-                                                                     float* o_buffer, uint16_t* o,
-                                                                     float scale_log2) {
+__global__ __launch_bounds__(kCombineThreads) void decode_finalize_compat_kernel(
+    DecodeProblem p, DecodePartials part, float* score, uint32_t msl, float* o_buffer,
+    uint16_t* o, float scale_log2) {
     const uint32_t h = blockIdx.x;
     const uint32_t L = seq_length(p, 0);
-    __shared__ float s_stats[2];
     __shared__ float s_q[D];
-    float my_o = 0.0f;
-    if (threadIdx.x < D) {
-        float m, l;
-        merge_splits<D>(part, h, p.splits, threadIdx.x, &my_o, &m, &l);
-        if (threadIdx.x == 0) {
-            s_stats[0] = m;
-            s_stats[1] = l;
-        }
-        s_q[threadIdx.x] = bf16_to_f32(p.q[(int64_t)h * D + threadIdx.x]);
-    }
-    __syncthreads();
+    float M, den;
+    const float my_o = merge_splits<D>(part, h, p.splits, &M, &den);
+    if (threadIdx.x < D) s_q[threadIdx.x] = bf16_to_f32(p.q[(int64_t)h * D + threadIdx.x]);
+    __syncthreads();  // all partial reads of this head are done
     if (threadIdx.x < D) {
         o_buffer[(int64_t)h * D + threadIdx.x] = my_o;
         o[(int64_t)h * D + threadIdx.x] = f32_to_bf16(my_o);
     }
-    const float M = s_stats[0], den = s_stats[1];
     const float inv = den > 0.0f ? 1.0f / den : 0.0f;
     const float mref = M == -INFINITY ? 0.0f : M;
     const uint32_t kvh = h / (p.hq / p.hkv);
@@ -306,62 +382,83 @@ __global__ __launch_bounds__(256) void decode_finalize_compat_kernel(DecodeProbl
                     dot = fmaf(s_q[8 * c + 2 * e + 1], bf16_hi(ws[e]), dot);
                 }
             }
-            val = exp2f(fmaf(dot, scale_log2, -mref)) * inv;
+            val = __builtin_amdgcn_exp2f(fmaf(dot, scale_log2, -mref)) * inv;
         }
         srow[t] = val;
     }
 }
 
-template <int D, int HG>
+template <int D>
 hipError_t launch_split_t(const DecodeProblem& p, const DecodePartials& part, hipStream_t st) {
     const uint32_t group = p.hq / p.hkv;
-    const uint32_t n_hg = (group + HG - 1) / HG;
-    const dim3 grid(p.splits, p.hkv * n_hg, p.batch);
+    const dim3 grid(p.splits, p.hkv * decode_head_groups(group), p.batch);
     const float sl2 = kLog2e / sqrtf((float)D);
-    hipLaunchKernelGGL((decode_split_kernel<D, HG>), grid, dim3(256), 0, st, p, part, sl2);
+    hipLaunchKernelGGL((decode_split_kernel<D>), grid, dim3(256), 0, st, p, part, sl2);
     return hipGetLastError();
 }
 
-template <int D>
-hipError_t launch_split_d(const DecodeProblem& p, const DecodePartials& part, hipStream_t st) {
-    const uint32_t group = p.hq / p.hkv;
-    if (group == 1) return launch_split_t<D, 1>(p, part, st);
-    return launch_split_t<D, 2>(p, part, st);
+// Concurrent split workgroups the device holds (CUs x resident blocks per
+// CU), queried once per device; 256 CUs x 3 when no device is visible.
+uint32_t split_slots(uint32_t d) {
+    static int cache[2][64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
+        (void)hipGetLastError();
+        return 256 * 3;
+    }
+    const int which = d == 64 ? 0 : 1;
+    int v = __atomic_load_n(&cache[which][dev], __ATOMIC_RELAXED);
+    if (v > 0) return (uint32_t)v;
+    int cus = 0, per = 0;
+    hipError_t e1 = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+    hipError_t e2 = d == 64
+        ? hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, decode_split_kernel<64>, 256, 0)
+        : hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, decode_split_kernel<128>, 256, 0);
+    if (e1 != hipSuccess || e2 != hipSuccess || cus <= 0 || per <= 0) {
+        (void)hipGetLastError();
+        return 256 * 3;
+    }
+    v = cus * per;
+    __atomic_store_n(&cache[which][dev], v, __ATOMIC_RELAXED);
+    return (uint32_t)v;
 }
 
 }  // namespace
 
-uint32_t decode_head_groups(uint32_t group) { return group == 1 ? 1 : (group + 1) / 2; }
+uint32_t decode_head_groups(uint32_t group) {
+    return (group + kDecMaxHeads - 1) / kDecMaxHeads;
+}
+
+uint32_t decode_max_splits() { return kMaxSplits; }
 
 uint32_t decode_default_splits(uint32_t batch, uint32_t hq, uint32_t hkv, uint32_t d,
                                uint32_t seq_len) {
-    (void)d;
     const uint32_t group = hq / hkv;
-    const uint32_t n_hg = decode_head_groups(group);
-    const uint64_t wgs_per_split = (uint64_t)batch * hkv * n_hg;
-    const uint64_t target = 1024;  // about 4 workgroups per CU on 256 CUs
-    uint64_t s = (target + wgs_per_split - 1) / wgs_per_split;
+    const uint64_t wgs_per_split = (uint64_t)batch * hkv * decode_head_groups(group);
+    const uint64_t slots = split_slots(d);
+    uint64_t s = slots / wgs_per_split;  // one round of resident workgroups
     const uint64_t max_s = ((uint64_t)seq_len + kDecIterRows - 1) / kDecIterRows;
     if (s > max_s) s = max_s;
-    if (n_hg > 1) s = (s + 7) / 8 * 8;  // same-XCD pairing, see the file header
+    if (s > kMaxSplits) s = kMaxSplits;
     if (s < 1) s = 1;
     return (uint32_t)s;
 }
 
 hipError_t launch_decode_split(const DecodeProblem& p, const DecodePartials& part,
                                hipStream_t stream) {
-    if (p.d == 64) return launch_split_d<64>(p, part, stream);
-    return launch_split_d<128>(p, part, stream);
+    if (p.d == 64) return launch_split_t<64>(p, part, stream);
+    return launch_split_t<128>(p, part, stream);
 }
 
 hipError_t launch_decode_combine(const DecodeProblem& p, const DecodePartials& part, uint16_t* o,
                                  hipStream_t stream) {
     const dim3 grid(p.batch * p.hq);
     if (p.d == 64)
-        hipLaunchKernelGGL(decode_combine_kernel<64>, grid, dim3(64), 0, stream, part, p.splits, o);
+        hipLaunchKernelGGL(decode_combine_kernel<64>, grid, dim3(kCombineThreads), 0, stream, part,
+                           p.splits, o);
     else
-        hipLaunchKernelGGL(decode_combine_kernel<128>, grid, dim3(128), 0, stream, part, p.splits,
-                           o);
+        hipLaunchKernelGGL(decode_combine_kernel<128>, grid, dim3(kCombineThreads), 0, stream,
+                           part, p.splits, o);
     return hipGetLastError();
 }
 
@@ -371,11 +468,11 @@ hipError_t launch_decode_finalize_compat(const DecodeProblem& p, const DecodePar
     const dim3 grid(p.hq);
     const float sl2 = kLog2e / sqrtf((float)p.d);
     if (p.d == 64)
-        hipLaunchKernelGGL(decode_finalize_compat_kernel<64>, grid, dim3(256), 0, stream, p, part,
-                           score, msl, o_buffer, o, sl2);
+        hipLaunchKernelGGL(decode_finalize_compat_kernel<64>, grid, dim3(kCombineThreads), 0,
+                           stream, p, part, score, msl, o_buffer, o, sl2);
     else
-        hipLaunchKernelGGL(decode_finalize_compat_kernel<128>, grid, dim3(256), 0, stream, p, part,
-                           score, msl, o_buffer, o, sl2);
+        hipLaunchKernelGGL(decode_finalize_compat_kernel<128>, grid, dim3(kCombineThreads), 0,
+                           stream, p, part, score, msl, o_buffer, o, sl2);
     return hipGetLastError();
 }
 

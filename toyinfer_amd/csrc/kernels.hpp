@@ -55,8 +55,10 @@ hipError_t launch_decode_finalize_compat(const DecodeProblem& p, const DecodePar
 
 uint32_t decode_default_splits(uint32_t batch, uint32_t hq, uint32_t hkv, uint32_t d,
                                uint32_t seq_len);
-// Workgroups per KV head: query heads are taken two at a time.
+// Workgroups per KV head: up to 16 query heads share one workgroup.
 uint32_t decode_head_groups(uint32_t group);
+// Largest split count the combine kernels accept.
+uint32_t decode_max_splits();
 
 // ----------------------------------------------------------------- prefill
 struct PrefillProblem {

@@ -14,15 +14,19 @@
 //   lane (q = lane%32, half = lane/32) holds 32 keys of query q, so the row
 //   max and row sum are in-lane plus one lane^32 exchange.
 // * O^T += V^T P^T on the same MFMA: B = P^T is exactly the lane's own
-//   probabilities (converted to bf16 in place); A = V^T is read from a
-//   transposed V tile in LDS with two 8-byte reads per operand.  The output
-//   lane again owns one query row, so the running rescale is in-lane.
+//   probabilities (converted to bf16 in place); A = V^T comes from the
+//   row-major V tile in LDS through ds_read_b64_tr_b16, which transposes
+//   16-bit elements across each 16-lane group (source lane s addresses key
+//   row base + s/4, dims d0 + 4*(s%4); lane i receives keys base..base+3 of
+//   dim d0 + i).  The output lane again owns one query row, so the running
+//   rescale is in-lane.
 // * The running max is only moved when it grows by more than 2^8 (the sum
 //   and output share the stale max, so the result is exact); fully masked
 //   tiles past the diagonal are never visited.
 // * K and V tiles are double-buffered in LDS: the next tile's global loads
-//   are in flight while the current tile computes.  K rows are stored with
-//   their 16-byte chunks XOR-swizzled by row; V^T rows are padded to 136 B.
+//   are in flight while the current tile computes.  K and V rows are stored
+//   with their 16-byte chunks XOR-swizzled by row (differently for K and V,
+//   each chosen for the access pattern of its MFMA operand reads).
 //
 // Optional fused prologue (Qwen3, src/transformer.cpp:380-391): Q rows are
 // RMS-normalised with gamma, rounded to bf16, rotated (RoPE at position =
@@ -40,23 +44,36 @@ constexpr int kPfBM = 128;  // query rows per workgroup
 constexpr int kPfBN = 64;   // keys per tile
 constexpr float kRescaleThreshold = 8.0f;
 
+typedef short v4i16_t __attribute__((ext_vector_type(4)));
+
 template <int D>
 struct PfShape {
-    static constexpr int CPR = D / 8;                       // 16-byte chunks per K row
-    static constexpr int VT_PITCH = kPfBN + 4;              // bf16 per V^T row (136 B)
-    static constexpr int K_ELEMS = kPfBN * D;
-    static constexpr int VT_ELEMS = D * VT_PITCH;
-    static constexpr int K_LOADS = kPfBN * D / 8 / kPfThreads;  // uint4 per thread
-    static constexpr int V_BLOCKS = (kPfBN / 4) * (D / 8);      // 4 keys x 8 dims blocks
-    static constexpr int KSTEPS = D / 16;                   // QK MFMA k-steps
-    static constexpr int DBLK = D / 32;                     // PV output d-blocks
+    static constexpr int CPR = D / 8;                           // 16-byte chunks per row
+    static constexpr int T_ELEMS = kPfBN * D;                   // one K or V tile
+    static constexpr int LOADS = kPfBN * D / 8 / kPfThreads;    // uint4 per thread per tile
+    static constexpr int KSTEPS = D / 16;                       // QK MFMA k-steps
+    static constexpr int DBLK = D / 32;                         // PV output d-blocks
 };
+
+// Chunk swizzles.  K: the QK A-operand read takes 32 rows at one chunk, so
+// XOR by row spreads them over all chunks.  V: a tr16 read takes 8 rows x 4
+// consecutive chunks, so XOR by 4*(row%4) places those rows' chunk groups
+// in four different quarters of the row.
+template <int D>
+__device__ __forceinline__ int k_swz(int row) { return row & (D / 8 - 1); }
+template <int D>
+__device__ __forceinline__ int v_swz(int row) { return (4 * row) & (D / 8 - 1); }
 
 template <int D>
 struct TileRegs {
-    uint4 k[PfShape<D>::K_LOADS];
-    uint4 v[4];
+    uint4 k[PfShape<D>::LOADS];
+    uint4 v[PfShape<D>::LOADS];
 };
+
+__device__ __forceinline__ v4i16_t ds_read_tr16(const uint16_t* p) {
+    return __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (__attribute__((address_space(3))) v4i16_t*)(p));
+}
 
 template <int D>
 __device__ __forceinline__ void load_tile(TileRegs<D>& r, const uint16_t* __restrict__ K,
@@ -65,25 +82,20 @@ __device__ __forceinline__ void load_tile(TileRegs<D>& r, const uint16_t* __rest
     using P = PfShape<D>;
     const int tid = threadIdx.x;
 #pragma unroll
-    for (int it = 0; it < P::K_LOADS; ++it) {
+    for (int it = 0; it < P::LOADS; ++it) {
         const int idx = tid + kPfThreads * it;
         const int row = idx / P::CPR, c = idx % P::CPR;
         const uint32_t key = n0 + row;
         const uint32_t kc = key < S ? key : S - 1;
-        uint4 x = ldg16(K + (int64_t)kc * kv_row + (int64_t)kvh * D + c * 8);
-        if (key >= S) x = make_uint4(0, 0, 0, 0);
-        r.k[it] = x;
-    }
-    if (tid < P::V_BLOCKS) {
-        const int dgi = tid % (D / 8), kgi = tid / (D / 8);
-#pragma unroll
-        for (int rr = 0; rr < 4; ++rr) {
-            const uint32_t key = n0 + 4 * kgi + rr;
-            const uint32_t kc = key < S ? key : S - 1;
-            uint4 x = ldg16(V + (int64_t)kc * kv_row + (int64_t)kvh * D + dgi * 8);
-            if (key >= S) x = make_uint4(0, 0, 0, 0);
-            r.v[rr] = x;
+        const int64_t off = (int64_t)kc * kv_row + (int64_t)kvh * D + c * 8;
+        uint4 x = ldg16(K + off);
+        uint4 y = ldg16(V + off);
+        if (key >= S) {
+            x = make_uint4(0, 0, 0, 0);
+            y = make_uint4(0, 0, 0, 0);
         }
+        r.k[it] = x;
+        r.v[it] = y;
     }
 }
 
@@ -92,32 +104,15 @@ __device__ __forceinline__ uint32_t word_of(const uint4& v, int i) {
 }
 
 template <int D>
-__device__ __forceinline__ void store_tile(const TileRegs<D>& r, uint16_t* sk, uint16_t* svt) {
+__device__ __forceinline__ void store_tile(const TileRegs<D>& r, uint16_t* sk, uint16_t* sv) {
     using P = PfShape<D>;
     const int tid = threadIdx.x;
 #pragma unroll
-    for (int it = 0; it < P::K_LOADS; ++it) {
+    for (int it = 0; it < P::LOADS; ++it) {
         const int idx = tid + kPfThreads * it;
         const int row = idx / P::CPR, c = idx % P::CPR;
-        const int phys = c ^ (row & (P::CPR - 1));
-        *reinterpret_cast<uint4*>(sk + row * D + phys * 8) = r.k[it];
-    }
-    if (tid < P::V_BLOCKS) {
-        const int dgi = tid % (D / 8), kgi = tid / (D / 8);
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const uint32_t w0 = word_of(r.v[0], j / 2), w1 = word_of(r.v[1], j / 2);
-            const uint32_t w2 = word_of(r.v[2], j / 2), w3 = word_of(r.v[3], j / 2);
-            uint2 out;
-            if ((j & 1) == 0) {
-                out.x = (w0 & 0xffffu) | (w1 << 16);
-                out.y = (w2 & 0xffffu) | (w3 << 16);
-            } else {
-                out.x = (w0 >> 16) | (w1 & 0xffff0000u);
-                out.y = (w2 >> 16) | (w3 & 0xffff0000u);
-            }
-            *reinterpret_cast<uint2*>(svt + (dgi * 8 + j) * P::VT_PITCH + 4 * kgi) = out;
-        }
+        *reinterpret_cast<uint4*>(sk + row * D + 8 * (c ^ k_swz<D>(row))) = r.k[it];
+        *reinterpret_cast<uint4*>(sv + row * D + 8 * (c ^ v_swz<D>(row))) = r.v[it];
     }
 }
 
@@ -190,8 +185,8 @@ __device__ __forceinline__ void load_q(bf16x8_t (&qf)[PfShape<D>::KSTEPS], const
 template <int D, bool FUSED>
 __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(PrefillProblem p, float scale_log2) {
     using P = PfShape<D>;
-    __shared__ __align__(16) uint16_t s_k[2][P::K_ELEMS];
-    __shared__ __align__(16) uint16_t s_vt[2][P::VT_ELEMS];
+    __shared__ __align__(16) uint16_t s_k[2][P::T_ELEMS];
+    __shared__ __align__(16) uint16_t s_v[2][P::T_ELEMS];
 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int ql = lane & 31, kg = lane >> 5;
@@ -223,7 +218,7 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(PrefillProblem p
         for (int i = 0; i < 16; ++i) oacc[db][i] = 0.0f;
     float m_run = -INFINITY, l_run = 0.0f;
 
-    store_tile<D>(regs, s_k[0], s_vt[0]);
+    store_tile<D>(regs, s_k[0], s_v[0]);
     __syncthreads();
 
     for (uint32_t t = 0; t < n_tiles; ++t) {
@@ -233,14 +228,14 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(PrefillProblem p
         if (t < wave_tiles) {
             const uint32_t n0 = t * kPfBN;
             const uint16_t* kb = s_k[buf];
-            const uint16_t* vb = s_vt[buf];
+            const uint16_t* vb = s_v[buf];
             f32x16_t st0, st1;
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
                 st0[i] = 0.0f;
                 st1[i] = 0.0f;
             }
-            const int sw = ql & (P::CPR - 1);
+            const int sw = k_swz<D>(ql);
 #pragma unroll
             for (int ks = 0; ks < P::KSTEPS; ++ks) {
                 const int phys = (ks * 2 + kg) ^ sw;
@@ -267,7 +262,7 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(PrefillProblem p
             if (__any(need)) {
                 float alpha = 1.0f;
                 if (need) {
-                    alpha = exp2f(m_run - mt);
+                    alpha = __builtin_amdgcn_exp2f(m_run - mt);
                     m_run = mt;
                 }
                 l_run *= alpha;
@@ -280,8 +275,8 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(PrefillProblem p
             float rs = 0.0f;
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
-                st0[i] = exp2f(fmaf(st0[i], scale_log2, -mref));
-                st1[i] = exp2f(fmaf(st1[i], scale_log2, -mref));
+                st0[i] = __builtin_amdgcn_exp2f(fmaf(st0[i], scale_log2, -mref));
+                st1[i] = __builtin_amdgcn_exp2f(fmaf(st1[i], scale_log2, -mref));
                 rs += st0[i] + st1[i];
             }
             l_run += rs;
@@ -297,20 +292,26 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(PrefillProblem p
                 w.w = pack_bf16x2(src[o8 + 6], src[o8 + 7]);
                 pf[tt] = as_bf16x8(w);
             }
+            // A = V^T for k-step tt: lane group G = lane/16 (kg = G/2) reads key
+            // rows 16*tt + 4*kg + s/4 (+8 for the second half) at dims
+            // 32*db + 16*(G%2) + 4*(s%4), s = lane%16.
+            const int s16 = lane & 15, grp = lane >> 4;
 #pragma unroll
             for (int db = 0; db < P::DBLK; ++db) {
-                const uint16_t* vrow = vb + (db * 32 + ql) * P::VT_PITCH + 4 * kg;
+                const int col = db * 32 + 16 * (grp & 1) + 4 * (s16 & 3);
 #pragma unroll
                 for (int tt = 0; tt < 4; ++tt) {
-                    const uint2 x0 = *reinterpret_cast<const uint2*>(vrow + 16 * tt);
-                    const uint2 x1 = *reinterpret_cast<const uint2*>(vrow + 16 * tt + 8);
-                    const uint4 a = make_uint4(x0.x, x0.y, x1.x, x1.y);
+                    const int r0 = 16 * tt + 4 * kg + (s16 >> 2), r1 = r0 + 8;
+                    const v4i16_t lo = ds_read_tr16(vb + r0 * D + 8 * ((col >> 3) ^ v_swz<D>(r0)) + (col & 7));
+                    const v4i16_t hi = ds_read_tr16(vb + r1 * D + 8 * ((col >> 3) ^ v_swz<D>(r1)) + (col & 7));
+                    const uint4 a = make_uint4(__builtin_bit_cast(uint2, lo).x, __builtin_bit_cast(uint2, lo).y,
+                                               __builtin_bit_cast(uint2, hi).x, __builtin_bit_cast(uint2, hi).y);
                     oacc[db] = mfma32x32x16(as_bf16x8(a), pf[tt], oacc[db]);
                 }
             }
         }
 
-        if (t + 1 < n_tiles) store_tile<D>(regs, s_k[buf ^ 1], s_vt[buf ^ 1]);
+        if (t + 1 < n_tiles) store_tile<D>(regs, s_k[buf ^ 1], s_v[buf ^ 1]);
         __syncthreads();
     }
 

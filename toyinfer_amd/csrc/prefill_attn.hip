@@ -24,9 +24,10 @@
 //   and output share the stale max, so the result is exact); fully masked
 //   tiles past the diagonal are never visited.
 // * K and V tiles are double-buffered in LDS: the next tile's global loads
-//   are in flight while the current tile computes.  K and V rows are stored
-//   with their 16-byte chunks XOR-swizzled by row (differently for K and V,
-//   each chosen for the access pattern of its MFMA operand reads).
+//   (buffer loads whose range check returns zeros past row S-1) are in
+//   flight while the current tile computes.  LDS rows are padded (K: D+8,
+//   V: D+32 elements) so that each MFMA-operand read pattern hits distinct
+//   banks and every LDS address is a per-lane constant plus an immediate.
 //
 // Optional fused prologue (Qwen3, src/transformer.cpp:380-391): Q rows are
 // RMS-normalised with gamma, rounded to bf16, rotated (RoPE at position =
@@ -49,20 +50,15 @@ typedef short v4i16_t __attribute__((ext_vector_type(4)));
 template <int D>
 struct PfShape {
     static constexpr int CPR = D / 8;                           // 16-byte chunks per row
-    static constexpr int T_ELEMS = kPfBN * D;                   // one K or V tile
+    static constexpr int PK = D + 8;                            // K row pitch (elements)
+    static constexpr int PV = D + 32;                           // V row pitch (elements)
+    static constexpr int K_ELEMS = kPfBN * PK;
+    static constexpr int V_ELEMS = kPfBN * PV;
     static constexpr int LOADS = kPfBN * D / 8 / kPfThreads;    // uint4 per thread per tile
+    static constexpr int ROWS_PER_LOAD = kPfThreads / CPR;      // rows covered by one load step
     static constexpr int KSTEPS = D / 16;                       // QK MFMA k-steps
     static constexpr int DBLK = D / 32;                         // PV output d-blocks
 };
-
-// Chunk swizzles.  K: the QK A-operand read takes 32 rows at one chunk, so
-// XOR by row spreads them over all chunks.  V: a tr16 read takes 8 rows x 4
-// consecutive chunks, so XOR by 4*(row%4) places those rows' chunk groups
-// in four different quarters of the row.
-template <int D>
-__device__ __forceinline__ int k_swz(int row) { return row & (D / 8 - 1); }
-template <int D>
-__device__ __forceinline__ int v_swz(int row) { return (4 * row) & (D / 8 - 1); }
 
 template <int D>
 struct TileRegs {
@@ -75,27 +71,28 @@ __device__ __forceinline__ v4i16_t ds_read_tr16(const uint16_t* p) {
         (__attribute__((address_space(3))) v4i16_t*)(p));
 }
 
+// Buffer resource over [base, base + bytes): loads outside return 0.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
+                                             0x00020000);
+}
+
+__device__ __forceinline__ uint4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+    return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
+}
+
+// Tile n0 of K and V into registers.  voff: this thread's byte offset of its
+// first chunk; soff: the tile's byte offset (n0 * row pitch).
 template <int D>
-__device__ __forceinline__ void load_tile(TileRegs<D>& r, const uint16_t* __restrict__ K,
-                                          const uint16_t* __restrict__ V, uint32_t n0, uint32_t S,
-                                          int64_t kv_row, uint32_t kvh) {
+__device__ __forceinline__ void load_tile(TileRegs<D>& r, __amdgpu_buffer_rsrc_t rk,
+                                          __amdgpu_buffer_rsrc_t rv, uint32_t voff,
+                                          uint32_t row_bytes, uint32_t soff) {
     using P = PfShape<D>;
-    const int tid = threadIdx.x;
 #pragma unroll
     for (int it = 0; it < P::LOADS; ++it) {
-        const int idx = tid + kPfThreads * it;
-        const int row = idx / P::CPR, c = idx % P::CPR;
-        const uint32_t key = n0 + row;
-        const uint32_t kc = key < S ? key : S - 1;
-        const int64_t off = (int64_t)kc * kv_row + (int64_t)kvh * D + c * 8;
-        uint4 x = ldg16(K + off);
-        uint4 y = ldg16(V + off);
-        if (key >= S) {
-            x = make_uint4(0, 0, 0, 0);
-            y = make_uint4(0, 0, 0, 0);
-        }
-        r.k[it] = x;
-        r.v[it] = y;
+        const uint32_t o = voff + it * P::ROWS_PER_LOAD * row_bytes;
+        r.k[it] = buf_load16(rk, o, soff);
+        r.v[it] = buf_load16(rv, o, soff);
     }
 }
 
@@ -107,12 +104,12 @@ template <int D>
 __device__ __forceinline__ void store_tile(const TileRegs<D>& r, uint16_t* sk, uint16_t* sv) {
     using P = PfShape<D>;
     const int tid = threadIdx.x;
+    const int row = tid / P::CPR, c = tid % P::CPR;
 #pragma unroll
     for (int it = 0; it < P::LOADS; ++it) {
-        const int idx = tid + kPfThreads * it;
-        const int row = idx / P::CPR, c = idx % P::CPR;
-        *reinterpret_cast<uint4*>(sk + row * D + 8 * (c ^ k_swz<D>(row))) = r.k[it];
-        *reinterpret_cast<uint4*>(sv + row * D + 8 * (c ^ v_swz<D>(row))) = r.v[it];
+        const int rr = row + it * P::ROWS_PER_LOAD;
+        *reinterpret_cast<uint4*>(sk + rr * P::PK + 8 * c) = r.k[it];
+        *reinterpret_cast<uint4*>(sv + rr * P::PV + 8 * c) = r.v[it];
     }
 }
 
@@ -185,8 +182,8 @@ __device__ __forceinline__ void load_q(bf16x8_t (&qf)[PfShape<D>::KSTEPS], const
 template <int D, bool FUSED>
 __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(PrefillProblem p, float scale_log2) {
     using P = PfShape<D>;
-    __shared__ __align__(16) uint16_t s_k[2][P::T_ELEMS];
-    __shared__ __align__(16) uint16_t s_v[2][P::T_ELEMS];
+    __shared__ __align__(16) uint16_t s_k[2][P::K_ELEMS];
+    __shared__ __align__(16) uint16_t s_v[2][P::V_ELEMS];
 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int ql = lane & 31, kg = lane >> 5;
@@ -203,13 +200,19 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(PrefillProblem p
     const uint32_t q0 = qt * kPfBM + wave * 32;
     const uint32_t qq = q0 + ql;
     const uint32_t wave_tiles = q0 < p.s ? (min(q0 + 31, p.s - 1) / kPfBN + 1) : 0;
-    const int64_t kv_row = (int64_t)p.hkv * D;
+    // K/V rows of this KV head: row t at byte t*row_bytes from the head's
+    // first element; the buffer range ends after row S-1's D elements.
+    const uint32_t row_bytes = p.hkv * D * 2;
+    const uint32_t kv_bytes = (p.s - 1) * row_bytes + D * 2;
+    const __amdgpu_buffer_rsrc_t rk = make_rsrc(p.k + (int64_t)kvh * D, kv_bytes);
+    const __amdgpu_buffer_rsrc_t rv = make_rsrc(p.v + (int64_t)kvh * D, kv_bytes);
+    const uint32_t voff = (threadIdx.x / P::CPR) * row_bytes + (threadIdx.x % P::CPR) * 16;
 
     bf16x8_t qf[P::KSTEPS];
     load_q<D, FUSED>(qf, p, qq, h, kg);
 
     TileRegs<D> regs;
-    load_tile<D>(regs, p.k, p.v, 0, p.s, kv_row, kvh);
+    load_tile<D>(regs, rk, rv, voff, row_bytes, 0);
 
     f32x16_t oacc[P::DBLK];
 #pragma unroll
@@ -223,7 +226,7 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(PrefillProblem p
 
     for (uint32_t t = 0; t < n_tiles; ++t) {
         const int buf = t & 1;
-        if (t + 1 < n_tiles) load_tile<D>(regs, p.k, p.v, (t + 1) * kPfBN, p.s, kv_row, kvh);
+        if (t + 1 < n_tiles) load_tile<D>(regs, rk, rv, voff, row_bytes, (t + 1) * kPfBN * row_bytes);
 
         if (t < wave_tiles) {
             const uint32_t n0 = t * kPfBN;
@@ -235,12 +238,11 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(PrefillProblem p
                 st0[i] = 0.0f;
                 st1[i] = 0.0f;
             }
-            const int sw = k_swz<D>(ql);
+            const uint16_t* ka = kb + ql * P::PK + 8 * kg;
 #pragma unroll
             for (int ks = 0; ks < P::KSTEPS; ++ks) {
-                const int phys = (ks * 2 + kg) ^ sw;
-                const uint4 a0 = *reinterpret_cast<const uint4*>(kb + ql * D + phys * 8);
-                const uint4 a1 = *reinterpret_cast<const uint4*>(kb + (32 + ql) * D + phys * 8);
+                const uint4 a0 = *reinterpret_cast<const uint4*>(ka + 16 * ks);
+                const uint4 a1 = *reinterpret_cast<const uint4*>(ka + 32 * P::PK + 16 * ks);
                 st0 = mfma32x32x16(as_bf16x8(a0), qf[ks], st0);
                 st1 = mfma32x32x16(as_bf16x8(a1), qf[ks], st1);
             }
@@ -253,10 +255,15 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(PrefillProblem p
                     if (key + 32 > qq) st1[i] = -INFINITY;
                 }
             }
-            float mx = fmaxf(st0[0], st1[0]);
+            float m8[8];
 #pragma unroll
-            for (int i = 1; i < 16; ++i) mx = fmaxf(mx, fmaxf(st0[i], st1[i]));
-            mx = fmaxf(mx, xor32(mx));
+            for (int i = 0; i < 8; ++i)
+                m8[i] = fmaxf(fmaxf(st0[i], st0[i + 8]), fmaxf(st1[i], st1[i + 8]));
+#pragma unroll
+            for (int w = 4; w >= 1; w >>= 1)
+#pragma unroll
+                for (int i = 0; i < w; ++i) m8[i] = fmaxf(m8[i], m8[i + w]);
+            float mx = fmaxf(m8[0], xor32(m8[0]));
             const float mt = mx * scale_log2;
             const bool need = mt > m_run + kRescaleThreshold;
             if (__any(need)) {
@@ -272,14 +279,19 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(PrefillProblem p
                     for (int i = 0; i < 16; ++i) oacc[db][i] *= alpha;
             }
             const float mref = m_run == -INFINITY ? 0.0f : m_run;
-            float rs = 0.0f;
+            float r8[8];
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
                 st0[i] = __builtin_amdgcn_exp2f(fmaf(st0[i], scale_log2, -mref));
                 st1[i] = __builtin_amdgcn_exp2f(fmaf(st1[i], scale_log2, -mref));
-                rs += st0[i] + st1[i];
             }
-            l_run += rs;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) r8[i] = (st0[i] + st0[i + 8]) + (st1[i] + st1[i + 8]);
+#pragma unroll
+            for (int w = 4; w >= 1; w >>= 1)
+#pragma unroll
+                for (int i = 0; i < w; ++i) r8[i] += r8[i + w];
+            l_run += r8[0];
             bf16x8_t pf[4];
 #pragma unroll
             for (int tt = 0; tt < 4; ++tt) {
@@ -296,14 +308,13 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(PrefillProblem p
             // rows 16*tt + 4*kg + s/4 (+8 for the second half) at dims
             // 32*db + 16*(G%2) + 4*(s%4), s = lane%16.
             const int s16 = lane & 15, grp = lane >> 4;
+            const uint16_t* va = vb + (4 * kg + (s16 >> 2)) * P::PV + 16 * (grp & 1) + 4 * (s16 & 3);
 #pragma unroll
             for (int db = 0; db < P::DBLK; ++db) {
-                const int col = db * 32 + 16 * (grp & 1) + 4 * (s16 & 3);
 #pragma unroll
                 for (int tt = 0; tt < 4; ++tt) {
-                    const int r0 = 16 * tt + 4 * kg + (s16 >> 2), r1 = r0 + 8;
-                    const v4i16_t lo = ds_read_tr16(vb + r0 * D + 8 * ((col >> 3) ^ v_swz<D>(r0)) + (col & 7));
-                    const v4i16_t hi = ds_read_tr16(vb + r1 * D + 8 * ((col >> 3) ^ v_swz<D>(r1)) + (col & 7));
+                    const v4i16_t lo = ds_read_tr16(va + 16 * tt * P::PV + 32 * db);
+                    const v4i16_t hi = ds_read_tr16(va + (16 * tt + 8) * P::PV + 32 * db);
                     const uint4 a = make_uint4(__builtin_bit_cast(uint2, lo).x, __builtin_bit_cast(uint2, lo).y,
                                                __builtin_bit_cast(uint2, hi).x, __builtin_bit_cast(uint2, hi).y);
                     oacc[db] = mfma32x32x16(as_bf16x8(a), pf[tt], oacc[db]);

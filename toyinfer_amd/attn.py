@@ -33,6 +33,8 @@ SIGNATURES = {
     "toyinfer_last_hip_error": (_i32, []),
     "toyinfer_abi_version": (_u32, []),
     "toyinfer_flash_attention_v1_bf16": (_i32, [_vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _vp]),
+    "toyinfer_flash_attention_algo_bf16": (_i32, [_vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _i32,
+                                                  _vp]),
     "toyinfer_prefill_qknorm_rope_attention_bf16": (
         _i32, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _f32, _u32, _u32, _u32, _u32, _vp]),
     "toyinfer_attention_bf16": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32,
@@ -44,6 +46,7 @@ SIGNATURES = {
     "toyinfer_decode_default_splits": (_u32, [_u32, _u32, _u32, _u32, _u32]),
     "toyinfer_decode_workspace_bytes": (_sz, [_u32, _u32, _u32, _u32]),
     "toyinfer_precompute_freq_f32": (_i32, [_vp, _i32, _f32, _vp]),
+    "toyinfer_rope_cos_sin_f32": (_i32, [_vp, _vp, _u32, _u32, _vp]),
     "toyinfer_multi_rmsnorm_bf16": (_i32, [_vp, _vp, _vp, _f32, _u32, _u32, _vp]),
     "toyinfer_batch_multi_rmsnorm_bf16": (_i32, [_vp, _vp, _vp, _f32, _u32, _u32, _u32, _vp]),
     "toyinfer_batch_rope_bf16": (_i32, [_vp, _vp, _u32, _u32, _u32, _vp]),
@@ -119,15 +122,29 @@ def flash_attention_v1_bf16(Qs, Ks, Vs, Os, num_q_heads: int, num_kv_heads: int,
                                                 _stream(stream)))
 
 
-def prefill_qknorm_rope_attention_bf16(Q_raw, K_raw, Vs, Os, K_out, q_gamma, k_gamma, inv_freq,
-                                       rms_norm_eps: float, num_q_heads: int, num_kv_heads: int,
-                                       heads_dim: int, seq_len: int, stream=None) -> None:
-    """QK-RMSNorm + RoPE fused in front of causal GQA prefill."""
+ALGO_AUTO, ALGO_SPLIT_KEYS, ALGO_ROW_TILES = 0, 1, 2
+
+
+def flash_attention_algo_bf16(Qs, Ks, Vs, Os, num_q_heads: int, num_kv_heads: int,
+                              heads_dim: int, seq_len: int, algo: int, stream=None) -> None:
+    """Prefill with an explicit kernel choice (0 auto, 1 split keys, 2 row tiles)."""
+    _check("flash_attention_algo_bf16",
+           LIB.toyinfer_flash_attention_algo_bf16(_ptr(Qs), _ptr(Ks), _ptr(Vs), _ptr(Os),
+                                                  num_q_heads, num_kv_heads, heads_dim, seq_len,
+                                                  algo, _stream(stream)))
+
+
+def prefill_qknorm_rope_attention_bf16(Q_raw, K_raw, Vs, Os, K_out, q_gamma, k_gamma,
+                                       rope_cos_sin, rms_norm_eps: float, num_q_heads: int,
+                                       num_kv_heads: int, heads_dim: int, seq_len: int,
+                                       stream=None) -> None:
+    """QK-RMSNorm + RoPE fused in front of causal GQA prefill; rope_cos_sin is
+    the fp32 [>= S][D/2][2] table from rope_cos_sin_f32."""
     _check("prefill_qknorm_rope_attention_bf16",
            LIB.toyinfer_prefill_qknorm_rope_attention_bf16(
                _ptr(Q_raw), _ptr(K_raw), _ptr(Vs), _ptr(Os), _ptr(K_out), _ptr(q_gamma),
-               _ptr(k_gamma), _ptr(inv_freq), rms_norm_eps, num_q_heads, num_kv_heads, heads_dim,
-               seq_len, _stream(stream)))
+               _ptr(k_gamma), _ptr(rope_cos_sin), rms_norm_eps, num_q_heads, num_kv_heads,
+               heads_dim, seq_len, _stream(stream)))
 
 
 # ----------------------------------------------------------------- decode
@@ -180,6 +197,13 @@ def decode_attention_bf16(q, k_cache, v_cache, o, batch: int, num_q_heads: int,
 def precompute_freq_f32(inv_freq, head_dim: int, theta: float, stream=None) -> None:
     _check("precompute_freq_f32",
            LIB.toyinfer_precompute_freq_f32(_ptr(inv_freq), head_dim, theta, _stream(stream)))
+
+
+def rope_cos_sin_f32(table, inv_freq, num_positions: int, head_dim: int, stream=None) -> None:
+    """table [num_positions][D/2][2] fp32 = (cos, sin)(t * inv_freq[i])."""
+    _check("rope_cos_sin_f32",
+           LIB.toyinfer_rope_cos_sin_f32(_ptr(table), _ptr(inv_freq), num_positions, head_dim,
+                                         _stream(stream)))
 
 
 def multi_rmsnorm_bf16(input, weight, output, rms_norm_eps: float, nums_head: int,

@@ -37,6 +37,11 @@ hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 
 size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 
+// Prefill addresses one KV head's rows with 32-bit byte offsets.
+bool kv_fits_32bit(uint32_t s, uint32_t hkv, uint32_t d) {
+    return (uint64_t)s * hkv * d * 2 < 0xffffffffull;
+}
+
 // Where the reference-contract decode keeps its split partials: in score
 // rows when they are long enough (mode B), else in O_buffer/O rows with a
 // single split (mode A).  Either way each head's partials live only in that
@@ -89,7 +94,17 @@ uint32_t toyinfer_abi_version(void) { return TOYINFER_ABI_VERSION; }
 int toyinfer_flash_attention_v1_bf16(const void* Qs, const void* Ks, const void* Vs, void* Os,
                                      uint32_t num_q_heads, uint32_t num_kv_heads,
                                      uint32_t heads_dim, uint32_t seq_len, void* stream) {
+    return toyinfer_flash_attention_algo_bf16(Qs, Ks, Vs, Os, num_q_heads, num_kv_heads,
+                                              heads_dim, seq_len, 0, stream);
+}
+
+int toyinfer_flash_attention_algo_bf16(const void* Qs, const void* Ks, const void* Vs, void* Os,
+                                       uint32_t num_q_heads, uint32_t num_kv_heads,
+                                       uint32_t heads_dim, uint32_t seq_len, int algo,
+                                       void* stream) {
     if (int st = check_heads(num_q_heads, num_kv_heads, heads_dim)) return st;
+    if (algo < 0 || algo > 2) return TOYINFER_ERR_INVALID_ARGUMENT;
+    if (!kv_fits_32bit(seq_len, num_kv_heads, heads_dim)) return TOYINFER_ERR_UNSUPPORTED;
     if (seq_len == 0) return TOYINFER_ERR_INVALID_ARGUMENT;
     if (!Qs || !Ks || !Vs || !Os) return TOYINFER_ERR_INVALID_ARGUMENT;
     if (!aligned(Qs, 16) || !aligned(Ks, 16) || !aligned(Vs, 16) || !aligned(Os, 16))
@@ -106,30 +121,32 @@ int toyinfer_flash_attention_v1_bf16(const void* Qs, const void* Ks, const void*
     p.hkv = num_kv_heads;
     p.d = heads_dim;
     p.fused_q = false;
+    p.variant = algo;
     return from_hip(launch_prefill(p, as_stream(stream)));
 }
 
 int toyinfer_prefill_qknorm_rope_attention_bf16(
     const void* Q_raw, const void* K_raw, const void* Vs, void* Os, void* K_out,
-    const void* q_gamma, const void* k_gamma, const float* inv_freq, float rms_norm_eps,
+    const void* q_gamma, const void* k_gamma, const float* rope_cos_sin, float rms_norm_eps,
     uint32_t num_q_heads, uint32_t num_kv_heads, uint32_t heads_dim, uint32_t seq_len,
     void* stream) {
     if (int st = check_heads(num_q_heads, num_kv_heads, heads_dim)) return st;
     if (seq_len == 0) return TOYINFER_ERR_INVALID_ARGUMENT;
-    if (!Q_raw || !K_raw || !Vs || !Os || !K_out || !q_gamma || !k_gamma || !inv_freq)
+    if (!kv_fits_32bit(seq_len, num_kv_heads, heads_dim)) return TOYINFER_ERR_UNSUPPORTED;
+    if (!Q_raw || !K_raw || !Vs || !Os || !K_out || !q_gamma || !k_gamma || !rope_cos_sin)
         return TOYINFER_ERR_INVALID_ARGUMENT;
     if (!aligned(Q_raw, 16) || !aligned(Vs, 16) || !aligned(Os, 16) || !aligned(K_out, 16) ||
         !aligned(q_gamma, 16) || !aligned(K_raw, 2) || !aligned(k_gamma, 2) ||
-        !aligned(inv_freq, 4))
+        !aligned(rope_cos_sin, 16))
         return TOYINFER_ERR_INVALID_ARGUMENT;
     if ((uint64_t)((seq_len + 127) / 128) * num_q_heads > 0x7fffffffull)
         return TOYINFER_ERR_INVALID_ARGUMENT;
     hipStream_t st = as_stream(stream);
     hipError_t e = launch_row_norm_rope(static_cast<const uint16_t*>(K_raw),
                                         static_cast<uint16_t*>(K_out),
-                                        static_cast<const uint16_t*>(k_gamma), inv_freq,
-                                        rms_norm_eps, seq_len, num_kv_heads, heads_dim,
-                                        kRowNorm | kRowRope, st);
+                                        static_cast<const uint16_t*>(k_gamma), nullptr,
+                                        rope_cos_sin, rms_norm_eps, seq_len, num_kv_heads,
+                                        heads_dim, kRowNorm | kRowRope, st);
     if (e != hipSuccess) return from_hip(e);
     PrefillProblem p{};
     p.q = static_cast<const uint16_t*>(Q_raw);
@@ -142,7 +159,7 @@ int toyinfer_prefill_qknorm_rope_attention_bf16(
     p.d = heads_dim;
     p.fused_q = true;
     p.q_gamma = static_cast<const uint16_t*>(q_gamma);
-    p.inv_freq = inv_freq;
+    p.rope = rope_cos_sin;
     p.eps = rms_norm_eps;
     return from_hip(launch_prefill(p, st));
 }
@@ -283,6 +300,16 @@ int toyinfer_precompute_freq_f32(float* inv_freq, int head_dim, float theta, voi
     return from_hip(launch_precompute_freq(inv_freq, head_dim, theta, as_stream(stream)));
 }
 
+int toyinfer_rope_cos_sin_f32(float* table, const float* inv_freq, uint32_t num_positions,
+                              uint32_t head_dim, void* stream) {
+    if (!table || !inv_freq || num_positions == 0 || head_dim < 2 || head_dim % 2 != 0)
+        return TOYINFER_ERR_INVALID_ARGUMENT;
+    if (!aligned(table, 8) || !aligned(inv_freq, 4)) return TOYINFER_ERR_INVALID_ARGUMENT;
+    if ((uint64_t)num_positions * (head_dim / 2) > 0xffffffffull * 128ull)
+        return TOYINFER_ERR_INVALID_ARGUMENT;
+    return from_hip(launch_rope_table(table, inv_freq, num_positions, head_dim, as_stream(stream)));
+}
+
 static int row_op(const void* input, const void* weight, void* output, const float* inv_freq,
                   float eps, uint32_t num_tokens, uint32_t nums_head, uint32_t head_dim, int mode,
                   void* stream) {
@@ -297,8 +324,8 @@ static int row_op(const void* input, const void* weight, void* output, const flo
         return TOYINFER_ERR_INVALID_ARGUMENT;
     return from_hip(launch_row_norm_rope(static_cast<const uint16_t*>(input),
                                          static_cast<uint16_t*>(output),
-                                         static_cast<const uint16_t*>(weight), inv_freq, eps,
-                                         num_tokens, nums_head, head_dim, mode,
+                                         static_cast<const uint16_t*>(weight), inv_freq, nullptr,
+                                         eps, num_tokens, nums_head, head_dim, mode,
                                          as_stream(stream)));
 }
 

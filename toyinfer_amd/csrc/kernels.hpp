@@ -69,8 +69,9 @@ struct PrefillProblem {
     uint32_t s, hq, hkv, d;
     bool fused_q;
     const uint16_t* q_gamma;  // [D] (fused_q)
-    const float* inv_freq;    // [D/2] (fused_q)
+    const float* rope;        // [S][D/2] (cos, sin) pairs (fused_q)
     float eps;
+    int variant;              // 0: pick by shape, 1: split over keys, 2: 128-row tiles
 };
 hipError_t launch_prefill(const PrefillProblem& p, hipStream_t stream);
 
@@ -78,8 +79,13 @@ hipError_t launch_prefill(const PrefillProblem& p, hipStream_t stream);
 hipError_t launch_precompute_freq(float* inv_freq, int d, float theta, hipStream_t stream);
 // mode bit 1: RMSNorm with weight; bit 2: RoPE at position = row / nums_head.
 enum RowOpMode : int { kRowNorm = 1, kRowRope = 2 };
+// RoPE angles come from `table` ([tokens][D/2] (cos, sin)) when non-null,
+// else from sincosf(token * inv_freq[i]).
 hipError_t launch_row_norm_rope(const uint16_t* in, uint16_t* out, const uint16_t* weight,
-                                const float* inv_freq, float eps, uint32_t num_tokens,
-                                uint32_t nums_head, uint32_t d, int mode, hipStream_t stream);
+                                const float* inv_freq, const float* table, float eps,
+                                uint32_t num_tokens, uint32_t nums_head, uint32_t d, int mode,
+                                hipStream_t stream);
+hipError_t launch_rope_table(float* table, const float* inv_freq, uint32_t num_pos, uint32_t d,
+                             hipStream_t stream);
 
 }  // namespace tiattn

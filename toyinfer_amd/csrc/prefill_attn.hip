@@ -77,22 +77,24 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, ui
                                              0x00020000);
 }
 
-__device__ __forceinline__ uint4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
-    return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
+// The whole byte offset goes in the VGPR operand (soffset = 0), so that the
+// hardware range check sees all of it and returns zeros past the end.
+__device__ __forceinline__ uint4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t voff) {
+    return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, 0, 0));
 }
 
-// Tile n0 of K and V into registers.  voff: this thread's byte offset of its
-// first chunk; soff: the tile's byte offset (n0 * row pitch).
+// Tile starting at byte `tile_off` of K and V into registers; voff is this
+// thread's byte offset of its first chunk within a tile.
 template <int D>
 __device__ __forceinline__ void load_tile(TileRegs<D>& r, __amdgpu_buffer_rsrc_t rk,
                                           __amdgpu_buffer_rsrc_t rv, uint32_t voff,
-                                          uint32_t row_bytes, uint32_t soff) {
+                                          uint32_t row_bytes, uint32_t tile_off) {
     using P = PfShape<D>;
 #pragma unroll
     for (int it = 0; it < P::LOADS; ++it) {
-        const uint32_t o = voff + it * P::ROWS_PER_LOAD * row_bytes;
-        r.k[it] = buf_load16(rk, o, soff);
-        r.v[it] = buf_load16(rv, o, soff);
+        const uint32_t o = tile_off + voff + it * P::ROWS_PER_LOAD * row_bytes;
+        r.k[it] = buf_load16(rk, o);
+        r.v[it] = buf_load16(rv, o);
     }
 }
 
@@ -145,12 +147,16 @@ __device__ __forceinline__ void load_q(bf16x8_t (&qf)[PfShape<D>::KSTEPS], const
             }
         ss += xor32(ss);
         const float inv = 1.0f / sqrtf(ss / (float)D + p.eps);
-        const float pos = (float)qq;
+        // (cos, sin) of this row's angles; rows past S read row S-1 (unused).
+        const float4* rope = reinterpret_cast<const float4*>(p.rope + (int64_t)qc * D);
         // Chunk ks (dims < D/2) pairs with chunk ks + KS/2 (dims + D/2).
 #pragma unroll
         for (int ks = 0; ks < KS / 2; ++ks) {
             const uint4 g_re = ldg16(p.q_gamma + ks * 16 + 8 * kg);
             const uint4 g_im = ldg16(p.q_gamma + (ks + KS / 2) * 16 + 8 * kg);
+            float4 cs4[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) cs4[e] = rope[(ks * 16 + 8 * kg) / 2 + e];
             uint32_t o_re[4], o_im[4];
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
@@ -165,8 +171,8 @@ __device__ __forceinline__ void load_q(bf16x8_t (&qf)[PfShape<D>::KSTEPS], const
                     const float gim = hlf ? bf16_hi(gi) : bf16_lo(gi);
                     const float re = bf16_lo(pack_bf16x2(xre * inv * gre, 0.0f));
                     const float im = bf16_lo(pack_bf16x2(xim * inv * gim, 0.0f));
-                    float sn, cs;
-                    sincosf(pos * p.inv_freq[ks * 16 + 8 * kg + 2 * e + hlf], &sn, &cs);
+                    const float cs = hlf ? cs4[e].z : cs4[e].x;
+                    const float sn = hlf ? cs4[e].w : cs4[e].y;
                     r2[hlf] = cs * re - sn * im;
                     i2[hlf] = cs * im + sn * re;
                 }
@@ -342,12 +348,238 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(PrefillProblem p
     }
 }
 
+// ---------------------------------------------------------------------------
+// Short-sequence variant: intra-workgroup split over keys.
+//
+// With few query tiles (S=1371 gives ceil(S/128) x Hq = 176 workgroups for
+// 256 CUs) the kernel above is bound by its longest workgroup, which walks
+// every key tile of the last rows alone.  Here a workgroup takes 32 query
+// rows of one head and its four waves split that row block's key tiles (32
+// keys each) round-robin; every wave streams its own tiles through a
+// private LDS region (register prefetch of its next tile, no barriers), and
+// the four partial (m, l, O) are merged through LDS at the end.
+constexpr int kSkBM = 32;
+constexpr int kSkBN = 32;
+
+template <int D>
+struct SkShape {
+    static constexpr int CPR = D / 8;
+    static constexpr int PK = D + 8;
+    static constexpr int PV = D + 32;
+    static constexpr int K_ELEMS = kSkBN * PK;
+    static constexpr int WAVE_ELEMS = kSkBN * PK + kSkBN * PV;
+    static constexpr int LOADS = kSkBN * D / 8 / 64;  // uint4 per lane per tile
+    static constexpr int ROWS_PER_LOAD = 64 / CPR;
+    static constexpr int KSTEPS = D / 16;
+    static constexpr int DBLK = D / 32;
+    static constexpr int OPITCH = D + 1;              // merge buffer pitch (floats)
+};
+
+template <int D, bool FUSED>
+__global__ __launch_bounds__(kPfThreads, 2) void prefill_splitkv_kernel(PrefillProblem p,
+                                                                        float scale_log2) {
+    using P = SkShape<D>;
+    constexpr int LDS_TILES = 4 * P::WAVE_ELEMS * 2;
+    constexpr int LDS_MERGE = 4 * kSkBM * P::OPITCH * 4;
+    static_assert(LDS_MERGE <= LDS_TILES, "merge buffer must fit in the tile buffers");
+    __shared__ __align__(16) unsigned char s_raw[LDS_TILES];
+    __shared__ float s_ml[4][kSkBM][2];
+
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int ql = lane & 31, kg = lane >> 5;
+    const uint32_t group = p.hq / p.hkv;
+    const uint32_t n_qt = (p.s + kSkBM - 1) / kSkBM;
+    const uint32_t bid = blockIdx.x;
+    const uint32_t kvh = bid % p.hkv;
+    const uint32_t r = bid / p.hkv;
+    const uint32_t h = kvh * group + r % group;
+    const uint32_t qt = n_qt - 1 - r / group;
+    const uint32_t q0 = qt * kSkBM;
+    const uint32_t qq = q0 + ql;
+    const uint32_t q_end = min(p.s, q0 + kSkBM);
+    const uint32_t n_tiles = (q_end + kSkBN - 1) / kSkBN;
+
+    bf16x8_t qf[P::KSTEPS];
+    load_q<D, FUSED>(qf, p, qq, h, kg);
+
+    const uint32_t row_bytes = p.hkv * D * 2;
+    const uint32_t kv_bytes = (p.s - 1) * row_bytes + D * 2;
+    const __amdgpu_buffer_rsrc_t rk = make_rsrc(p.k + (int64_t)kvh * D, kv_bytes);
+    const __amdgpu_buffer_rsrc_t rv = make_rsrc(p.v + (int64_t)kvh * D, kv_bytes);
+    const uint32_t voff = (lane / P::CPR) * row_bytes + (lane % P::CPR) * 16;
+    uint16_t* sk = reinterpret_cast<uint16_t*>(s_raw) + wave * P::WAVE_ELEMS;
+    uint16_t* sv = sk + P::K_ELEMS;
+
+    uint4 kreg[P::LOADS], vreg[P::LOADS];
+    auto load = [&](uint32_t t) {
+#pragma unroll
+        for (int it = 0; it < P::LOADS; ++it) {
+            const uint32_t o = t * kSkBN * row_bytes + voff + it * P::ROWS_PER_LOAD * row_bytes;
+            kreg[it] = buf_load16(rk, o);
+            vreg[it] = buf_load16(rv, o);
+        }
+    };
+
+    f32x16_t oacc[P::DBLK];
+#pragma unroll
+    for (int db = 0; db < P::DBLK; ++db)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) oacc[db][i] = 0.0f;
+    float m_run = -INFINITY, l_run = 0.0f;
+
+    uint32_t t = wave;
+    if (t < n_tiles) load(t);
+    for (; t < n_tiles; t += 4) {
+        {
+            const int row = lane / P::CPR, c = lane % P::CPR;
+#pragma unroll
+            for (int it = 0; it < P::LOADS; ++it) {
+                const int rr = row + it * P::ROWS_PER_LOAD;
+                *reinterpret_cast<uint4*>(sk + rr * P::PK + 8 * c) = kreg[it];
+                *reinterpret_cast<uint4*>(sv + rr * P::PV + 8 * c) = vreg[it];
+            }
+        }
+        if (t + 4 < n_tiles) load(t + 4);
+        const uint32_t n0 = t * kSkBN;
+        f32x16_t st;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) st[i] = 0.0f;
+        const uint16_t* ka = sk + ql * P::PK + 8 * kg;
+#pragma unroll
+        for (int ks = 0; ks < P::KSTEPS; ++ks)
+            st = mfma32x32x16(as_bf16x8(*reinterpret_cast<const uint4*>(ka + 16 * ks)), qf[ks], st);
+        if (n0 + kSkBN - 1 > q0) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const uint32_t key = n0 + 8 * (i / 4) + 4 * kg + (i % 4);
+                if (key > qq) st[i] = -INFINITY;
+            }
+        }
+        float m8[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) m8[i] = fmaxf(st[i], st[i + 8]);
+#pragma unroll
+        for (int w = 4; w >= 1; w >>= 1)
+#pragma unroll
+            for (int i = 0; i < w; ++i) m8[i] = fmaxf(m8[i], m8[i + w]);
+        const float mx = fmaxf(m8[0], xor32(m8[0]));
+        const float mt = mx * scale_log2;
+        const bool need = mt > m_run + kRescaleThreshold;
+        if (__any(need)) {
+            float alpha = 1.0f;
+            if (need) {
+                alpha = __builtin_amdgcn_exp2f(m_run - mt);
+                m_run = mt;
+            }
+            l_run *= alpha;
+#pragma unroll
+            for (int db = 0; db < P::DBLK; ++db)
+#pragma unroll
+                for (int i = 0; i < 16; ++i) oacc[db][i] *= alpha;
+        }
+        const float mref = m_run == -INFINITY ? 0.0f : m_run;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) st[i] = __builtin_amdgcn_exp2f(fmaf(st[i], scale_log2, -mref));
+        float r8[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) r8[i] = st[i] + st[i + 8];
+#pragma unroll
+        for (int w = 4; w >= 1; w >>= 1)
+#pragma unroll
+            for (int i = 0; i < w; ++i) r8[i] += r8[i + w];
+        l_run += r8[0];
+        bf16x8_t pf[2];
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt) {
+            const int o8 = 8 * tt;
+            pf[tt] = as_bf16x8(make_uint4(pack_bf16x2(st[o8 + 0], st[o8 + 1]),
+                                          pack_bf16x2(st[o8 + 2], st[o8 + 3]),
+                                          pack_bf16x2(st[o8 + 4], st[o8 + 5]),
+                                          pack_bf16x2(st[o8 + 6], st[o8 + 7])));
+        }
+        const int s16 = lane & 15, grp = lane >> 4;
+        const uint16_t* va = sv + (4 * kg + (s16 >> 2)) * P::PV + 16 * (grp & 1) + 4 * (s16 & 3);
+#pragma unroll
+        for (int db = 0; db < P::DBLK; ++db)
+#pragma unroll
+            for (int tt = 0; tt < 2; ++tt) {
+                const v4i16_t lo = ds_read_tr16(va + 16 * tt * P::PV + 32 * db);
+                const v4i16_t hi = ds_read_tr16(va + (16 * tt + 8) * P::PV + 32 * db);
+                const uint4 a = make_uint4(__builtin_bit_cast(uint2, lo).x, __builtin_bit_cast(uint2, lo).y,
+                                           __builtin_bit_cast(uint2, hi).x, __builtin_bit_cast(uint2, hi).y);
+                oacc[db] = mfma32x32x16(as_bf16x8(a), pf[tt], oacc[db]);
+            }
+    }
+
+    // Merge the four waves' partials of the 32 rows.
+    const float l_tot = l_run + xor32(l_run);
+    __syncthreads();  // all waves are done with their tile buffers
+    float* s_o = reinterpret_cast<float*>(s_raw);  // [wave][row][OPITCH]
+#pragma unroll
+    for (int db = 0; db < P::DBLK; ++db)
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+            s_o[(wave * kSkBM + ql) * P::OPITCH + db * 32 + 8 * (i / 4) + 4 * kg + (i % 4)] = oacc[db][i];
+    if (kg == 0) {
+        s_ml[wave][ql][0] = m_run;
+        s_ml[wave][ql][1] = l_tot;
+    }
+    __syncthreads();
+    constexpr int PER = D / 8;  // dims per thread in the final pass
+    const int row = threadIdx.x >> 3, part = threadIdx.x & 7;
+    const uint32_t orow_q = q0 + row;
+    if (orow_q < p.s) {
+        float M = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) M = fmaxf(M, s_ml[w][row][0]);
+        float wgt[4], den = 0.0f;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+            const float mw = s_ml[w][row][0];
+            wgt[w] = mw == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mw - M);
+            den = fmaf(wgt[w], s_ml[w][row][1], den);
+        }
+        const float inv = 1.0f / den;
+        uint16_t* orow = p.o + ((int64_t)orow_q * p.hq + h) * D + part * PER;
+#pragma unroll
+        for (int e = 0; e < PER; e += 8) {
+            uint32_t w4[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                float v2[2];
+#pragma unroll
+                for (int u = 0; u < 2; ++u) {
+                    const int d = part * PER + e + 2 * j + u;
+                    float o = 0.0f;
+#pragma unroll
+                    for (int w = 0; w < 4; ++w)
+                        o = wgt[w] != 0.0f ? fmaf(wgt[w], s_o[(w * kSkBM + row) * P::OPITCH + d], o) : o;
+                    v2[u] = o * inv;
+                }
+                w4[j] = pack_bf16x2(v2[0], v2[1]);
+            }
+            *reinterpret_cast<uint4*>(orow + e) = make_uint4(w4[0], w4[1], w4[2], w4[3]);
+        }
+    }
+}
+
+// Below this many 128-row workgroups the split-over-keys variant wins: the
+// 128-row kernel would leave CUs idle and be bound by its longest tile walk.
+constexpr uint32_t kSplitKvBelowWgs = 257;
+
 template <int D, bool FUSED>
 hipError_t launch_t(const PrefillProblem& p, hipStream_t st) {
     const uint32_t n_qtiles = (p.s + kPfBM - 1) / kPfBM;
-    const dim3 grid(n_qtiles * p.hq);
     const float sl2 = kLog2e / sqrtf((float)D);
-    hipLaunchKernelGGL((prefill_kernel<D, FUSED>), grid, dim3(kPfThreads), 0, st, p, sl2);
+    const bool split = p.variant == 1 || (p.variant == 0 && n_qtiles * p.hq < kSplitKvBelowWgs);
+    if (split) {
+        const dim3 grid(((p.s + kSkBM - 1) / kSkBM) * p.hq);
+        hipLaunchKernelGGL((prefill_splitkv_kernel<D, FUSED>), grid, dim3(kPfThreads), 0, st, p,
+                           sl2);
+    } else {
+        const dim3 grid(n_qtiles * p.hq);
+        hipLaunchKernelGGL((prefill_kernel<D, FUSED>), grid, dim3(kPfThreads), 0, st, p, sl2);
+    }
     return hipGetLastError();
 }
 

@@ -1,0 +1,173 @@
+"""Host-side checks that need no GPU: the C ABI library loads and exports
+every declared entry point, argument validation happens on the host with
+the documented status codes, workspace sizing, the synthetic generator, and
+bench.py's single-GPU contract."""
+import ctypes
+import json
+import os
+import re
+import subprocess
+import sys
+
+import numpy as np
+import pytest
+
+from toyinfer_amd import attn, synth
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "toyinfer_attn.h")
+L = attn.LIB
+P = 0x10000  # a 256-byte aligned stand-in address; never dereferenced here
+INVALID, UNSUPPORTED, WORKSPACE = (attn.ERR_INVALID_ARGUMENT, attn.ERR_UNSUPPORTED,
+                                   attn.ERR_WORKSPACE)
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(toyinfer_\w+)\s*\(", text)))
+
+
+def test_every_declared_function_is_exported_and_bound():
+    names = declared_functions()
+    assert len(names) >= 15
+    out = subprocess.run(["nm", "-D", "--defined-only", attn.LIB_PATH], capture_output=True,
+                         text=True, check=True).stdout
+    exported = set(re.findall(r"\bT (toyinfer_\w+)", out))
+    assert set(names) <= exported, set(names) - exported
+    assert set(names) == set(attn.SIGNATURES), set(names) ^ set(attn.SIGNATURES)
+
+
+def test_abi_version_and_status_strings():
+    assert L.toyinfer_abi_version() == 1
+    assert attn.status_string(0) == "ok"
+    for st in (INVALID, UNSUPPORTED, WORKSPACE, attn.ERR_HIP):
+        assert attn.status_string(st) not in ("ok", "unknown status")
+
+
+def flash(q=P, k=P, v=P, o=P, hq=16, hkv=8, d=128, s=100, algo=0):
+    return L.toyinfer_flash_attention_algo_bf16(q, k, v, o, hq, hkv, d, s, algo, None)
+
+
+def test_prefill_argument_validation():
+    assert flash(hkv=3) == INVALID                 # Hq % Hkv != 0
+    assert flash(hq=0) == INVALID
+    assert flash(d=96) == UNSUPPORTED              # the reference instantiates 64 and 128 only
+    assert flash(s=0) == INVALID
+    assert flash(q=None) == INVALID
+    assert flash(k=P + 2) == INVALID               # 16-byte alignment
+    assert flash(algo=3) == INVALID
+    assert flash(s=1 << 30) == UNSUPPORTED         # K/V rows beyond 32-bit byte offsets
+    assert L.toyinfer_flash_attention_v1_bf16(P, P, P, P, 8, 3, 128, 4, None) == INVALID
+
+
+def test_fused_prefill_argument_validation():
+    f = L.toyinfer_prefill_qknorm_rope_attention_bf16
+    assert f(P, P, P, P, P, P, P, None, 1e-6, 32, 8, 128, 64, None) == INVALID   # no rope table
+    assert f(P, P, P, P, P, P, P, P + 8, 1e-6, 32, 8, 128, 64, None) == INVALID  # table alignment
+    assert f(P, P, P, P, None, P, P, P, 1e-6, 32, 8, 128, 64, None) == INVALID   # no K_out
+    assert f(P, P, P, P, P, P, P, P, 1e-6, 32, 8, 64 + 32, 64, None) == UNSUPPORTED
+
+
+def test_decode_reference_contract_validation():
+    f = L.toyinfer_attention_bf16
+    assert f(P, P, P, P, P, P, 32, 8, 128, 40, 40, None) == INVALID     # pos >= max_seq_len
+    assert f(P, P, P, P, P, P, 32, 8, 128, 0, 0, None) == INVALID       # empty cache
+    assert f(P, P, P, None, P, P, 32, 8, 128, 3, 40, None) == INVALID   # no score buffer
+    assert f(P, P, P, P, P, P, 32, 6, 128, 3, 40, None) == INVALID
+    g = L.toyinfer_attention_bf16_graph
+    assert g(P, P, P, P, P, P, 32, 8, 128, None, 40, None) == INVALID   # no device pos
+    assert g(P, P, P, P, P, P, 32, 8, 128, P + 2, 40, None) == INVALID
+
+
+def test_batched_decode_validation_and_workspace():
+    f = L.toyinfer_decode_attention_bf16
+    ws = L.toyinfer_decode_workspace_bytes(8, 32, 128, 12)
+    heads = 8 * 32
+    assert ws == ((heads * 12 * 2 * 4 + 255) // 256) * 256 + heads * 12 * 128 * 4
+    args = dict(q=P, k=P, v=P, o=P, b=8, hq=32, hkv=8, d=128, lens=None, L=4096,
+                stride=4096 * 8 * 128, splits=12, w=P, wb=ws)
+
+    def call(**kw):
+        a = dict(args, **kw)
+        return f(a["q"], a["k"], a["v"], a["o"], a["b"], a["hq"], a["hkv"], a["d"], a["lens"],
+                 a["L"], a["stride"], a["splits"], a["w"], a["wb"], None)
+
+    assert call(wb=ws - 1) == WORKSPACE
+    assert call(b=0) == INVALID
+    assert call(L=0) == INVALID
+    assert call(stride=4095 * 8 * 128) == INVALID   # sequences would overlap
+    assert call(splits=1025) == INVALID
+    assert call(w=P + 64) == INVALID                # workspace 256-byte alignment
+    assert call(lens=P + 1) == INVALID
+    assert call(d=80) == UNSUPPORTED
+
+
+def test_default_split_counts_are_bounded():
+    for b, hq, hkv, L_ in [(8, 32, 8, 4096), (1, 32, 8, 32768), (1, 16, 8, 100), (3, 6, 3, 1)]:
+        s = L.toyinfer_decode_default_splits(b, hq, hkv, 128, L_)
+        assert 1 <= s <= max(1, -(-L_ // 128)) and s <= 1024
+
+
+def test_prologue_op_validation():
+    assert L.toyinfer_precompute_freq_f32(P, 127, 1e6, None) == INVALID
+    assert L.toyinfer_precompute_freq_f32(None, 128, 1e6, None) == INVALID
+    assert L.toyinfer_rope_cos_sin_f32(P, P, 0, 128, None) == INVALID
+    assert L.toyinfer_batch_rope_bf16(P, None, 4, 8, 128, None) == INVALID
+    assert L.toyinfer_batch_multi_rmsnorm_bf16(P, None, P, 1e-6, 4, 8, 128, None) == INVALID
+    assert L.toyinfer_batch_multi_rmsnorm_bf16(P, P, P, 1e-6, 0, 8, 128, None) == INVALID
+    assert L.toyinfer_multi_rmsnorm_bf16(P, P, P, 1e-6, 8, 96, None) == UNSUPPORTED
+
+
+def test_python_wrapper_raises_on_bad_status():
+    class Fake:
+        def __init__(self, addr):
+            self.addr = addr
+
+        def data_ptr(self):
+            return self.addr
+
+    with pytest.raises(attn.ToyInferError) as e:
+        attn.flash_attention_v1_bf16(Fake(P), Fake(P), Fake(P), Fake(P), 4, 3, 128, 8, stream=0)
+    assert e.value.status == INVALID
+
+
+# ------------------------------------------------------ synthetic inputs
+
+def test_generator_c_matches_numpy_specification():
+    for seed, name, n in [(1, "q", 100003), (2026, "k", 4097), (7, "v", 1), (2 ** 63 + 9, "x", 2)]:
+        assert np.array_equal(synth.normal_bf16(seed, name, (n,), use_c=True),
+                              synth.normal_bf16(seed, name, (n,), use_c=False))
+        assert np.array_equal(synth.uniform_bf16(seed, name, (n,), 0.9, 1.1, use_c=True),
+                              synth.uniform_bf16(seed, name, (n,), 0.9, 1.1, use_c=False))
+
+
+def test_generator_pinned_values_and_statistics():
+    assert synth.normal_bf16(2026, "q", (8,)).tolist() == [16346, 16293, 49012, 49049, 49147,
+                                                            16008, 16289, 48714]
+    assert synth.uniform_bf16(2026, "gamma_q", (4,), 0.9, 1.1).tolist() == [16268, 16257,
+                                                                            16267, 16267]
+    z = synth.bf16_bits_to_f32(synth.normal_bf16(3, "stats", (1 << 20,))).astype(np.float64)
+    assert abs(z.mean()) < 5e-3 and abs(z.std() - 1) < 5e-3
+    assert abs((np.abs(z) > 1.96).mean() - 0.05) < 2e-3
+    u = synth.bf16_bits_to_f32(synth.uniform_bf16(3, "u", (1 << 16,), 0.9, 1.1))
+    assert u.min() >= 0.9 - 1e-2 and u.max() <= 1.1 + 1e-2
+
+
+def test_generator_ln_and_sincos_accuracy():
+    u = np.linspace(1e-12, 1.0, 200001)
+    assert np.abs(synth._ln(u) - np.log(u)).max() < 1e-14
+    w = np.linspace(0, 1, 200001, endpoint=False)
+    s, c = synth._sincos_2pi(w)
+    assert np.abs(s - np.sin(2 * np.pi * w)).max() < 1e-14
+    assert np.abs(c - np.cos(2 * np.pi * w)).max() < 1e-14
+
+
+# --------------------------------------------------------------- bench.py
+
+def test_bench_refuses_more_than_one_gpu():
+    res = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--gpus", "2"],
+                         capture_output=True, text=True, timeout=300)
+    assert res.returncode != 0
+    msg = json.loads(res.stdout.strip().splitlines()[-1])
+    assert "one GPU" in msg["error"]

@@ -1,0 +1,322 @@
+"""Pins the CPU oracle (oracle/) on the CPU, before it is trusted as the checker.
+
+Each oracle function is checked against something other than its own
+formula: the golden fixtures (torch float64, tests/golden/make_golden.py),
+closed forms, invariants, brute force in numpy float64, torch's SDPA, and
+the literal cases held by the reference's own tests.
+"""
+import hashlib
+import os
+
+import numpy as np
+import pytest
+
+import oracle
+from tests import helpers as H
+from toyinfer_amd import synth
+
+GOLD = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+def gold(name):
+    return np.load(os.path.join(GOLD, name + ".npz"))
+
+
+def sha(*arrays):
+    h = hashlib.sha256()
+    for a in arrays:
+        h.update(np.ascontiguousarray(a).tobytes())
+    return h.hexdigest()
+
+
+def bf16_ulp_diff(a_bits, b_bits):
+    """|a - b| in units of one bf16 ulp at the larger magnitude (2^-7 relative
+    upper bound), with differences under 1e-6 absolute counted as 0."""
+    a, b = H.bf16_bits_to_f32(a_bits), H.bf16_bits_to_f32(b_bits)
+    diff = np.abs(a.astype(np.float64) - b)
+    ulp = np.maximum(np.abs(a), np.abs(b)).astype(np.float64) * 2.0 ** -7
+    return np.where(diff <= 1e-6, 0, np.ceil(diff / np.maximum(ulp, 1e-30))).astype(np.int64)
+
+
+# ------------------------------------------------------------------ bf16
+
+def test_bf16_rounding_matches_torch():
+    torch = pytest.importorskip("torch")
+    rng = np.random.default_rng(0)
+    specials = np.array([0.0, -0.0, 1.0, -1.0, 1.0 + 2 ** -8, 1.0 + 3 * 2 ** -8, 1.0 + 2 ** -9,
+                         1.0 + 2 ** -9 + 2 ** -20, 3.0e38, 3.4028235e38, 1e-40, -1e-42,
+                         np.inf, -np.inf, 65504.0, 1e-30], np.float32)
+    ties = (np.arange(1 << 16, dtype=np.uint32) << 16 | 0x8000).view(np.float32)  # exact ties
+    vals = np.concatenate([specials, ties[np.isfinite(ties)],
+                           rng.standard_normal(200000).astype(np.float32) * 10 ** rng.uniform(
+                               -30, 30, 200000).astype(np.float32)])
+    ours = oracle.f32_to_bf16(vals)
+    ref = torch.from_numpy(vals).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(ours, ref)
+    nan = oracle.f32_to_bf16(np.array([np.nan, -np.nan], np.float32))
+    assert np.all((nan & 0x7F80) == 0x7F80) and np.all(nan & 0x7F)
+    assert np.array_equal(synth.f32_to_bf16_bits(vals), ours)
+
+
+# --------------------------------------------------------------- prefill
+
+PREFILL_CASES = ["seq1_gqa", "exact_kv_tile", "gqa_tail_tiles", "multi_kv_tile",
+                 "large_magnitude", "causal_focus"]
+
+
+@pytest.mark.parametrize("name", PREFILL_CASES)
+def test_flash_vs_golden(name):
+    g = gold("prefill_" + name)
+    o = oracle.flash_reference(g["q"], g["k"], g["v"])
+    scale = max(1.0, float(np.abs(g["o"]).max()))
+    assert np.abs(o - g["o"]).max() <= 2e-6 * scale
+    ulps = bf16_ulp_diff(oracle.f32_to_bf16(o), g["o_bf16"])
+    assert ulps.max() <= 1 and (ulps > 0).mean() < 1e-3
+
+
+def test_case_generators_reproduce_golden_inputs():
+    """The restated case formulas give the inputs the fixtures were made from."""
+    q, k, v = oracle.make_flash_case(6, 3, 128, 65, 0.028, 0.019)
+    g = gold("prefill_multi_kv_tile")
+    assert np.array_equal(oracle.f32_to_bf16(q), g["q"])
+    assert np.array_equal(oracle.f32_to_bf16(k), g["k"])
+    assert np.array_equal(oracle.f32_to_bf16(v), g["v"])
+
+
+def test_flash_config1_vs_golden():
+    g = gold("prefill_config1")
+    qb = synth.normal_bf16(int(g["seed"]), "q", (128, 16, 128))
+    kb = synth.normal_bf16(int(g["seed"]), "k", (128, 8, 128))
+    vb = synth.normal_bf16(int(g["seed"]), "v", (128, 8, 128))
+    assert sha(qb, kb, vb) == str(g["inputs_sha256"]), "synthetic generator drifted"
+    ulps = bf16_ulp_diff(oracle.f32_to_bf16(oracle.flash_reference(qb, kb, vb)), g["o_bf16"])
+    assert ulps.max() <= 1 and (ulps > 0).mean() < 1e-3
+
+
+def test_flash_matches_torch_sdpa():
+    torch = pytest.importorskip("torch")
+    rng = np.random.default_rng(1)
+    s, hq, hkv, d = 50, 6, 2, 64
+    q, k, v = (oracle.round_bf16(rng.standard_normal(sh).astype(np.float32))
+               for sh in [(s, hq, d), (s, hkv, d), (s, hkv, d)])
+    ours = oracle.flash_reference(q, k, v)
+    tq = torch.from_numpy(q).double().permute(1, 0, 2)
+    tk = torch.from_numpy(k).double().repeat_interleave(3, 1).permute(1, 0, 2)
+    tv = torch.from_numpy(v).double().repeat_interleave(3, 1).permute(1, 0, 2)
+    ref = torch.nn.functional.scaled_dot_product_attention(tq, tk, tv, is_causal=True)
+    assert np.abs(ours - ref.permute(1, 0, 2).numpy()).max() < 2e-6
+
+
+def test_flash_brute_force_tiny():
+    rng = np.random.default_rng(2)
+    s, hq, hkv, d = 7, 4, 2, 8
+    q, k, v = (rng.standard_normal(sh).astype(np.float32) for sh in
+               [(s, hq, d), (s, hkv, d), (s, hkv, d)])
+    ours = oracle.flash_reference(q, k, v)
+    for t in range(s):
+        for h in range(hq):
+            kv = h // 2
+            sc = np.array([np.dot(q[t, h].astype(np.float64), k[j, kv]) for j in range(t + 1)])
+            w = np.exp(sc / np.sqrt(d) - (sc / np.sqrt(d)).max())
+            w /= w.sum()
+            exp = (w[:, None] * v[: t + 1, kv].astype(np.float64)).sum(0)
+            assert np.abs(ours[t, h] - exp).max() < 1e-6
+
+
+def test_flash_row0_is_v0_and_constant_keys_give_prefix_mean():
+    rng = np.random.default_rng(3)
+    s, hq, hkv, d = 40, 4, 2, 32
+    q = rng.standard_normal((s, hq, d)).astype(np.float32)
+    v = rng.standard_normal((s, hkv, d)).astype(np.float32)
+    k = np.repeat(rng.standard_normal((1, hkv, d)).astype(np.float32), s, 0)
+    o = oracle.flash_reference(q, k, v)
+    assert np.array_equal(o[0], np.repeat(v[0], 2, 0))
+    prefix_mean = np.cumsum(v.astype(np.float64), 0) / np.arange(1, s + 1)[:, None, None]
+    assert np.abs(o - np.repeat(prefix_mean, 2, 1)).max() < 1e-5
+
+
+def test_flash_dominant_key_selects_its_value():
+    s, hq, hkv, d = 12, 2, 1, 16
+    q = np.zeros((s, hq, d), np.float32)
+    q[:, :, 0] = 40.0
+    k = np.zeros((s, hkv, d), np.float32)
+    k[:, 0, 0] = np.arange(s, dtype=np.float32)    # score grows by 40/4 per key
+    v = np.random.default_rng(4).standard_normal((s, hkv, d)).astype(np.float32)
+    o = oracle.flash_reference(q, k, v)
+    # query t sees keys 0..t; key t wins by >= 10 nats over key t-1
+    assert np.abs(o[:, 0] - v[:, 0]).max() < 1e-3
+
+
+def test_flash_gqa_equals_mha_and_shift_invariance():
+    rng = np.random.default_rng(5)
+    s, hq, hkv, d = 30, 8, 2, 64
+    q, k, v = (rng.standard_normal(sh).astype(np.float32) for sh in
+               [(s, hq, d), (s, hkv, d), (s, hkv, d)])
+    a = oracle.flash_reference(q, k, v)
+    b = oracle.flash_reference(q, np.repeat(k, 4, 1), np.repeat(v, 4, 1))
+    assert np.array_equal(a, b)
+    u = rng.standard_normal((1, hkv, d)).astype(np.float32)  # adds q.u to every score of q
+    c = oracle.flash_reference(q, k + u, v)
+    assert np.abs(a - c).max() < 1e-5
+
+
+def test_flash_row_subset_matches_full():
+    rng = np.random.default_rng(6)
+    s, hq, hkv, d = 90, 4, 1, 32
+    q, k, v = (rng.standard_normal(sh).astype(np.float32) for sh in
+               [(s, hq, d), (s, hkv, d), (s, hkv, d)])
+    full = oracle.flash_reference(q, k, v)
+    rows = [0, 5, 61, 89]
+    part = oracle.flash_reference(q, k, v, rows=rows)
+    assert np.array_equal(part[rows], full[rows])
+    assert np.isnan(part[1]).all()
+
+
+# ---------------------------------------------------------------- decode
+
+@pytest.mark.parametrize("name", ["pos0_gqa", "full_kv", "tiled_seq"])
+def test_decode_vs_golden(name):
+    g = gold("decode_" + name)
+    q, k, v = (oracle.bf16_to_f32(g[x]) for x in "qkv")
+    pos, msl = int(g["pos"]), g["score"].shape[1]
+    score, ob, o = oracle.decode_attention(q, k, v, pos, msl)
+    assert np.abs(score - g["score"]).max() < 1e-6
+    assert np.all(score[:, pos + 1:] == 0)
+    assert np.abs(ob - g["o"]).max() < 2e-6
+    ulps = bf16_ulp_diff(o, g["o_bf16"])
+    assert ulps.max() <= 1
+
+
+def test_decode_batched_vs_golden():
+    g = gold("decode_seeded")
+    sd = int(g["seed"])
+    qb = synth.normal_bf16(sd, "q", (2, 8, 128))
+    kb = synth.normal_bf16(sd, "k", (2, 300, 2, 128))
+    vb = synth.normal_bf16(sd, "v", (2, 300, 2, 128))
+    assert sha(qb, kb, vb) == str(g["inputs_sha256"])
+    o = oracle.decode_batched(qb, kb, vb, g["lens"])
+    assert np.abs(o - g["o"]).max() < 2e-6
+
+
+def test_softmax_reference_literal_cases():
+    """tests/test_softmax_f32_kernel.cu:42-60, against scipy in float64."""
+    from scipy.special import softmax
+
+    rng_i = np.arange(24)
+    mixed = (-2.5 + 0.37 * np.sin((rng_i + 1) * 0.19) + 0.11 * (rng_i % 7)).astype(np.float32)
+    cases = [(2, 0, 5, np.array([1.25, -9.0, 3.0, 4.0, -2.0, -0.5, 7.0, -1.0, 2.0, 3.0],
+                                np.float32)),
+             (3, 5, 8, mixed),
+             (2, 4, 7, np.array([80.0, 81.5, 79.25, 90.0, 88.0, -3.0, 4.0, -45.0, -44.5, -46.25,
+                                 -41.0, -42.0, 6.0, -7.0], np.float32))]
+    for hq, pos, msl, sc in cases:
+        sc = sc.reshape(hq, msl)
+        out = oracle.decode_softmax(sc, pos)
+        exp = softmax(sc[:, : pos + 1].astype(np.float64), axis=1)
+        assert np.abs(out[:, : pos + 1] - exp).max() < 1e-6
+        assert np.array_equal(out[:, pos + 1:], sc[:, pos + 1:])
+        assert np.abs(out[:, : pos + 1].sum(1) - 1).max() < 1e-6
+
+
+def test_decode_qk_accumulates_onto_initial_score():
+    """tests/test_gqa_qk_gemv_bf16_kernel.cu:25-31: scores add onto a dirty buffer."""
+    q, k, _ = oracle.make_attention_case(8, 2, 128, 12, 0.03, 0.017)
+    q, k = oracle.round_bf16(q), oracle.round_bf16(k)
+    init = (-0.45 + 0.03 * ((np.arange(8 * 12) * 7) % 13)).astype(np.float32).reshape(8, 12)
+    out = oracle.decode_qk_scores(q, k, init, 9, 12)
+    exp = init.astype(np.float64).copy()
+    for h in range(8):
+        for t in range(10):
+            exp[h, t] += np.dot(q[h].astype(np.float64), k[t, h // 4]) / np.sqrt(128)
+    assert np.abs(out - exp).max() < 1e-5
+
+
+def test_decode_apply_accumulates_onto_initial_o():
+    """tests/test_apply_score2v_f32_kernel.cu:59-75 (single-tile case)."""
+    _, _, v = oracle.make_attention_case(4, 2, 64, 8, 0.04, 0.02)
+    v = oracle.round_bf16(v)
+    score = np.zeros((4, 8), np.float32)
+    for h in range(4):
+        for t in range(4):
+            score[h, t] = 0.12 + 0.03 * ((h + t) % 5)
+    init = (0.6 - 0.04 * ((np.arange(4 * 64) * 3) % 17)).astype(np.float32).reshape(4, 64)
+    out = oracle.decode_apply(score, v, init, 3)
+    exp = init.astype(np.float64) + np.einsum("ht,thd->hd", score[:, :4].astype(np.float64),
+                                              np.repeat(v[:4], 2, 1).astype(np.float64))
+    assert np.abs(out - exp).max() < 1e-5
+
+
+def test_decode_equals_last_prefill_row_and_is_permutation_invariant():
+    rng = np.random.default_rng(7)
+    L, hq, hkv, d = 60, 8, 2, 64
+    q = oracle.round_bf16(rng.standard_normal((L, hq, d)).astype(np.float32))
+    k = oracle.round_bf16(rng.standard_normal((L, hkv, d)).astype(np.float32))
+    v = oracle.round_bf16(rng.standard_normal((L, hkv, d)).astype(np.float32))
+    pre = oracle.flash_reference(q, k, v)[L - 1]
+    _, ob, _ = oracle.decode_attention(q[L - 1], k, v, L - 1, L)
+    assert np.abs(pre - ob).max() < 1e-5
+    perm = rng.permutation(L)
+    _, obp, _ = oracle.decode_attention(q[L - 1], k[perm], v[perm], L - 1, L)
+    assert np.abs(ob - obp).max() < 1e-5
+
+
+# ------------------------------------------------ QK-norm, RoPE, inv_freq
+
+def test_inv_freq_closed_forms():
+    f = oracle.inv_freq(128, 1e6)
+    assert f[0] == 1.0
+    exp = 1.0 / np.power(1e6, 2.0 * np.arange(64) / 128)
+    assert np.abs(f / exp - 1).max() < 1e-6
+    assert np.all(oracle.inv_freq(258, 1.0) == 1.0)      # theta 1 (reference case)
+    assert np.allclose(oracle.inv_freq(2, 2.0), [1.0])
+
+
+def test_rmsnorm_constant_row_and_vs_float64():
+    w = oracle.round_bf16(np.linspace(0.9, 1.1, 64).astype(np.float32))
+    x = np.full(64, -0.75, np.float32)
+    y = oracle.multi_rmsnorm(x, w, 64, 1e-6)
+    assert np.abs(y - oracle.round_bf16(-w / np.sqrt(1 + 1e-6 / 0.5625))).max() == 0
+    x, w = oracle.make_rmsnorm_case(4, 128, 4 * 128, 0.09, 0.05)
+    xq, wq = oracle.round_bf16(x), oracle.round_bf16(w)
+    y = oracle.multi_rmsnorm(xq, wq, 128, 1e-5).reshape(4, 128)
+    x64 = xq.reshape(4, 128).astype(np.float64)
+    exp = x64 / np.sqrt((x64 ** 2).mean(1, keepdims=True) + 1e-5) * wq
+    ulps = bf16_ulp_diff(oracle.f32_to_bf16(y), oracle.f32_to_bf16(exp.astype(np.float32)))
+    assert ulps.max() <= 1
+
+
+def test_rope_position0_identity_and_vs_float64():
+    qk, f = oracle.make_rope_case(4, 128, 4 * 128, 0.021, 0.0)
+    f = oracle.inv_freq(128, 10000.0)
+    x = oracle.round_bf16(qk).reshape(1, 4, 128)
+    assert np.array_equal(oracle.rope(x, f, 1, 4, 128), x)
+    x5 = np.repeat(x, 37, 0)
+    out = oracle.rope(x5, f, 37, 4, 128)
+    ang = (np.arange(37, dtype=np.float32)[:, None] * f[None, :]).astype(np.float64)
+    c, s = np.cos(ang)[:, None, :], np.sin(ang)[:, None, :]
+    re, im = x5[..., :64].astype(np.float64), x5[..., 64:].astype(np.float64)
+    exp = np.concatenate([re * c - im * s, im * c + re * s], -1).astype(np.float32)
+    assert bf16_ulp_diff(oracle.f32_to_bf16(out), oracle.f32_to_bf16(exp)).max() <= 1
+
+
+def test_qk_norm_rope_and_fused_attention_vs_golden():
+    g = gold("fused_small")
+    sd = int(g["seed"])
+    s, hq, hkv, d = 96, 4, 2, 128
+    qb = synth.normal_bf16(sd, "q", (s, hq, d))
+    kb = synth.normal_bf16(sd, "k", (s, hkv, d))
+    vb = synth.normal_bf16(sd, "v", (s, hkv, d))
+    gq = synth.uniform_bf16(sd, "gamma_q", (d,), 0.9, 1.1)
+    gk = synth.uniform_bf16(sd, "gamma_k", (d,), 0.9, 1.1)
+    assert sha(qb, kb, vb, gq, gk) == str(g["inputs_sha256"])
+    f = oracle.inv_freq(d, float(g["theta"]))
+    kn = oracle.qk_norm_rope(oracle.bf16_to_f32(kb), oracle.bf16_to_f32(gk), f, float(g["eps"]))
+    qn = oracle.qk_norm_rope(oracle.bf16_to_f32(qb), oracle.bf16_to_f32(gq), f, float(g["eps"]))
+    # A 1-ulp difference after the norm's rounding (float32 vs float64 sums)
+    # enters both inputs of a rotation, so 2 ulps can appear after RoPE.
+    for ours, ref in [(kn, g["k_norm_rope"]), (qn, g["q_norm_rope"])]:
+        ulps = bf16_ulp_diff(oracle.f32_to_bf16(ours), ref)
+        assert ulps.max() <= 2 and (ulps > 0).mean() < 5e-3
+    o = oracle.round_bf16(oracle.flash_reference(qn, kn, oracle.bf16_to_f32(vb)))
+    H.check_bar(o, H.bf16_bits_to_f32(g["o_bf16"]), "fused oracle vs golden",
+                max_abs=1e-2, mean_abs=2e-4)

@@ -38,6 +38,23 @@ METRIC = "prefill attn TFLOP/s + decode attn HBM GB/s (% MI355X roofline), Qwen3
 PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
 PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
 SEED = 2026
+# HBM bytes per launch of each workload's dominant kernel: rocprofv3 --pmc
+# FETCH_SIZE and WRITE_SIZE passes (KiB per dispatch) over
+# `bench.py --workload <name>`, scaled by what the same counters read for a
+# 256 MiB device-to-device copy (reads x2.0, writes x1.0); the summaries are
+# under profiles/.  (read KiB, write KiB) as the counters report them.
+PMC_KIB = {"prefill": (5555.6, 5484.0),            # prefill_splitkv_kernel<128,false>
+           "prefill_fused": (98220.4, 65538.7),    # prefill_kernel<128,true>
+           "decode_b8_l4096": (65880.1, 1508.3),   # decode_split_kernel<128>
+           "decode_b1_l32768": (65648.6, 1476.3)}  # decode_split_kernel<128>
+FETCH_SCALE, WRITE_SCALE = 2.0, 1.0
+
+
+def traffic_bytes(workload):
+    r, w = PMC_KIB[workload]
+    return int(round((r * FETCH_SCALE + w * WRITE_SCALE) * 1024))
+WORKLOADS = ("all", "prefill", "prefill_fused", "decode_b8_l4096", "decode_b1_l32768",
+             "copy_calibration")
 
 
 def causal_flops(s, hq, d):
@@ -54,6 +71,9 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the cpu_baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="target CPU time of the cpu_baseline sample")
+    ap.add_argument("--workload", default="all", choices=WORKLOADS,
+                    help="profiling aid: run one workload alone and print its own JSON "
+                         "(the default 'all' prints the benchmark line)")
     return ap.parse_args()
 
 
@@ -141,7 +161,8 @@ def bench_prefill_fused(dev, stream, steps, warmup, s=8192, hq=32, hkv=8, d=128)
             "entry": "toyinfer_prefill_qknorm_rope_attention_bf16", "steps": steps,
             "ms_per_step": round(ms, 5), "value": round(tflops, 2), "unit": "TFLOP/s",
             "note": "time includes the K norm+RoPE pre-pass; FLOPs count attention only",
-            "roofline": roofline("mfma", tflops, PEAK_BF16_TFLOPS, "TFLOP/s")}
+            "roofline": roofline("mfma", tflops, PEAK_BF16_TFLOPS, "TFLOP/s",
+                                 traffic_bytes("prefill_fused"))}
 
 
 # ------------------------------------------------------------------- decode
@@ -175,7 +196,23 @@ def bench_decode(dev, stream, steps, warmup, b, L, hq=32, hkv=8, d=128, sets=4):
             "ms_per_step": round(ms, 5), "value": round(gbs, 1), "unit": "GB/s",
             "note": "KV bytes read per step / step time (split + combine kernels); "
                     f"{sets} rotating KV sets defeat the Infinity Cache",
-            "roofline": roofline("hbm", gbs, PEAK_HBM_GBS, "GB/s")}
+            "roofline": roofline("hbm", gbs, PEAK_HBM_GBS, "GB/s",
+                                 traffic_bytes(f"decode_b{b}_l{L}"))}
+
+
+def bench_copy(dev, stream, steps, warmup, mib=256):
+    """Device-to-device copy of `mib` MiB: a kernel with known HBM traffic (mib
+    read + mib written per launch), the scale for the FETCH_SIZE / WRITE_SIZE
+    counters of the attention kernels."""
+    import torch
+
+    x = torch.ones(mib << 18, dtype=torch.float32, device=dev)
+    y = torch.empty_like(x)
+    ms = time_steps(lambda i: y.copy_(x), steps, warmup, stream)
+    nbytes = 2.0 * (mib << 20)
+    return {"workload": f"copy_{mib}MiB", "steps": steps, "ms_per_step": round(ms, 5),
+            "value": round(nbytes / (ms * 1e-3) / 1e9, 1), "unit": "GB/s",
+            "note": "read + write bytes / step time"}
 
 
 # ------------------------------------------------------------- CPU baseline
@@ -220,6 +257,19 @@ def main():
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     stream = torch.cuda.Stream(device=dev)
+    if args.workload != "all":
+        one = {"prefill": lambda: dict(zip(("ms_per_step", "value"),
+                                           bench_prefill(dev, stream, args.steps, args.warmup)[:2]),
+                                       workload="prefill_causal_gqa_s1371_hq16_hkv8_d128",
+                                       unit="TFLOP/s"),
+               "prefill_fused": lambda: bench_prefill_fused(dev, stream, args.steps, args.warmup),
+               "decode_b8_l4096": lambda: bench_decode(dev, stream, args.steps, args.warmup,
+                                                       b=8, L=4096),
+               "decode_b1_l32768": lambda: bench_decode(dev, stream, args.steps, args.warmup,
+                                                        b=1, L=32768),
+               "copy_calibration": lambda: bench_copy(dev, stream, args.steps, args.warmup)}
+        print(json.dumps(one[args.workload]()), flush=True)
+        return
 
     ms, tflops, host_inputs, gpu_out = bench_prefill(dev, stream, args.steps, args.warmup)
     line = {
@@ -231,7 +281,8 @@ def main():
                    "seq_len": 1371, "num_q_heads": 16, "num_kv_heads": 8, "head_dim": 128,
                    "flops_per_step": causal_flops(1371, 16, 128), "accumulate": "fp32",
                    "parallelism": "single GPU"},
-        "roofline": roofline("mfma", tflops, PEAK_BF16_TFLOPS, "TFLOP/s"),
+        "roofline": roofline("mfma", tflops, PEAK_BF16_TFLOPS, "TFLOP/s",
+                             traffic_bytes("prefill")),
     }
     if not args.no_components:
         comps = [bench_prefill_fused(dev, stream, max(10, args.steps // 4), 3)]

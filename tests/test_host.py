@@ -171,3 +171,53 @@ def test_bench_refuses_more_than_one_gpu():
     assert res.returncode != 0
     msg = json.loads(res.stdout.strip().splitlines()[-1])
     assert "one GPU" in msg["error"]
+
+
+# ------------------------------------------------------- drop-in C++ header
+
+CALL_SITES = r"""
+#include "kernel_warpper.h"
+using toyinfer::bf16;
+void prefill(const bf16* q, const bf16* k, const bf16* v, bf16* o, uint32_t hd, hipStream_t s) {
+    // the instantiations src/prefill.cu:433-452 provides
+    toyinfer::flash_attention_v1_bf16<32, 2, 64>(q, k, v, o, 16, 8, hd, 100);
+    toyinfer::flash_attention_v1_bf16<32, 4, 64>(q, k, v, o, 16, 8, hd, 100);
+    toyinfer::flash_attention_v1_bf16<32, 4, 128>(q, k, v, o, 16, 8, hd, 100, s);
+    toyinfer::flash_attention_v1_bf16<64, 4, 128>(q, k, v, o, 16, 8, hd, 100, s);
+}
+void decode(const bf16* q, const bf16* k, const bf16* v, float* sc, float* ob, bf16* o,
+            const uint32_t* pos_d, hipStream_t s) {
+    toyinfer::attention_bf16<256, 32>(q, k, v, sc, ob, o, 32, 8, 128, 5, 40);
+    toyinfer::attention_bf16_graph<256, 32>(q, k, v, sc, ob, o, 32, 8, 128, pos_d, 40, s);
+}
+void prologue(bf16* x, const bf16* w, float* f, hipStream_t s) {
+    toyinfer::precompute_freq_f32(f, 128, 1e6f);
+    toyinfer::batch_multi_rmsnorm_bf16(x, w, x, 1e-6f, 7, 8, 128, s);
+    toyinfer::multi_rmsnorm_bf16(x, w, x, 1e-6f, 8, 128);
+    toyinfer::batch_rope_bf16(x, f, 7, 8, 128, s);
+}
+"""
+
+
+def compile_snippet(tmp_path, text):
+    src = tmp_path / "snippet.cpp"
+    src.write_text(text)
+    return subprocess.run(["/opt/rocm/llvm/bin/clang++", "-std=c++17", "-fsyntax-only", "-Wall",
+                           "-D__HIP_PLATFORM_AMD__", "-I/opt/rocm/include",
+                           "-I" + os.path.join(ROOT, "include"), str(src)],
+                          capture_output=True, text=True, timeout=120)
+
+
+def test_dropin_header_compiles_reference_call_sites(tmp_path):
+    res = compile_snippet(tmp_path, CALL_SITES)
+    assert res.returncode == 0, res.stderr
+
+
+@pytest.mark.parametrize("bad", ["toyinfer::flash_attention_v1_bf16<32, 4, 96>(q, q, q, o, 1, 1, 96, 1);",
+                                 "toyinfer::flash_attention_v1_bf16<48, 4, 128>(q, q, q, o, 1, 1, 128, 1);",
+                                 "toyinfer::attention_bf16<100, 32>(q, q, q, f, f, o, 1, 1, 128, 0, 1);"])
+def test_dropin_header_rejects_illegal_instantiations(tmp_path, bad):
+    text = ('#include "kernel_warpper.h"\nusing toyinfer::bf16;\n'
+            "void f_(const bf16* q, bf16* o, float* f) { " + bad + " }\n")
+    res = compile_snippet(tmp_path, text)
+    assert res.returncode != 0 and "static assertion failed" in res.stderr

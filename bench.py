@@ -180,8 +180,7 @@ def bench_decode(dev, stream, steps, warmup, b, L, hq=32, hkv=8, d=128, sets=4):
     q = to_dev(synth.normal_bf16(SEED + 10, "q", (b, hq, d)), dev)
     o = torch.empty((b, hq, d), dtype=torch.bfloat16, device=dev)
     splits = attn.decode_default_splits(b, hq, hkv, d, L)
-    ws = torch.empty(attn.decode_workspace_bytes(b, hq, d, splits), dtype=torch.uint8,
-                     device=dev)
+    ws = attn.decode_workspace(b, hq, d, splits, dev)
 
     def step(i):
         kc, vc = kv[i % sets]

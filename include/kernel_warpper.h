@@ -177,7 +177,8 @@ inline void prefill_qknorm_rope_attention_bf16(
 
 // Batched decode: q/o [B][Hq][D], sequence b's cache at k/v + b*kv_batch_stride
 // elements ([max_len][Hkv][D]), length seq_lens_d[b] (device) or seq_len for
-// all when seq_lens_d is null.  workspace: decode_workspace_bytes(...) bytes.
+// all when seq_lens_d is null.  workspace: decode_workspace_bytes(...) bytes
+// (no initialisation needed).  Calls sharing a workspace must not overlap.
 inline void decode_attention_bf16(const bf16* q, const bf16* k_cache, const bf16* v_cache, bf16* o,
                                   uint32_t batch, uint32_t num_q_heads, uint32_t num_kv_heads,
                                   uint32_t heads_dim, const uint32_t* seq_lens_d, uint32_t seq_len,

@@ -104,7 +104,8 @@ int toyinfer_attention_bf16_graph(const void* Q, const void* Ks, const void* Vs,
  * sequence has length seq_len.  num_splits = 0 picks a default (at most
  * 1024 splits are accepted); the workspace must hold
  * toyinfer_decode_workspace_bytes(B, Hq, D, splits) bytes (256-byte
- * aligned) for the split count used. */
+ * aligned) for the split count used; its contents need no initialisation.
+ * Calls that share a workspace must not overlap. */
 int toyinfer_decode_attention_bf16(const void* q, const void* k_cache, const void* v_cache,
                                    void* o, uint32_t batch, uint32_t num_q_heads,
                                    uint32_t num_kv_heads, uint32_t heads_dim,

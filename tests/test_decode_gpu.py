@@ -101,7 +101,7 @@ def run_batched(qb, kb, vb, lens, dev, splits=0, seq_lens_on_device=False):
     o = torch.full((b, hq, d), 9.0, dtype=torch.bfloat16, device=dev)
     L = int(max(lens))
     s = splits or attn.decode_default_splits(b, hq, hkv, d, L)
-    ws = torch.empty(attn.decode_workspace_bytes(b, hq, d, s), dtype=torch.uint8, device=dev)
+    ws = attn.decode_workspace(b, hq, d, s, dev)
     lens_d = (torch.tensor(np.asarray(lens, np.int32), device=dev)
               if seq_lens_on_device else None)
     attn.decode_attention_bf16(q, k, v, o, b, hq, hkv, d, lens_d, L, cap * hkv * d, s, ws)
@@ -156,6 +156,24 @@ def test_deterministic(dev):
     a = run_batched(qb, kb, vb, [2048] * 8, dev)
     b2 = run_batched(qb, kb, vb, [2048] * 8, dev)
     assert np.array_equal(a, b2)
+
+
+def test_workspace_reused_across_shapes(dev):
+    """One workspace, filled with garbage first, serves calls of different shapes in turn."""
+    shapes = [(4, 3000, 32, 8, 128), (1, 20000, 16, 8, 128), (3, 77, 6, 3, 64),
+              (4, 3000, 32, 8, 128)]
+    big = max(attn.decode_workspace_bytes(b, hq, d, attn.decode_default_splits(b, hq, hkv, d, L))
+              for b, L, hq, hkv, d in shapes)
+    ws = torch.full((big,), 0x7F, dtype=torch.uint8, device=dev)
+    for i, (b, L, hq, hkv, d) in enumerate(shapes):
+        qb, kb, vb = batched_inputs(40 + i, b, L, hq, hkv, d)
+        q, k, v = H.to_dev_bf16(qb, dev), H.to_dev_bf16(kb, dev), H.to_dev_bf16(vb, dev)
+        o = torch.empty((b, hq, d), dtype=torch.bfloat16, device=dev)
+        s = attn.decode_default_splits(b, hq, hkv, d, L)
+        attn.decode_attention_bf16(q, k, v, o, b, hq, hkv, d, None, L, L * hkv * d, s, ws)
+        H.sync()
+        exp = oracle.round_bf16(oracle.decode_batched(qb, kb, vb, [L] * b))
+        H.check_bar(H.bf16_bits_to_f32(H.from_dev_bf16(o)), exp, f"shape {i}")
 
 
 def test_kv_permutation_invariance(dev):

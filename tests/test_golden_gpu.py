@@ -84,7 +84,7 @@ def test_decode_batched_vs_golden(dev):
     lens = torch.tensor(g["lens"].astype(np.int32), device=dev)
     o = torch.empty((2, 8, 128), dtype=torch.bfloat16, device=dev)
     s = attn.decode_default_splits(2, 8, 2, 128, 300)
-    ws = torch.empty(attn.decode_workspace_bytes(2, 8, 128, s), dtype=torch.uint8, device=dev)
+    ws = attn.decode_workspace(2, 8, 128, s, dev)
     attn.decode_attention_bf16(q, k, v, o, 2, 8, 2, 128, lens, 300, 300 * 2 * 128, s, ws)
     H.sync()
     H.check_bar(H.bf16_bits_to_f32(H.from_dev_bf16(o)), H.bf16_bits_to_f32(g["o_bf16"]),

@@ -84,7 +84,11 @@ def test_batched_decode_validation_and_workspace():
     f = L.toyinfer_decode_attention_bf16
     ws = L.toyinfer_decode_workspace_bytes(8, 32, 128, 12)
     heads = 8 * 32
-    assert ws == ((heads * 12 * 2 * 4 + 255) // 256) * 256 + heads * 12 * 128 * 4
+
+    def a256(x):
+        return (x + 255) // 256 * 256
+    # (m, l) pairs, then o[D] partials
+    assert ws == a256(heads * 12 * 2 * 4) + heads * 12 * 128 * 4
     args = dict(q=P, k=P, v=P, o=P, b=8, hq=32, hkv=8, d=128, lens=None, L=4096,
                 stride=4096 * 8 * 128, splits=12, w=P, wb=ws)
 

@@ -178,11 +178,20 @@ def decode_workspace_bytes(batch: int, num_q_heads: int, heads_dim: int, num_spl
     return int(LIB.toyinfer_decode_workspace_bytes(batch, num_q_heads, heads_dim, num_splits))
 
 
+def decode_workspace(batch: int, num_q_heads: int, heads_dim: int, num_splits: int, device):
+    """An uninitialised uint8 workspace tensor sized for these shapes."""
+    import torch
+
+    return torch.empty(decode_workspace_bytes(batch, num_q_heads, heads_dim, num_splits),
+                       dtype=torch.uint8, device=device)
+
+
 def decode_attention_bf16(q, k_cache, v_cache, o, batch: int, num_q_heads: int,
                           num_kv_heads: int, heads_dim: int, seq_lens_d, seq_len: int,
                           kv_batch_stride: int, num_splits: int, workspace,
                           stream=None) -> None:
-    """Batched split-K decode; workspace is a device tensor (any dtype)."""
+    """Batched split-K decode; workspace is a device tensor (any dtype) of at least
+    decode_workspace_bytes(...) bytes (see decode_workspace)."""
     ws_bytes = workspace.numel() * workspace.element_size()
     _check("decode_attention_bf16",
            LIB.toyinfer_decode_attention_bf16(_ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(o), batch,

@@ -37,6 +37,7 @@ hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 
 size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 
+
 // Prefill addresses one KV head's rows with 32-bit byte offsets.
 bool kv_fits_32bit(uint32_t s, uint32_t hkv, uint32_t d) {
     return (uint64_t)s * hkv * d * 2 < 0xffffffffull;
@@ -280,11 +281,11 @@ int toyinfer_decode_attention_bf16(const void* q, const void* k_cache, const voi
     p.len_cap = seq_len;
     p.splits = splits;
     const size_t heads = (size_t)batch * num_q_heads;
+    char* ws = static_cast<char*>(workspace);
     DecodePartials part{};
-    part.ml = static_cast<float*>(workspace);
+    part.ml = reinterpret_cast<float*>(ws);
     part.ml_head = 2 * (int64_t)splits;
-    part.o = reinterpret_cast<float*>(static_cast<char*>(workspace) +
-                                      align_up(heads * splits * 2 * sizeof(float), 256));
+    part.o = reinterpret_cast<float*>(ws + align_up(heads * splits * 2 * sizeof(float), 256));
     part.o_head = (int64_t)splits * heads_dim;
     part.o_split = heads_dim;
     hipStream_t st = as_stream(stream);

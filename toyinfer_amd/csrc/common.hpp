@@ -76,6 +76,15 @@ __device__ __forceinline__ float wave_sum(float x) {
     return x;
 }
 
+// Full wave64 max (every lane gets the result).
+__device__ __forceinline__ float wave_max(float x) {
+    x = row16_max(x);
+    x = fmaxf(x, __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(
+                                               ((__lane_id() ^ 16) << 2), __builtin_bit_cast(int, x))));
+    x = fmaxf(x, xor32(x));
+    return x;
+}
+
 __device__ __forceinline__ uint4 ldg16(const void* p) {
     return *reinterpret_cast<const uint4*>(p);
 }

@@ -55,13 +55,14 @@ __device__ __forceinline__ uint32_t seq_length(const DecodeProblem& p, uint32_t 
     return (pos < p.len_cap ? pos : p.len_cap - 1) + 1;
 }
 
+// Split s of `splits` covers L/splits rows, plus one for the first L%splits
+// splits: every workgroup streams the same number of bytes (the slowest one
+// sets the kernel time).
 __device__ __forceinline__ void split_range(uint32_t L, uint32_t splits, uint32_t split,
                                             uint32_t* begin, uint32_t* end) {
-    uint32_t per = (L + splits - 1) / splits;
-    per = (per + kDecIterRows - 1) / kDecIterRows * kDecIterRows;
-    const uint64_t b = (uint64_t)split * per;
-    *begin = b < L ? (uint32_t)b : L;
-    *end = (uint64_t)*begin + per < L ? *begin + per : L;
+    const uint32_t per = L / splits, rem = L % splits;
+    *begin = split * per + min(split, rem);
+    *end = *begin + per + (split < rem ? 1u : 0u);
 }
 
 // Row-major V tile of one wave in LDS: element (row, col) at
@@ -81,6 +82,72 @@ __device__ __forceinline__ float shfl_xor_f(float x, int m) {
                                                                    __builtin_bit_cast(int, x)));
 }
 
+constexpr int kMaxSplits = 1024;
+
+// Threads i = 0..T-1 of a block merge the splits of head bh for the DW dims
+// [d0, d0 + DW) and write them as bf16.  Thread i covers dims
+// d0 + 4*(i % (DW/4)) .. +3 for the splits s = i / (DW/4) (mod SG),
+// SG = T / (DW/4) split groups, with an online softmax over its splits, so
+// all of its loads are independent of each other; the SG groups are then
+// merged through LDS (s_red: SG*(DW+2) floats).
+// Splits with m = -inf (no positions) get weight 0 and their o is not used.
+template <int DW, int T>
+__device__ void merge_head(const DecodePartials& part, int64_t bh, int d0, uint32_t splits, int i,
+                           float* s_red, uint16_t* out) {
+    constexpr int DG = DW / 4;
+    constexpr int SG = T / DG;
+    static_assert(SG >= 1 && T % DG == 0, "bad merge shape");
+    const int dg = i % DG, sg = i / DG;
+    const float* ml = part.ml + bh * part.ml_head;
+    const float* po = part.o + bh * part.o_head + d0 + 4 * dg;
+    float m = -INFINITY, l = 0.0f;
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll 8
+    for (uint32_t sp = sg; sp < splits; sp += SG) {
+        const float ms = ml[2 * sp];
+        const float ls = ml[2 * sp + 1];
+        const float4 v = *reinterpret_cast<const float4*>(po + (int64_t)sp * part.o_split);
+        const float os[4] = {v.x, v.y, v.z, v.w};
+        if (ms != -INFINITY) {
+            const float mn = fmaxf(m, ms);
+            const float a = __builtin_amdgcn_exp2f(m - mn), b = __builtin_amdgcn_exp2f(ms - mn);
+            l = fmaf(l, a, ls * b);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) acc[e] = fmaf(acc[e], a, os[e] * b);
+            m = mn;
+        }
+    }
+    float* row = s_red + sg * (DW + 2);
+    if (dg == 0) {
+        row[DW] = m;
+        row[DW + 1] = l;
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) row[4 * dg + e] = acc[e];
+    __syncthreads();
+    if (sg != 0) return;
+    float M = -INFINITY;
+#pragma unroll
+    for (int g2 = 0; g2 < SG; ++g2) M = fmaxf(M, s_red[g2 * (DW + 2) + DW]);
+    float den = 0.0f, num[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int g2 = 0; g2 < SG; ++g2) {
+        const float* r = s_red + g2 * (DW + 2);
+        const float mg = r[DW];
+        if (mg == -INFINITY) continue;
+        const float w = __builtin_amdgcn_exp2f(mg - M);
+        den = fmaf(w, r[DW + 1], den);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) num[e] = fmaf(w, r[4 * dg + e], num[e]);
+    }
+    const float inv = den > 0.0f ? 1.0f / den : 0.0f;
+    const uint32_t lo = pack_bf16x2(num[0] * inv, num[1] * inv);
+    const uint32_t hi = pack_bf16x2(num[2] * inv, num[3] * inv);
+    *reinterpret_cast<uint2*>(out + d0 + 4 * dg) = make_uint2(lo, hi);
+}
+
+// Workgroup blockIdx.x takes a fixed slice [t_begin, t_end) of the positions
+// (split_range), its wave w the 32-row chunks w, w+4, ... of that slice.
 template <int D>
 __global__ __launch_bounds__(256, 3) void decode_split_kernel(DecodeProblem p, DecodePartials part,
                                                               float scale_log2) {
@@ -130,8 +197,8 @@ __global__ __launch_bounds__(256, 3) void decode_split_kernel(DecodeProblem p, D
     }
 
     const int64_t row_stride = (int64_t)p.hkv * D;
-    const uint16_t* kbase = p.k + (int64_t)b * p.kv_stride + (int64_t)kvh * D + 8 * g;
-    const uint16_t* vbase = p.v + (int64_t)b * p.kv_stride + (int64_t)kvh * D + 8 * g;
+    const uint16_t* kbase = p.k + (int64_t)b * p.kv_stride + (int64_t)kvh * D;
+    const uint16_t* vbase = p.v + (int64_t)b * p.kv_stride + (int64_t)kvh * D;
     uint16_t* vs = reinterpret_cast<uint16_t*>(s_raw) + wave * V_ELEMS;
 
     f32x4_t acc[NDB];
@@ -151,43 +218,65 @@ __global__ __launch_bounds__(256, 3) void decode_split_kernel(DecodeProblem p, D
         }
     }
 
-    uint4 kr[2][NLD], vr[2][NLD];
-    auto load_kv = [&](uint32_t bb) {
-        const uint32_t tb = bb + wave * kDecWaveRows;
+    // Global loads: instruction j of lane l reads row (l>>3) + 8*(j / CPL) of the
+    // wave's 32, 16-byte chunk (l&7) + 8*(j % CPL): each instruction covers 8
+    // whole 128-byte lines, the shape the memory pipeline streams fastest.
+    constexpr int CPR = D / 8;        // 16-byte chunks per row
+    constexpr int CPL = CPR / 8;      // 128-byte lines per row
+    constexpr int NJ = kDecWaveRows * CPR / 64;
+    const int lrow = lane >> 3, lchunk = lane & 7;
+    int st_off[NJ];  // LDS element offset of instruction j's chunk
 #pragma unroll
-        for (int tt = 0; tt < 2; ++tt) {
-            const uint32_t t = tb + 16 * tt + n;
+    for (int j = 0; j < NJ; ++j) {
+        const int row = lrow + 8 * (j / CPL), chunk = lchunk + 8 * (j % CPL);
+        st_off[j] = row * D + 8 * (chunk ^ vt_swz<D>(row));
+    }
+    uint4 kr[NJ], vr[NJ];
+    auto load_kv = [&](uint32_t tb) {  // rows tb .. tb+31, clamped below t_end
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) {
+            const uint32_t t = tb + lrow + 8 * (j / CPL);
             const uint32_t tc = t < t_end ? t : t_end - 1;
-            const uint16_t* kp = kbase + (int64_t)tc * row_stride;
-            const uint16_t* vp = vbase + (int64_t)tc * row_stride;
-#pragma unroll
-            for (int i = 0; i < NLD; ++i) kr[tt][i] = ldg16(kp + 32 * i);
-#pragma unroll
-            for (int i = 0; i < NLD; ++i) vr[tt][i] = ldg16(vp + 32 * i);
+            const int64_t off = (int64_t)tc * row_stride + 8 * (lchunk + 8 * (j % CPL));
+            kr[j] = ldg16(kbase + off);
+            vr[j] = ldg16(vbase + off);
         }
     };
-    load_kv(t_begin);
-    for (uint32_t base = t_begin; base < t_end; base += kDecIterRows) {
-        const uint32_t t0 = base + wave * kDecWaveRows;
-        // V -> this wave's LDS tile (row 16*tt + n, 16-byte chunk 4i + g).
+    // Chunk c = rows [t_begin + 32c, t_begin + 32c + 32) (masked at t_end).
+    const uint32_t nchunks = (t_end - t_begin + kDecWaveRows - 1) / kDecWaveRows;
+    uint32_t cur = wave;
+    if (cur < nchunks) load_kv(t_begin + cur * kDecWaveRows);
+    while (cur < nchunks) {
+        const uint32_t t0 = t_begin + cur * kDecWaveRows;
+        // K -> this wave's LDS tile, then the A operand (row 16*tt + n, chunk
+        // 4i + g) back out of it.
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) *reinterpret_cast<uint4*>(vs + st_off[j]) = kr[j];
+        bf16x8_t ka[2][NLD];
 #pragma unroll
         for (int tt = 0; tt < 2; ++tt) {
             const int row = 16 * tt + n;
 #pragma unroll
-            for (int i = 0; i < NLD; ++i) {
-                const int chunk = 4 * i + g;
-                *reinterpret_cast<uint4*>(vs + row * D + 8 * (chunk ^ vt_swz<D>(row))) = vr[tt][i];
-            }
+            for (int i = 0; i < NLD; ++i)
+                ka[tt][i] = as_bf16x8(*reinterpret_cast<const uint4*>(
+                    vs + row * D + 8 * ((4 * i + g) ^ vt_swz<D>(row))));
         }
+        // V -> the same tile (LDS operations of a wave complete in order, so
+        // the K reads above see K).
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) *reinterpret_cast<uint4*>(vs + st_off[j]) = vr[j];
         // S^T: lane (head n, g) value r of tile tt = position t0 + 16*tt + 4g + r.
         f32x4_t st[2];
 #pragma unroll
         for (int tt = 0; tt < 2; ++tt) {
             st[tt] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-            for (int i = 0; i < NLD; ++i) st[tt] = mfma16x16x32(as_bf16x8(kr[tt][i]), qb[i], st[tt]);
+            for (int i = 0; i < NLD; ++i) st[tt] = mfma16x16x32(ka[tt][i], qb[i], st[tt]);
         }
-        if (base + kDecIterRows < t_end) load_kv(base + kDecIterRows);
+        // The load registers are free: the next chunk's loads overlap this
+        // chunk's softmax and P.V.
+        const uint32_t nxt = cur + kDecWaves;
+        if (nxt < nchunks) load_kv(t_begin + nxt * kDecWaveRows);
         float mx = -INFINITY;
 #pragma unroll
         for (int tt = 0; tt < 2; ++tt)
@@ -226,6 +315,7 @@ __global__ __launch_bounds__(256, 3) void decode_split_kernel(DecodeProblem p, D
                                        __builtin_bit_cast(uint2, hi).x, __builtin_bit_cast(uint2, hi).y);
             acc[db] = mfma16x16x32(as_bf16x8(a), pb, acc[db]);
         }
+        cur = nxt;
     }
 
     // Merge the four waves: per head n, l summed over the 4 lanes of the head.
@@ -274,7 +364,7 @@ __global__ __launch_bounds__(256, 3) void decode_split_kernel(DecodeProblem p, D
 // partial outputs is a set of independent loads.  Empty splits (m = -inf)
 // get weight 0 and their never-written o is not used.
 constexpr int kCombineThreads = 256;
-constexpr int kMaxSplits = 1024;
+constexpr int kCombineDims = 32;  // dims per combine block: D/32 blocks per head
 
 __device__ __forceinline__ float block_reduce(float x, bool is_max, float* s_red) {
     x = is_max ? fmaxf(x, dpp_f32<kDppXor1>(x)) : x + dpp_f32<kDppXor1>(x);
@@ -337,10 +427,11 @@ template <int D>
 __global__ __launch_bounds__(kCombineThreads) void decode_combine_kernel(DecodePartials part,
                                                                          uint32_t splits,
                                                                          uint16_t* o) {
+    constexpr int DW = kCombineDims;
+    __shared__ float s_red[kCombineThreads / (DW / 4) * (DW + 2)];
     const int64_t bh = blockIdx.x;
-    float m, l;
-    const float r = merge_splits<D>(part, bh, splits, &m, &l);
-    if (threadIdx.x < D) o[bh * D + threadIdx.x] = f32_to_bf16(r);
+    merge_head<DW, kCombineThreads>(part, bh, DW * blockIdx.y, splits, threadIdx.x, s_red,
+                                    o + bh * D);
 }
 
 // Reference-contract finaliser for one sequence: block h merges head h's
@@ -431,6 +522,7 @@ uint32_t decode_head_groups(uint32_t group) {
 
 uint32_t decode_max_splits() { return kMaxSplits; }
 
+
 uint32_t decode_default_splits(uint32_t batch, uint32_t hq, uint32_t hkv, uint32_t d,
                                uint32_t seq_len) {
     const uint32_t group = hq / hkv;
@@ -452,7 +544,7 @@ hipError_t launch_decode_split(const DecodeProblem& p, const DecodePartials& par
 
 hipError_t launch_decode_combine(const DecodeProblem& p, const DecodePartials& part, uint16_t* o,
                                  hipStream_t stream) {
-    const dim3 grid(p.batch * p.hq);
+    const dim3 grid(p.batch * p.hq, p.d / kCombineDims);
     if (p.d == 64)
         hipLaunchKernelGGL(decode_combine_kernel<64>, grid, dim3(kCombineThreads), 0, stream, part,
                            p.splits, o);

@@ -125,16 +125,30 @@ __device__ __forceinline__ void load_q(bf16x8_t (&qf)[PfShape<D>::KSTEPS], const
     const uint32_t qc = qq < p.s ? qq : p.s - 1;
     const uint16_t* qrow = p.q + ((int64_t)qc * p.hq + h) * D + 8 * kg;
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-        uint4 x = ldg16(qrow + ks * 16);
-        if (qq >= p.s) x = make_uint4(0, 0, 0, 0);
-        raw[ks] = x;
-    }
+    for (int ks = 0; ks < KS; ++ks) raw[ks] = ldg16(qrow + ks * 16);
     if constexpr (!FUSED) {
 #pragma unroll
-        for (int ks = 0; ks < KS; ++ks) qf[ks] = as_bf16x8(raw[ks]);
+        for (int ks = 0; ks < KS; ++ks)
+            qf[ks] = as_bf16x8(qq < p.s ? raw[ks] : make_uint4(0, 0, 0, 0));
     } else {
 #pragma clang fp contract(off)
+        // gamma and the (cos, sin) pairs of this row go out with the Q loads,
+        // before anything waits on Q.  Rows past S read row S-1 (unused).
+        const float4* rope = reinterpret_cast<const float4*>(p.rope + (int64_t)qc * D);
+        uint4 gam[KS];
+        float4 cs[KS / 2][4];
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) gam[ks] = ldg16(p.q_gamma + ks * 16 + 8 * kg);
+#pragma unroll
+        for (int ks = 0; ks < KS / 2; ++ks)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) cs[ks][e] = rope[(ks * 16 + 8 * kg) / 2 + e];
+        // Keep every load above ahead of the first use of Q.
+        __builtin_amdgcn_sched_barrier(0);
+        if (qq >= p.s) {
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) raw[ks] = make_uint4(0, 0, 0, 0);
+        }
         float ss = 0.0f;
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks)
@@ -147,16 +161,12 @@ __device__ __forceinline__ void load_q(bf16x8_t (&qf)[PfShape<D>::KSTEPS], const
             }
         ss += xor32(ss);
         const float inv = 1.0f / sqrtf(ss / (float)D + p.eps);
-        // (cos, sin) of this row's angles; rows past S read row S-1 (unused).
-        const float4* rope = reinterpret_cast<const float4*>(p.rope + (int64_t)qc * D);
         // Chunk ks (dims < D/2) pairs with chunk ks + KS/2 (dims + D/2).
 #pragma unroll
         for (int ks = 0; ks < KS / 2; ++ks) {
-            const uint4 g_re = ldg16(p.q_gamma + ks * 16 + 8 * kg);
-            const uint4 g_im = ldg16(p.q_gamma + (ks + KS / 2) * 16 + 8 * kg);
-            float4 cs4[4];
-#pragma unroll
-            for (int e = 0; e < 4; ++e) cs4[e] = rope[(ks * 16 + 8 * kg) / 2 + e];
+            const uint4 g_re = gam[ks];
+            const uint4 g_im = gam[ks + KS / 2];
+            const float4* cs4 = cs[ks];
             uint32_t o_re[4], o_im[4];
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
@@ -214,11 +224,10 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(PrefillProblem p
     const __amdgpu_buffer_rsrc_t rv = make_rsrc(p.v + (int64_t)kvh * D, kv_bytes);
     const uint32_t voff = (threadIdx.x / P::CPR) * row_bytes + (threadIdx.x % P::CPR) * 16;
 
-    bf16x8_t qf[P::KSTEPS];
-    load_q<D, FUSED>(qf, p, qq, h, kg);
-
     TileRegs<D> regs;
     load_tile<D>(regs, rk, rv, voff, row_bytes, 0);
+    bf16x8_t qf[P::KSTEPS];
+    load_q<D, FUSED>(qf, p, qq, h, kg);
 
     f32x16_t oacc[P::DBLK];
 #pragma unroll
@@ -399,9 +408,6 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_splitkv_kernel(PrefillP
     const uint32_t q_end = min(p.s, q0 + kSkBM);
     const uint32_t n_tiles = (q_end + kSkBN - 1) / kSkBN;
 
-    bf16x8_t qf[P::KSTEPS];
-    load_q<D, FUSED>(qf, p, qq, h, kg);
-
     const uint32_t row_bytes = p.hkv * D * 2;
     const uint32_t kv_bytes = (p.s - 1) * row_bytes + D * 2;
     const __amdgpu_buffer_rsrc_t rk = make_rsrc(p.k + (int64_t)kvh * D, kv_bytes);
@@ -419,6 +425,13 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_splitkv_kernel(PrefillP
             vreg[it] = buf_load16(rv, o);
         }
     };
+    // The first tile's loads go out before anything waits on Q (after the
+    // fused prologue, whose loads need the registers, when FUSED).
+    uint32_t t = wave;
+    bf16x8_t qf[P::KSTEPS];
+    if constexpr (FUSED) load_q<D, FUSED>(qf, p, qq, h, kg);
+    if (t < n_tiles) load(t);
+    if constexpr (!FUSED) load_q<D, FUSED>(qf, p, qq, h, kg);
 
     f32x16_t oacc[P::DBLK];
 #pragma unroll
@@ -427,8 +440,6 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_splitkv_kernel(PrefillP
         for (int i = 0; i < 16; ++i) oacc[db][i] = 0.0f;
     float m_run = -INFINITY, l_run = 0.0f;
 
-    uint32_t t = wave;
-    if (t < n_tiles) load(t);
     for (; t < n_tiles; t += 4) {
         {
             const int row = lane / P::CPR, c = lane % P::CPR;

@@ -64,7 +64,7 @@ int toyinfer_flash_attention_algo_bf16(const void* Qs, const void* Ks, const voi
  * per model with toyinfer_rope_cos_sin_f32.  Q_raw is read only (normalised
  * and rotated on load); the normalised and rotated K is written to K_out
  * [S][Hkv][D] (may alias K_raw; typically the layer's KV-cache slot), then
- * used as the attention's K. */
+ * used as the attention's K.  All tensor pointers 16-byte aligned. */
 int toyinfer_prefill_qknorm_rope_attention_bf16(
     const void* Q_raw, const void* K_raw, const void* Vs, void* Os, void* K_out,
     const void* q_gamma, const void* k_gamma, const float* rope_cos_sin, float rms_norm_eps,
@@ -119,7 +119,9 @@ uint32_t toyinfer_decode_default_splits(uint32_t batch, uint32_t num_q_heads,
 size_t toyinfer_decode_workspace_bytes(uint32_t batch, uint32_t num_q_heads, uint32_t heads_dim,
                                        uint32_t num_splits);
 
-/* --------------------------------------------- Qwen3 pre-attention ops */
+/* --------------------------------------------- Qwen3 pre-attention ops
+ * bf16 tensors and gamma are 16-byte aligned (rows are moved with 16-byte
+ * accesses); inv_freq 4-byte aligned. */
 
 /* inv_freq[i] = 1 / powf(theta, 2i/D), i < D/2.  Replaces
  * toyinfer::precompute_freq_f32 (include/kernel_warpper.h:23; src/decode.cu:35-50). */

@@ -121,6 +121,10 @@ def test_prologue_op_validation():
     assert L.toyinfer_batch_multi_rmsnorm_bf16(P, None, P, 1e-6, 4, 8, 128, None) == INVALID
     assert L.toyinfer_batch_multi_rmsnorm_bf16(P, P, P, 1e-6, 0, 8, 128, None) == INVALID
     assert L.toyinfer_multi_rmsnorm_bf16(P, P, P, 1e-6, 8, 96, None) == UNSUPPORTED
+    # rows move with 16-byte accesses
+    assert L.toyinfer_batch_rope_bf16(P + 2, P, 4, 8, 128, None) == INVALID
+    assert L.toyinfer_batch_multi_rmsnorm_bf16(P, P + 8, P, 1e-6, 4, 8, 128, None) == INVALID
+    assert L.toyinfer_qk_norm_rope_bf16(P, P, P + 4, P, 1e-6, 4, 8, 128, None) == INVALID
 
 
 def test_python_wrapper_raises_on_bad_status():

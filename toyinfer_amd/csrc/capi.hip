@@ -137,7 +137,7 @@ int toyinfer_prefill_qknorm_rope_attention_bf16(
     if (!Q_raw || !K_raw || !Vs || !Os || !K_out || !q_gamma || !k_gamma || !rope_cos_sin)
         return TOYINFER_ERR_INVALID_ARGUMENT;
     if (!aligned(Q_raw, 16) || !aligned(Vs, 16) || !aligned(Os, 16) || !aligned(K_out, 16) ||
-        !aligned(q_gamma, 16) || !aligned(K_raw, 2) || !aligned(k_gamma, 2) ||
+        !aligned(q_gamma, 16) || !aligned(K_raw, 16) || !aligned(k_gamma, 16) ||
         !aligned(rope_cos_sin, 16))
         return TOYINFER_ERR_INVALID_ARGUMENT;
     if ((uint64_t)((seq_len + 127) / 128) * num_q_heads > 0x7fffffffull)
@@ -320,7 +320,7 @@ static int row_op(const void* input, const void* weight, void* output, const flo
     if (!input || !output) return TOYINFER_ERR_INVALID_ARGUMENT;
     if ((mode & kRowNorm) && !weight) return TOYINFER_ERR_INVALID_ARGUMENT;
     if ((mode & kRowRope) && !inv_freq) return TOYINFER_ERR_INVALID_ARGUMENT;
-    if (!aligned(input, 2) || !aligned(output, 2) || (weight && !aligned(weight, 2)) ||
+    if (!aligned(input, 16) || !aligned(output, 16) || (weight && !aligned(weight, 16)) ||
         (inv_freq && !aligned(inv_freq, 4)))
         return TOYINFER_ERR_INVALID_ARGUMENT;
     return from_hip(launch_row_norm_rope(static_cast<const uint16_t*>(input),

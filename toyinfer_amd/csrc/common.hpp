@@ -85,6 +85,10 @@ __device__ __forceinline__ float wave_max(float x) {
     return x;
 }
 
+__device__ __forceinline__ uint32_t word_of(const uint4& v, int i) {
+    return i == 0 ? v.x : (i == 1 ? v.y : (i == 2 ? v.z : v.w));
+}
+
 __device__ __forceinline__ uint4 ldg16(const void* p) {
     return *reinterpret_cast<const uint4*>(p);
 }

@@ -98,9 +98,6 @@ __device__ __forceinline__ void load_tile(TileRegs<D>& r, __amdgpu_buffer_rsrc_t
     }
 }
 
-__device__ __forceinline__ uint32_t word_of(const uint4& v, int i) {
-    return i == 0 ? v.x : (i == 1 ? v.y : (i == 2 ? v.z : v.w));
-}
 
 template <int D>
 __device__ __forceinline__ void store_tile(const TileRegs<D>& r, uint16_t* sk, uint16_t* sv) {

@@ -1,9 +1,10 @@
 // Qwen3 pre-attention ops on gfx950: per-head RMSNorm, rotate-half RoPE and
 // the inverse-frequency table.
 //
-// One row (token, head) of D values is handled by D/2 lanes; lane i owns the
-// RoPE pair (i, i + D/2), so the rotation needs no data exchange and the
-// sum of squares is one xor-shuffle reduction over D/2 lanes.  Norm and RoPE
+// One row (token, head) of D values is handled by D/16 lanes; lane c owns the
+// eight RoPE pairs (8c + k, 8c + k + D/2) and moves them with 16-byte loads
+// and stores, so the rotation needs no data exchange and the sum of squares
+// is an xor-shuffle reduction over D/16 lanes.  Norm and RoPE
 // can run separately (the reference's batch_multi_rmsnorm_bf16 and
 // batch_rope_bf16, src/decode.cu:144-199, src/prefill.cu:185-218) or fused
 // in one pass with the intermediate rounded to bf16 exactly where the
@@ -47,38 +48,87 @@ __global__ __launch_bounds__(256) void row_norm_rope_kernel(const uint16_t* in, 
                                                             float eps, uint32_t rows,
                                                             uint32_t nums_head, int mode) {
 #pragma clang fp contract(off)
-    constexpr int LPR = D / 2;  // lanes per row
-    const uint32_t row = blockIdx.x * (256 / LPR) + threadIdx.x / LPR;
-    const int i = threadIdx.x % LPR;
-    if (row >= rows) return;  // whole rows exit together
-    const int64_t off = (int64_t)row * D;
-    float re = bf16_to_f32(in[off + i]);
-    float im = bf16_to_f32(in[off + i + LPR]);
+    constexpr int HALF = D / 2;
+    constexpr int LPR = HALF / 8;     // lanes per row; a lane owns the 8 pairs (8c + k, 8c + k + D/2)
+    constexpr int RPB = 256 / LPR;    // rows per block
+    const uint32_t row = blockIdx.x * RPB + threadIdx.x / LPR;
+    const int c = threadIdx.x % LPR;
+    if (row >= rows) return;  // the LPR lanes of a row exit together
+    const int64_t off = (int64_t)row * D + 8 * c;
+    // Every load goes out before the first use.
+    const uint4 xr = ldg16(in + off), xi = ldg16(in + off + HALF);
+    uint4 wr = make_uint4(0, 0, 0, 0), wi = wr;
     if (mode & kRowNorm) {
-        float ss = re * re + im * im;
+        wr = ldg16(weight + 8 * c);
+        wi = ldg16(weight + 8 * c + HALF);
+    }
+    float4 cs[4];
+    const uint32_t t = row / nums_head;
+    if ((mode & kRowRope) && table) {
+        const float4* tp = reinterpret_cast<const float4*>(table + (uint64_t)t * HALF + 8 * c);
 #pragma unroll
-        for (int m = LPR / 2; m >= 1; m >>= 1) ss += __shfl_xor(ss, m, 64);
+        for (int k = 0; k < 4; ++k) cs[k] = tp[k];
+    }
+    float re[8], im[8];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const uint32_t a = word_of(xr, k), b = word_of(xi, k);
+        re[2 * k] = bf16_lo(a);
+        re[2 * k + 1] = bf16_hi(a);
+        im[2 * k] = bf16_lo(b);
+        im[2 * k + 1] = bf16_hi(b);
+    }
+    if (mode & kRowNorm) {
+        float ss = 0.0f;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) ss += re[k] * re[k];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) ss += im[k] * im[k];
+#pragma unroll
+        for (int m = LPR / 2; m >= 1; m >>= 1) ss += __shfl_xor(ss, m, LPR);
         const float inv = 1.0f / sqrtf(ss / (float)D + eps);
-        re = bf16_lo(pack_bf16x2(re * inv * bf16_to_f32(weight[i]), 0.0f));
-        im = bf16_lo(pack_bf16x2(im * inv * bf16_to_f32(weight[i + LPR]), 0.0f));
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const uint32_t a = word_of(wr, k), b = word_of(wi, k);
+            re[2 * k] = bf16_lo(pack_bf16x2(re[2 * k] * inv * bf16_lo(a), 0.0f));
+            re[2 * k + 1] = bf16_lo(pack_bf16x2(re[2 * k + 1] * inv * bf16_hi(a), 0.0f));
+            im[2 * k] = bf16_lo(pack_bf16x2(im[2 * k] * inv * bf16_lo(b), 0.0f));
+            im[2 * k + 1] = bf16_lo(pack_bf16x2(im[2 * k + 1] * inv * bf16_hi(b), 0.0f));
+        }
     }
     if (mode & kRowRope) {
-        const uint32_t t = row / nums_head;
-        float sn, cs;
+        float cv[8], sv[8];
         if (table) {
-            const float2 c2 = table[(uint64_t)t * LPR + i];
-            cs = c2.x;
-            sn = c2.y;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                cv[2 * k] = cs[k].x;
+                sv[2 * k] = cs[k].y;
+                cv[2 * k + 1] = cs[k].z;
+                sv[2 * k + 1] = cs[k].w;
+            }
         } else {
-            sincosf((float)t * inv_freq[i], &sn, &cs);
+#pragma unroll
+            for (int k = 0; k < 8; ++k) sincosf((float)t * inv_freq[8 * c + k], &sv[k], &cv[k]);
         }
-        const float a = cs * re - sn * im;
-        const float b = cs * im + sn * re;
-        re = a;
-        im = b;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const float a = cv[k] * re[k] - sv[k] * im[k];
+            const float b = cv[k] * im[k] + sv[k] * re[k];
+            re[k] = a;
+            im[k] = b;
+        }
     }
-    out[off + i] = f32_to_bf16(re);
-    out[off + i + LPR] = f32_to_bf16(im);
+    uint4 orr, oi;
+    orr.x = pack_bf16x2(re[0], re[1]);
+    orr.y = pack_bf16x2(re[2], re[3]);
+    orr.z = pack_bf16x2(re[4], re[5]);
+    orr.w = pack_bf16x2(re[6], re[7]);
+    oi.x = pack_bf16x2(im[0], im[1]);
+    oi.y = pack_bf16x2(im[2], im[3]);
+    oi.z = pack_bf16x2(im[4], im[5]);
+    oi.w = pack_bf16x2(im[6], im[7]);
+    *reinterpret_cast<uint4*>(out + off) = orr;
+    *reinterpret_cast<uint4*>(out + off + HALF) = oi;
 }
 
 }  // namespace
@@ -103,7 +153,7 @@ hipError_t launch_row_norm_rope(const uint16_t* in, uint16_t* out, const uint16_
                                 uint32_t num_tokens, uint32_t nums_head, uint32_t d, int mode,
                                 hipStream_t stream) {
     const uint32_t rows = num_tokens * nums_head;
-    const uint32_t rows_per_block = 256 / (d / 2);
+    const uint32_t rows_per_block = 256 / (d / 16);
     const dim3 grid((rows + rows_per_block - 1) / rows_per_block);
     const float2* t2 = reinterpret_cast<const float2*>(table);
     if (d == 64)

@@ -85,6 +85,17 @@ __device__ __forceinline__ float wave_max(float x) {
     return x;
 }
 
+// acc + the sum of the eight bf16 values packed in v (v_dot2_f32_bf16 with ones).
+__device__ __forceinline__ float sum_bf16x8(uint4 v, float acc) {
+    typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+    const bf16x2_t one = __builtin_bit_cast(bf16x2_t, 0x3f803f80u);
+    acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, v.x), one, acc, false);
+    acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, v.y), one, acc, false);
+    acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, v.z), one, acc, false);
+    acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, v.w), one, acc, false);
+    return acc;
+}
+
 __device__ __forceinline__ uint32_t word_of(const uint4& v, int i) {
     return i == 0 ? v.x : (i == 1 ? v.y : (i == 2 ? v.z : v.w));
 }

@@ -267,15 +267,15 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(PrefillProblem p
                     if (key + 32 > qq) st1[i] = -INFINITY;
                 }
             }
-            float m8[8];
+            // Row max: two chains of three-input maxima.
+            float ma = fmaxf(st0[0], st0[1]), mb = fmaxf(st1[0], st1[1]);
 #pragma unroll
-            for (int i = 0; i < 8; ++i)
-                m8[i] = fmaxf(fmaxf(st0[i], st0[i + 8]), fmaxf(st1[i], st1[i + 8]));
-#pragma unroll
-            for (int w = 4; w >= 1; w >>= 1)
-#pragma unroll
-                for (int i = 0; i < w; ++i) m8[i] = fmaxf(m8[i], m8[i + w]);
-            float mx = fmaxf(m8[0], xor32(m8[0]));
+            for (int i = 2; i < 16; i += 2) {
+                ma = fmaxf(fmaxf(ma, st0[i]), st0[i + 1]);
+                mb = fmaxf(fmaxf(mb, st1[i]), st1[i + 1]);
+            }
+            float mx = fmaxf(ma, mb);
+            mx = fmaxf(mx, xor32(mx));
             const float mt = mx * scale_log2;
             const bool need = mt > m_run + kRescaleThreshold;
             if (__any(need)) {
@@ -291,19 +291,11 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(PrefillProblem p
                     for (int i = 0; i < 16; ++i) oacc[db][i] *= alpha;
             }
             const float mref = m_run == -INFINITY ? 0.0f : m_run;
-            float r8[8];
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
                 st0[i] = __builtin_amdgcn_exp2f(fmaf(st0[i], scale_log2, -mref));
                 st1[i] = __builtin_amdgcn_exp2f(fmaf(st1[i], scale_log2, -mref));
             }
-#pragma unroll
-            for (int i = 0; i < 8; ++i) r8[i] = (st0[i] + st0[i + 8]) + (st1[i] + st1[i + 8]);
-#pragma unroll
-            for (int w = 4; w >= 1; w >>= 1)
-#pragma unroll
-                for (int i = 0; i < w; ++i) r8[i] += r8[i + w];
-            l_run += r8[0];
             bf16x8_t pf[4];
 #pragma unroll
             for (int tt = 0; tt < 4; ++tt) {
@@ -316,6 +308,11 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(PrefillProblem p
                 w.w = pack_bf16x2(src[o8 + 6], src[o8 + 7]);
                 pf[tt] = as_bf16x8(w);
             }
+            // The row sum takes the bf16 probabilities the P.V product uses.
+            l_run += sum_bf16x8(__builtin_bit_cast(uint4, pf[0]),
+                                sum_bf16x8(__builtin_bit_cast(uint4, pf[1]), 0.0f)) +
+                     sum_bf16x8(__builtin_bit_cast(uint4, pf[2]),
+                                sum_bf16x8(__builtin_bit_cast(uint4, pf[3]), 0.0f));
             // A = V^T for k-step tt: lane group G = lane/16 (kg = G/2) reads key
             // rows 16*tt + 4*kg + s/4 (+8 for the second half) at dims
             // 32*db + 16*(G%2) + 4*(s%4), s = lane%16.
@@ -463,14 +460,14 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_splitkv_kernel(PrefillP
                 if (key > qq) st[i] = -INFINITY;
             }
         }
-        float m8[8];
+        float ma = fmaxf(st[0], st[1]), mb = fmaxf(st[8], st[9]);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) m8[i] = fmaxf(st[i], st[i + 8]);
-#pragma unroll
-        for (int w = 4; w >= 1; w >>= 1)
-#pragma unroll
-            for (int i = 0; i < w; ++i) m8[i] = fmaxf(m8[i], m8[i + w]);
-        const float mx = fmaxf(m8[0], xor32(m8[0]));
+        for (int i = 2; i < 8; i += 2) {
+            ma = fmaxf(fmaxf(ma, st[i]), st[i + 1]);
+            mb = fmaxf(fmaxf(mb, st[i + 8]), st[i + 9]);
+        }
+        float mx = fmaxf(ma, mb);
+        mx = fmaxf(mx, xor32(mx));
         const float mt = mx * scale_log2;
         const bool need = mt > m_run + kRescaleThreshold;
         if (__any(need)) {
@@ -488,14 +485,6 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_splitkv_kernel(PrefillP
         const float mref = m_run == -INFINITY ? 0.0f : m_run;
 #pragma unroll
         for (int i = 0; i < 16; ++i) st[i] = __builtin_amdgcn_exp2f(fmaf(st[i], scale_log2, -mref));
-        float r8[8];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) r8[i] = st[i] + st[i + 8];
-#pragma unroll
-        for (int w = 4; w >= 1; w >>= 1)
-#pragma unroll
-            for (int i = 0; i < w; ++i) r8[i] += r8[i + w];
-        l_run += r8[0];
         bf16x8_t pf[2];
 #pragma unroll
         for (int tt = 0; tt < 2; ++tt) {
@@ -505,6 +494,8 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_splitkv_kernel(PrefillP
                                           pack_bf16x2(st[o8 + 4], st[o8 + 5]),
                                           pack_bf16x2(st[o8 + 6], st[o8 + 7])));
         }
+        l_run += sum_bf16x8(__builtin_bit_cast(uint4, pf[0]),
+                            sum_bf16x8(__builtin_bit_cast(uint4, pf[1]), 0.0f));
         const int s16 = lane & 15, grp = lane >> 4;
         const uint16_t* va = sv + (4 * kg + (s16 >> 2)) * P::PV + 16 * (grp & 1) + 4 * (s16 & 3);
 #pragma unroll

@@ -60,6 +60,44 @@ struct PfShape {
     static constexpr int DBLK = D / 32;                         // PV output d-blocks
 };
 
+// 128-row kernel tiles: unpadded rows of D bf16, 16-byte chunks XOR-swizzled
+// per row so that the MFMA operand reads are bank-conflict free, filled by
+// buffer loads that write LDS directly (each instruction fills 1 KiB: 64
+// lanes x 16 bytes in lane order, so a lane loads the global chunk that
+// belongs at its LDS slot).
+//   K rows (A operand reads, 8 rows per cycle): chunk c at c ^ (row & 7).
+//   V rows (transposing reads of 4 rows x 32 bytes): chunk c at c ^ 2*(row & 3).
+template <int D>
+struct DmaShape {
+    static constexpr int CPR = D / 8;
+    static constexpr int TILE_ELEMS = kPfBN * D;
+    static constexpr int BLOCKS = kPfBN * D * 2 / 1024;        // 1 KiB blocks per tile and tensor
+    static constexpr int BLOCKS_PER_WAVE = BLOCKS / (kPfThreads / 64);
+    static constexpr int KSTEPS = D / 16;
+    static constexpr int DBLK = D / 32;
+};
+__device__ __forceinline__ int k_swz(int row) { return row & 7; }
+__device__ __forceinline__ int v_swz(int row) { return 2 * (row & 3); }
+
+// Issue this wave's share of tile `tile_off` (K and V) into LDS tiles sk, sv.
+template <int D>
+__device__ __forceinline__ void dma_tile(__amdgpu_buffer_rsrc_t rk, __amdgpu_buffer_rsrc_t rv,
+                                         uint32_t row_bytes, uint32_t tile_off, uint16_t* sk,
+                                         uint16_t* sv) {
+    using P = DmaShape<D>;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+    for (int j = 0; j < P::BLOCKS_PER_WAVE; ++j) {
+        const int blk = wave + (kPfThreads / 64) * j;
+        const int slot = 64 * blk + lane;                // 16-byte slot within the tile
+        const int row = slot / P::CPR, phys = slot % P::CPR;
+        const uint32_t koff = tile_off + row * row_bytes + 16 * (phys ^ k_swz(row));
+        const uint32_t vof = tile_off + row * row_bytes + 16 * (phys ^ v_swz(row));
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (__attribute__((address_space(3))) void*)(sk + 512 * blk), 16, koff, 0, 0, 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (__attribute__((address_space(3))) void*)(sv + 512 * blk), 16, vof, 0, 0, 0);
+    }
+}
+
 template <int D>
 struct TileRegs {
     uint4 k[PfShape<D>::LOADS];
@@ -194,9 +232,14 @@ __device__ __forceinline__ void load_q(bf16x8_t (&qf)[PfShape<D>::KSTEPS], const
 
 template <int D, bool FUSED>
 __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(PrefillProblem p, float scale_log2) {
-    using P = PfShape<D>;
-    __shared__ __align__(16) uint16_t s_k[2][P::K_ELEMS];
-    __shared__ __align__(16) uint16_t s_v[2][P::V_ELEMS];
+    using P = DmaShape<D>;
+    // Four separate arrays (not one indexed by buffer): the compiler can then
+    // tell the tile being computed from the one the LDS DMA is filling, and
+    // does not make the operand reads wait for the in-flight loads.
+    __shared__ __align__(1024) uint16_t s_k0[P::TILE_ELEMS];
+    __shared__ __align__(1024) uint16_t s_k1[P::TILE_ELEMS];
+    __shared__ __align__(1024) uint16_t s_v0[P::TILE_ELEMS];
+    __shared__ __align__(1024) uint16_t s_v1[P::TILE_ELEMS];
 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int ql = lane & 31, kg = lane >> 5;
@@ -219,10 +262,8 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(PrefillProblem p
     const uint32_t kv_bytes = (p.s - 1) * row_bytes + D * 2;
     const __amdgpu_buffer_rsrc_t rk = make_rsrc(p.k + (int64_t)kvh * D, kv_bytes);
     const __amdgpu_buffer_rsrc_t rv = make_rsrc(p.v + (int64_t)kvh * D, kv_bytes);
-    const uint32_t voff = (threadIdx.x / P::CPR) * row_bytes + (threadIdx.x % P::CPR) * 16;
 
-    TileRegs<D> regs;
-    load_tile<D>(regs, rk, rv, voff, row_bytes, 0);
+    dma_tile<D>(rk, rv, row_bytes, 0, s_k0, s_v0);
     bf16x8_t qf[P::KSTEPS];
     load_q<D, FUSED>(qf, p, qq, h, kg);
 
@@ -233,28 +274,41 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(PrefillProblem p
         for (int i = 0; i < 16; ++i) oacc[db][i] = 0.0f;
     float m_run = -INFINITY, l_run = 0.0f;
 
-    store_tile<D>(regs, s_k[0], s_v[0]);
+    // Operand read offsets (elements) within a tile.  K: row ql (and +32),
+    // chunk 2*ks + kg; V^T (transposing read): rows 4*kg + s16/4 (+16*tt, +8),
+    // dims 32*db + 16*(g16 & 1) + 4*(s16 & 3).
+    const int s16 = lane & 15, g16 = lane >> 4;
+    int k_off[P::KSTEPS], v_off[P::DBLK];
+#pragma unroll
+    for (int ks = 0; ks < P::KSTEPS; ++ks) k_off[ks] = ql * D + 8 * ((2 * ks + kg) ^ k_swz(ql));
+    {
+        const int vrow = 4 * kg + (s16 >> 2);
+#pragma unroll
+        for (int db = 0; db < P::DBLK; ++db) {
+            const int c = 4 * db + 2 * (g16 & 1) + ((s16 & 3) >> 1);
+            v_off[db] = vrow * D + 8 * (c ^ v_swz(vrow)) + 4 * (s16 & 1);
+        }
+    }
     __syncthreads();
 
-    for (uint32_t t = 0; t < n_tiles; ++t) {
-        const int buf = t & 1;
-        if (t + 1 < n_tiles) load_tile<D>(regs, rk, rv, voff, row_bytes, (t + 1) * kPfBN * row_bytes);
+    // Tile t computes from (kb, vb) while tile t+1 streams into (kn, vn),
+    // whose last readers passed the previous barrier.
+    auto step = [&](uint32_t t, const uint16_t* kb, const uint16_t* vb, uint16_t* kn,
+                    uint16_t* vn) __attribute__((always_inline)) {
+        if (t + 1 < n_tiles) dma_tile<D>(rk, rv, row_bytes, (t + 1) * kPfBN * row_bytes, kn, vn);
 
         if (t < wave_tiles) {
             const uint32_t n0 = t * kPfBN;
-            const uint16_t* kb = s_k[buf];
-            const uint16_t* vb = s_v[buf];
             f32x16_t st0, st1;
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
                 st0[i] = 0.0f;
                 st1[i] = 0.0f;
             }
-            const uint16_t* ka = kb + ql * P::PK + 8 * kg;
 #pragma unroll
             for (int ks = 0; ks < P::KSTEPS; ++ks) {
-                const uint4 a0 = *reinterpret_cast<const uint4*>(ka + 16 * ks);
-                const uint4 a1 = *reinterpret_cast<const uint4*>(ka + 32 * P::PK + 16 * ks);
+                const uint4 a0 = *reinterpret_cast<const uint4*>(kb + k_off[ks]);
+                const uint4 a1 = *reinterpret_cast<const uint4*>(kb + 32 * D + k_off[ks]);
                 st0 = mfma32x32x16(as_bf16x8(a0), qf[ks], st0);
                 st1 = mfma32x32x16(as_bf16x8(a1), qf[ks], st1);
             }
@@ -316,14 +370,12 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(PrefillProblem p
             // A = V^T for k-step tt: lane group G = lane/16 (kg = G/2) reads key
             // rows 16*tt + 4*kg + s/4 (+8 for the second half) at dims
             // 32*db + 16*(G%2) + 4*(s%4), s = lane%16.
-            const int s16 = lane & 15, grp = lane >> 4;
-            const uint16_t* va = vb + (4 * kg + (s16 >> 2)) * P::PV + 16 * (grp & 1) + 4 * (s16 & 3);
 #pragma unroll
             for (int db = 0; db < P::DBLK; ++db) {
 #pragma unroll
                 for (int tt = 0; tt < 4; ++tt) {
-                    const v4i16_t lo = ds_read_tr16(va + 16 * tt * P::PV + 32 * db);
-                    const v4i16_t hi = ds_read_tr16(va + (16 * tt + 8) * P::PV + 32 * db);
+                    const v4i16_t lo = ds_read_tr16(vb + v_off[db] + 16 * tt * D);
+                    const v4i16_t hi = ds_read_tr16(vb + v_off[db] + (16 * tt + 8) * D);
                     const uint4 a = make_uint4(__builtin_bit_cast(uint2, lo).x, __builtin_bit_cast(uint2, lo).y,
                                                __builtin_bit_cast(uint2, hi).x, __builtin_bit_cast(uint2, hi).y);
                     oacc[db] = mfma32x32x16(as_bf16x8(a), pf[tt], oacc[db]);
@@ -331,8 +383,11 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(PrefillProblem p
             }
         }
 
-        if (t + 1 < n_tiles) store_tile<D>(regs, s_k[buf ^ 1], s_v[buf ^ 1]);
-        __syncthreads();
+        __syncthreads();  // (waits for this wave's tile loads, then for every wave)
+    };
+    for (uint32_t t = 0; t < n_tiles; t += 2) {
+        step(t, s_k0, s_v0, s_k1, s_v1);
+        if (t + 1 < n_tiles) step(t + 1, s_k1, s_v1, s_k0, s_v0);
     }
 
     const float l_tot = l_run + xor32(l_run);  // all lanes take part in the exchange

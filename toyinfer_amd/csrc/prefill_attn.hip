@@ -430,7 +430,7 @@ struct SkShape {
     static constexpr int ROWS_PER_LOAD = 64 / CPR;
     static constexpr int KSTEPS = D / 16;
     static constexpr int DBLK = D / 32;
-    static constexpr int OPITCH = D + 1;              // merge buffer pitch (floats)
+    static constexpr int OPITCH = D + 4;              // merge buffer pitch (floats, 16-byte rows)
 };
 
 template <int D, bool FUSED>
@@ -569,51 +569,60 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_splitkv_kernel(PrefillP
     const float l_tot = l_run + xor32(l_run);
     __syncthreads();  // all waves are done with their tile buffers
     float* s_o = reinterpret_cast<float*>(s_raw);  // [wave][row][OPITCH]
+    // Each lane's accumulator values come in runs of four adjacent columns:
+    // 16-byte stores; rows 528 bytes apart put a half-wave's stores in
+    // distinct bank groups.
 #pragma unroll
     for (int db = 0; db < P::DBLK; ++db)
 #pragma unroll
-        for (int i = 0; i < 16; ++i)
-            s_o[(wave * kSkBM + ql) * P::OPITCH + db * 32 + 8 * (i / 4) + 4 * kg + (i % 4)] = oacc[db][i];
+        for (int g = 0; g < 4; ++g)
+            *reinterpret_cast<float4*>(s_o + (wave * kSkBM + ql) * P::OPITCH + db * 32 + 8 * g + 4 * kg) =
+                make_float4(oacc[db][4 * g], oacc[db][4 * g + 1], oacc[db][4 * g + 2], oacc[db][4 * g + 3]);
     if (kg == 0) {
         s_ml[wave][ql][0] = m_run;
         s_ml[wave][ql][1] = l_tot;
     }
     __syncthreads();
-    constexpr int PER = D / 8;  // dims per thread in the final pass
-    const int row = threadIdx.x >> 3, part = threadIdx.x & 7;
+    // Final pass: lane (row 8*wave + lane%8, columns 16*(lane/8) .. +15);
+    // eight consecutive lanes read eight rows, again in distinct bank groups.
+    // Every load is unconditional: a wave that saw no key has o = 0 and
+    // weight 0.
+    constexpr int PER = D / 8;
+    const int row = 8 * wave + (lane & 7), part = lane >> 3;
     const uint32_t orow_q = q0 + row;
-    if (orow_q < p.s) {
-        float M = -INFINITY;
+    float M = -INFINITY;
 #pragma unroll
-        for (int w = 0; w < 4; ++w) M = fmaxf(M, s_ml[w][row][0]);
-        float wgt[4], den = 0.0f;
+    for (int w = 0; w < 4; ++w) M = fmaxf(M, s_ml[w][row][0]);
+    float wgt[4], den = 0.0f;
 #pragma unroll
-        for (int w = 0; w < 4; ++w) {
-            const float mw = s_ml[w][row][0];
-            wgt[w] = mw == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mw - M);
-            den = fmaf(wgt[w], s_ml[w][row][1], den);
+    for (int w = 0; w < 4; ++w) {
+        const float mw = s_ml[w][row][0];
+        wgt[w] = mw == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mw - M);
+        den = fmaf(wgt[w], s_ml[w][row][1], den);
+    }
+    const float inv = 1.0f / den;
+    float acc[PER];
+#pragma unroll
+    for (int e = 0; e < PER; ++e) acc[e] = 0.0f;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+        const float* src = s_o + (w * kSkBM + row) * P::OPITCH + part * PER;
+#pragma unroll
+        for (int e = 0; e < PER; e += 4) {
+            const float4 x = *reinterpret_cast<const float4*>(src + e);
+            acc[e] = fmaf(wgt[w], x.x, acc[e]);
+            acc[e + 1] = fmaf(wgt[w], x.y, acc[e + 1]);
+            acc[e + 2] = fmaf(wgt[w], x.z, acc[e + 2]);
+            acc[e + 3] = fmaf(wgt[w], x.w, acc[e + 3]);
         }
-        const float inv = 1.0f / den;
+    }
+    if (orow_q < p.s) {
         uint16_t* orow = p.o + ((int64_t)orow_q * p.hq + h) * D + part * PER;
 #pragma unroll
-        for (int e = 0; e < PER; e += 8) {
-            uint32_t w4[4];
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                float v2[2];
-#pragma unroll
-                for (int u = 0; u < 2; ++u) {
-                    const int d = part * PER + e + 2 * j + u;
-                    float o = 0.0f;
-#pragma unroll
-                    for (int w = 0; w < 4; ++w)
-                        o = wgt[w] != 0.0f ? fmaf(wgt[w], s_o[(w * kSkBM + row) * P::OPITCH + d], o) : o;
-                    v2[u] = o * inv;
-                }
-                w4[j] = pack_bf16x2(v2[0], v2[1]);
-            }
-            *reinterpret_cast<uint4*>(orow + e) = make_uint4(w4[0], w4[1], w4[2], w4[3]);
-        }
+        for (int e = 0; e < PER; e += 8)
+            *reinterpret_cast<uint4*>(orow + e) =
+                make_uint4(pack_bf16x2(acc[e] * inv, acc[e + 1] * inv), pack_bf16x2(acc[e + 2] * inv, acc[e + 3] * inv),
+                           pack_bf16x2(acc[e + 4] * inv, acc[e + 5] * inv), pack_bf16x2(acc[e + 6] * inv, acc[e + 7] * inv));
     }
 }
 

@@ -122,9 +122,13 @@ def test_config2_full(dev, algo):
     print(f"[prefill] config2 max-abs {mx:.3g} mean-abs {mn:.3g}", flush=True)
 
 
-def test_algos_agree_at_long_s(dev):
-    """Both kernels on one S=3000 problem (32/8 heads) agree closely."""
-    qb, kb, vb = seeded(3, 3000, 32, 8, 128)
+@pytest.mark.parametrize("s,hq,hkv,d", [(3000, 32, 8, 128), (2600, 16, 4, 64)])
+def test_algos_agree_at_long_s(dev, s, hq, hkv, d):
+    """Both kernels agree closely on problems with several times more query
+    tiles than the split kernel keeps resident (its workgroups then walk
+    several work items each)."""
+    print(f"[prefill] split vs rows S={s} {hq}/{hkv} D={d}", flush=True)
+    qb, kb, vb = seeded(3, s, hq, hkv, d)
     a = H.bf16_bits_to_f32(run_prefill(qb, kb, vb, dev, attn.ALGO_SPLIT_KEYS))
     b = H.bf16_bits_to_f32(run_prefill(qb, kb, vb, dev, attn.ALGO_ROW_TILES))
     H.check_bar(a, b, "split vs rows", max_abs=1.6e-2, mean_abs=3e-4)

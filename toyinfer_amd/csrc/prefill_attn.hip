@@ -163,8 +163,7 @@ __device__ __forceinline__ void load_q(bf16x8_t (&qf)[PfShape<D>::KSTEPS], const
     for (int ks = 0; ks < KS; ++ks) raw[ks] = ldg16(qrow + ks * 16);
     if constexpr (!FUSED) {
 #pragma unroll
-        for (int ks = 0; ks < KS; ++ks)
-            qf[ks] = as_bf16x8(qq < p.s ? raw[ks] : make_uint4(0, 0, 0, 0));
+        for (int ks = 0; ks < KS; ++ks) qf[ks] = as_bf16x8(raw[ks]);  // rows past S: row S-1, never stored
     } else {
 #pragma clang fp contract(off)
         // gamma and the (cos, sin) pairs of this row go out with the Q loads,
@@ -433,9 +432,43 @@ struct SkShape {
     static constexpr int OPITCH = D + 4;              // merge buffer pitch (floats, 16-byte rows)
 };
 
+// Barrier for LDS hand-offs only: waits for this wave's LDS operations but
+// leaves its global loads in flight (a plain __syncthreads also drains them).
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// Work item i = (query head, 32-row query tile), heaviest (last) tiles first;
+// consecutive items walk the KV heads, so with Hkv = 8 each XCD sees one KV
+// head's K/V.
+struct SkItem {
+    uint32_t h, kvh, q0, n_tiles;
+};
+
+__device__ __forceinline__ SkItem sk_item(const PrefillProblem& p, uint32_t i, uint32_t group,
+                                          uint32_t n_qt) {
+    SkItem it;
+    it.kvh = i % p.hkv;
+    const uint32_t r = i / p.hkv;
+    it.h = it.kvh * group + r % group;
+    it.q0 = (n_qt - 1 - r / group) * kSkBM;
+    it.n_tiles = (min(p.s, it.q0 + kSkBM) + kSkBN - 1) / kSkBN;
+    return it;
+}
+
+// Workgroup g of G takes, in round r, item r*G + g on even rounds and
+// r*G + G-1-g on odd ones: the heaviest item of one round pairs with the
+// lightest of the next.
+__device__ __forceinline__ uint32_t sk_item_index(uint32_t round, uint32_t g, uint32_t G) {
+    return round * G + ((round & 1) ? G - 1 - g : g);
+}
+
 template <int D, bool FUSED>
 __global__ __launch_bounds__(kPfThreads, 2) void prefill_splitkv_kernel(PrefillProblem p,
-                                                                        float scale_log2) {
+                                                                        float scale_log2,
+                                                                        uint32_t n_items) {
     using P = SkShape<D>;
     constexpr int LDS_TILES = 4 * P::WAVE_ELEMS * 2;
     constexpr int LDS_MERGE = 4 * kSkBM * P::OPITCH * 4;
@@ -447,182 +480,195 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_splitkv_kernel(PrefillP
     const int ql = lane & 31, kg = lane >> 5;
     const uint32_t group = p.hq / p.hkv;
     const uint32_t n_qt = (p.s + kSkBM - 1) / kSkBM;
-    const uint32_t bid = blockIdx.x;
-    const uint32_t kvh = bid % p.hkv;
-    const uint32_t r = bid / p.hkv;
-    const uint32_t h = kvh * group + r % group;
-    const uint32_t qt = n_qt - 1 - r / group;
-    const uint32_t q0 = qt * kSkBM;
-    const uint32_t qq = q0 + ql;
-    const uint32_t q_end = min(p.s, q0 + kSkBM);
-    const uint32_t n_tiles = (q_end + kSkBN - 1) / kSkBN;
 
     const uint32_t row_bytes = p.hkv * D * 2;
     const uint32_t kv_bytes = (p.s - 1) * row_bytes + D * 2;
-    const __amdgpu_buffer_rsrc_t rk = make_rsrc(p.k + (int64_t)kvh * D, kv_bytes);
-    const __amdgpu_buffer_rsrc_t rv = make_rsrc(p.v + (int64_t)kvh * D, kv_bytes);
     const uint32_t voff = (lane / P::CPR) * row_bytes + (lane % P::CPR) * 16;
     uint16_t* sk = reinterpret_cast<uint16_t*>(s_raw) + wave * P::WAVE_ELEMS;
     uint16_t* sv = sk + P::K_ELEMS;
 
+    uint32_t round = 0;
+    SkItem it = sk_item(p, blockIdx.x, group, n_qt);
+    __amdgpu_buffer_rsrc_t rk = make_rsrc(p.k + (int64_t)it.kvh * D, kv_bytes);
+    __amdgpu_buffer_rsrc_t rv = make_rsrc(p.v + (int64_t)it.kvh * D, kv_bytes);
+
     uint4 kreg[P::LOADS], vreg[P::LOADS];
     auto load = [&](uint32_t t) {
 #pragma unroll
-        for (int it = 0; it < P::LOADS; ++it) {
-            const uint32_t o = t * kSkBN * row_bytes + voff + it * P::ROWS_PER_LOAD * row_bytes;
-            kreg[it] = buf_load16(rk, o);
-            vreg[it] = buf_load16(rv, o);
+        for (int i = 0; i < P::LOADS; ++i) {
+            const uint32_t o = t * kSkBN * row_bytes + voff + i * P::ROWS_PER_LOAD * row_bytes;
+            kreg[i] = buf_load16(rk, o);
+            vreg[i] = buf_load16(rv, o);
         }
     };
     // The first tile's loads go out before anything waits on Q (after the
     // fused prologue, whose loads need the registers, when FUSED).
-    uint32_t t = wave;
     bf16x8_t qf[P::KSTEPS];
-    if constexpr (FUSED) load_q<D, FUSED>(qf, p, qq, h, kg);
-    if (t < n_tiles) load(t);
-    if constexpr (!FUSED) load_q<D, FUSED>(qf, p, qq, h, kg);
+    if constexpr (FUSED) load_q<D, FUSED>(qf, p, it.q0 + ql, it.h, kg);
+    if ((uint32_t)wave < it.n_tiles) load(wave);
+    if constexpr (!FUSED) load_q<D, FUSED>(qf, p, it.q0 + ql, it.h, kg);
 
-    f32x16_t oacc[P::DBLK];
-#pragma unroll
-    for (int db = 0; db < P::DBLK; ++db)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) oacc[db][i] = 0.0f;
-    float m_run = -INFINITY, l_run = 0.0f;
-
-    for (; t < n_tiles; t += 4) {
-        {
-            const int row = lane / P::CPR, c = lane % P::CPR;
-#pragma unroll
-            for (int it = 0; it < P::LOADS; ++it) {
-                const int rr = row + it * P::ROWS_PER_LOAD;
-                *reinterpret_cast<uint4*>(sk + rr * P::PK + 8 * c) = kreg[it];
-                *reinterpret_cast<uint4*>(sv + rr * P::PV + 8 * c) = vreg[it];
-            }
-        }
-        if (t + 4 < n_tiles) load(t + 4);
-        const uint32_t n0 = t * kSkBN;
-        f32x16_t st;
-#pragma unroll
-        for (int i = 0; i < 16; ++i) st[i] = 0.0f;
-        const uint16_t* ka = sk + ql * P::PK + 8 * kg;
-#pragma unroll
-        for (int ks = 0; ks < P::KSTEPS; ++ks)
-            st = mfma32x32x16(as_bf16x8(*reinterpret_cast<const uint4*>(ka + 16 * ks)), qf[ks], st);
-        if (n0 + kSkBN - 1 > q0) {
-#pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                const uint32_t key = n0 + 8 * (i / 4) + 4 * kg + (i % 4);
-                if (key > qq) st[i] = -INFINITY;
-            }
-        }
-        float ma = fmaxf(st[0], st[1]), mb = fmaxf(st[8], st[9]);
-#pragma unroll
-        for (int i = 2; i < 8; i += 2) {
-            ma = fmaxf(fmaxf(ma, st[i]), st[i + 1]);
-            mb = fmaxf(fmaxf(mb, st[i + 8]), st[i + 9]);
-        }
-        float mx = fmaxf(ma, mb);
-        mx = fmaxf(mx, xor32(mx));
-        const float mt = mx * scale_log2;
-        const bool need = mt > m_run + kRescaleThreshold;
-        if (__any(need)) {
-            float alpha = 1.0f;
-            if (need) {
-                alpha = __builtin_amdgcn_exp2f(m_run - mt);
-                m_run = mt;
-            }
-            l_run *= alpha;
-#pragma unroll
-            for (int db = 0; db < P::DBLK; ++db)
-#pragma unroll
-                for (int i = 0; i < 16; ++i) oacc[db][i] *= alpha;
-        }
-        const float mref = m_run == -INFINITY ? 0.0f : m_run;
-#pragma unroll
-        for (int i = 0; i < 16; ++i) st[i] = __builtin_amdgcn_exp2f(fmaf(st[i], scale_log2, -mref));
-        bf16x8_t pf[2];
-#pragma unroll
-        for (int tt = 0; tt < 2; ++tt) {
-            const int o8 = 8 * tt;
-            pf[tt] = as_bf16x8(make_uint4(pack_bf16x2(st[o8 + 0], st[o8 + 1]),
-                                          pack_bf16x2(st[o8 + 2], st[o8 + 3]),
-                                          pack_bf16x2(st[o8 + 4], st[o8 + 5]),
-                                          pack_bf16x2(st[o8 + 6], st[o8 + 7])));
-        }
-        l_run += sum_bf16x8(__builtin_bit_cast(uint4, pf[0]),
-                            sum_bf16x8(__builtin_bit_cast(uint4, pf[1]), 0.0f));
-        const int s16 = lane & 15, grp = lane >> 4;
-        const uint16_t* va = sv + (4 * kg + (s16 >> 2)) * P::PV + 16 * (grp & 1) + 4 * (s16 & 3);
+    while (true) {
+        const uint32_t q0 = it.q0, qq = q0 + ql, n_tiles = it.n_tiles;
+        f32x16_t oacc[P::DBLK];
 #pragma unroll
         for (int db = 0; db < P::DBLK; ++db)
 #pragma unroll
-            for (int tt = 0; tt < 2; ++tt) {
-                const v4i16_t lo = ds_read_tr16(va + 16 * tt * P::PV + 32 * db);
-                const v4i16_t hi = ds_read_tr16(va + (16 * tt + 8) * P::PV + 32 * db);
-                const uint4 a = make_uint4(__builtin_bit_cast(uint2, lo).x, __builtin_bit_cast(uint2, lo).y,
-                                           __builtin_bit_cast(uint2, hi).x, __builtin_bit_cast(uint2, hi).y);
-                oacc[db] = mfma32x32x16(as_bf16x8(a), pf[tt], oacc[db]);
-            }
-    }
+            for (int i = 0; i < 16; ++i) oacc[db][i] = 0.0f;
+        float m_run = -INFINITY, l_run = 0.0f;
 
-    // Merge the four waves' partials of the 32 rows.
-    const float l_tot = l_run + xor32(l_run);
-    __syncthreads();  // all waves are done with their tile buffers
-    float* s_o = reinterpret_cast<float*>(s_raw);  // [wave][row][OPITCH]
-    // Each lane's accumulator values come in runs of four adjacent columns:
-    // 16-byte stores; rows 528 bytes apart put a half-wave's stores in
-    // distinct bank groups.
+        for (uint32_t t = wave; t < n_tiles; t += 4) {
+            {
+                const int row = lane / P::CPR, c = lane % P::CPR;
 #pragma unroll
-    for (int db = 0; db < P::DBLK; ++db)
+                for (int i = 0; i < P::LOADS; ++i) {
+                    const int rr = row + i * P::ROWS_PER_LOAD;
+                    *reinterpret_cast<uint4*>(sk + rr * P::PK + 8 * c) = kreg[i];
+                    *reinterpret_cast<uint4*>(sv + rr * P::PV + 8 * c) = vreg[i];
+                }
+            }
+            if (t + 4 < n_tiles) load(t + 4);
+            const uint32_t n0 = t * kSkBN;
+            f32x16_t st;
 #pragma unroll
-        for (int g = 0; g < 4; ++g)
-            *reinterpret_cast<float4*>(s_o + (wave * kSkBM + ql) * P::OPITCH + db * 32 + 8 * g + 4 * kg) =
-                make_float4(oacc[db][4 * g], oacc[db][4 * g + 1], oacc[db][4 * g + 2], oacc[db][4 * g + 3]);
-    if (kg == 0) {
-        s_ml[wave][ql][0] = m_run;
-        s_ml[wave][ql][1] = l_tot;
-    }
-    __syncthreads();
-    // Final pass: lane (row 8*wave + lane%8, columns 16*(lane/8) .. +15);
-    // eight consecutive lanes read eight rows, again in distinct bank groups.
-    // Every load is unconditional: a wave that saw no key has o = 0 and
-    // weight 0.
-    constexpr int PER = D / 8;
-    const int row = 8 * wave + (lane & 7), part = lane >> 3;
-    const uint32_t orow_q = q0 + row;
-    float M = -INFINITY;
+            for (int i = 0; i < 16; ++i) st[i] = 0.0f;
+            const uint16_t* ka = sk + ql * P::PK + 8 * kg;
 #pragma unroll
-    for (int w = 0; w < 4; ++w) M = fmaxf(M, s_ml[w][row][0]);
-    float wgt[4], den = 0.0f;
+            for (int ks = 0; ks < P::KSTEPS; ++ks)
+                st = mfma32x32x16(as_bf16x8(*reinterpret_cast<const uint4*>(ka + 16 * ks)), qf[ks], st);
+            if (n0 + kSkBN - 1 > q0) {
 #pragma unroll
-    for (int w = 0; w < 4; ++w) {
-        const float mw = s_ml[w][row][0];
-        wgt[w] = mw == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mw - M);
-        den = fmaf(wgt[w], s_ml[w][row][1], den);
-    }
-    const float inv = 1.0f / den;
-    float acc[PER];
+                for (int i = 0; i < 16; ++i) {
+                    const uint32_t key = n0 + 8 * (i / 4) + 4 * kg + (i % 4);
+                    if (key > qq) st[i] = -INFINITY;
+                }
+            }
+            float ma = fmaxf(st[0], st[1]), mb = fmaxf(st[8], st[9]);
 #pragma unroll
-    for (int e = 0; e < PER; ++e) acc[e] = 0.0f;
+            for (int i = 2; i < 8; i += 2) {
+                ma = fmaxf(fmaxf(ma, st[i]), st[i + 1]);
+                mb = fmaxf(fmaxf(mb, st[i + 8]), st[i + 9]);
+            }
+            float mx = fmaxf(ma, mb);
+            mx = fmaxf(mx, xor32(mx));
+            const float mt = mx * scale_log2;
+            const bool need = mt > m_run + kRescaleThreshold;
+            if (__any(need)) {
+                float alpha = 1.0f;
+                if (need) {
+                    alpha = __builtin_amdgcn_exp2f(m_run - mt);
+                    m_run = mt;
+                }
+                l_run *= alpha;
 #pragma unroll
-    for (int w = 0; w < 4; ++w) {
-        const float* src = s_o + (w * kSkBM + row) * P::OPITCH + part * PER;
+                for (int db = 0; db < P::DBLK; ++db)
 #pragma unroll
-        for (int e = 0; e < PER; e += 4) {
-            const float4 x = *reinterpret_cast<const float4*>(src + e);
-            acc[e] = fmaf(wgt[w], x.x, acc[e]);
-            acc[e + 1] = fmaf(wgt[w], x.y, acc[e + 1]);
-            acc[e + 2] = fmaf(wgt[w], x.z, acc[e + 2]);
-            acc[e + 3] = fmaf(wgt[w], x.w, acc[e + 3]);
+                    for (int i = 0; i < 16; ++i) oacc[db][i] *= alpha;
+            }
+            const float mref = m_run == -INFINITY ? 0.0f : m_run;
+#pragma unroll
+            for (int i = 0; i < 16; ++i) st[i] = __builtin_amdgcn_exp2f(fmaf(st[i], scale_log2, -mref));
+            bf16x8_t pf[2];
+#pragma unroll
+            for (int tt = 0; tt < 2; ++tt) {
+                const int o8 = 8 * tt;
+                pf[tt] = as_bf16x8(make_uint4(pack_bf16x2(st[o8 + 0], st[o8 + 1]),
+                                              pack_bf16x2(st[o8 + 2], st[o8 + 3]),
+                                              pack_bf16x2(st[o8 + 4], st[o8 + 5]),
+                                              pack_bf16x2(st[o8 + 6], st[o8 + 7])));
+            }
+            l_run += sum_bf16x8(__builtin_bit_cast(uint4, pf[0]),
+                                sum_bf16x8(__builtin_bit_cast(uint4, pf[1]), 0.0f));
+            const int s16 = lane & 15, grp = lane >> 4;
+            const uint16_t* va = sv + (4 * kg + (s16 >> 2)) * P::PV + 16 * (grp & 1) + 4 * (s16 & 3);
+#pragma unroll
+            for (int db = 0; db < P::DBLK; ++db)
+#pragma unroll
+                for (int tt = 0; tt < 2; ++tt) {
+                    const v4i16_t lo = ds_read_tr16(va + 16 * tt * P::PV + 32 * db);
+                    const v4i16_t hi = ds_read_tr16(va + (16 * tt + 8) * P::PV + 32 * db);
+                    const uint4 a = make_uint4(__builtin_bit_cast(uint2, lo).x, __builtin_bit_cast(uint2, lo).y,
+                                               __builtin_bit_cast(uint2, hi).x, __builtin_bit_cast(uint2, hi).y);
+                    oacc[db] = mfma32x32x16(as_bf16x8(a), pf[tt], oacc[db]);
+                }
         }
-    }
-    if (orow_q < p.s) {
-        uint16_t* orow = p.o + ((int64_t)orow_q * p.hq + h) * D + part * PER;
+
+        // The next item's first tile and Q loads go out now and land while
+        // this item's partials are merged.  (With FUSED the grid holds every
+        // item: its Q prologue would not fit beside the merge's registers.)
+        ++round;
+        const uint32_t nxt = sk_item_index(round, blockIdx.x, gridDim.x);
+        const bool more = !FUSED && nxt < n_items;
+        const uint32_t h = it.h;
+        if (more) {
+            it = sk_item(p, nxt, group, n_qt);
+            rk = make_rsrc(p.k + (int64_t)it.kvh * D, kv_bytes);
+            rv = make_rsrc(p.v + (int64_t)it.kvh * D, kv_bytes);
+            if ((uint32_t)wave < it.n_tiles) load(wave);
+            load_q<D, FUSED>(qf, p, it.q0 + ql, it.h, kg);
+        }
+
+        // Merge the four waves' partials of the 32 rows.
+        const float l_tot = l_run + xor32(l_run);
+        lds_barrier();  // all waves are done with their tile buffers
+        float* s_o = reinterpret_cast<float*>(s_raw);  // [wave][row][OPITCH]
+        // Each lane's accumulator values come in runs of four adjacent
+        // columns: 16-byte stores; rows 528 bytes apart put a half-wave's
+        // stores in distinct bank groups.
 #pragma unroll
-        for (int e = 0; e < PER; e += 8)
-            *reinterpret_cast<uint4*>(orow + e) =
-                make_uint4(pack_bf16x2(acc[e] * inv, acc[e + 1] * inv), pack_bf16x2(acc[e + 2] * inv, acc[e + 3] * inv),
-                           pack_bf16x2(acc[e + 4] * inv, acc[e + 5] * inv), pack_bf16x2(acc[e + 6] * inv, acc[e + 7] * inv));
+        for (int db = 0; db < P::DBLK; ++db)
+#pragma unroll
+            for (int g = 0; g < 4; ++g)
+                *reinterpret_cast<float4*>(s_o + (wave * kSkBM + ql) * P::OPITCH + db * 32 + 8 * g + 4 * kg) =
+                    make_float4(oacc[db][4 * g], oacc[db][4 * g + 1], oacc[db][4 * g + 2], oacc[db][4 * g + 3]);
+        if (kg == 0) {
+            s_ml[wave][ql][0] = m_run;
+            s_ml[wave][ql][1] = l_tot;
+        }
+        lds_barrier();
+        // Final pass: lane (row 8*wave + lane%8, columns 16*(lane/8) .. +15);
+        // eight consecutive lanes read eight rows, again in distinct bank
+        // groups.  Every load is unconditional: a wave that saw no key has
+        // o = 0 and weight 0.
+        constexpr int PER = D / 8;
+        const int row = 8 * wave + (lane & 7), part = lane >> 3;
+        const uint32_t orow_q = q0 + row;
+        float M = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) M = fmaxf(M, s_ml[w][row][0]);
+        float wgt[4], den = 0.0f;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+            const float mw = s_ml[w][row][0];
+            wgt[w] = mw == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mw - M);
+            den = fmaf(wgt[w], s_ml[w][row][1], den);
+        }
+        const float inv = 1.0f / den;
+        float acc[PER];
+#pragma unroll
+        for (int e = 0; e < PER; ++e) acc[e] = 0.0f;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+            const float* src = s_o + (w * kSkBM + row) * P::OPITCH + part * PER;
+#pragma unroll
+            for (int e = 0; e < PER; e += 4) {
+                const float4 x = *reinterpret_cast<const float4*>(src + e);
+                acc[e] = fmaf(wgt[w], x.x, acc[e]);
+                acc[e + 1] = fmaf(wgt[w], x.y, acc[e + 1]);
+                acc[e + 2] = fmaf(wgt[w], x.z, acc[e + 2]);
+                acc[e + 3] = fmaf(wgt[w], x.w, acc[e + 3]);
+            }
+        }
+        if (orow_q < p.s) {
+            uint16_t* orow = p.o + ((int64_t)orow_q * p.hq + h) * D + part * PER;
+#pragma unroll
+            for (int e = 0; e < PER; e += 8)
+                *reinterpret_cast<uint4*>(orow + e) = make_uint4(
+                    pack_bf16x2(acc[e] * inv, acc[e + 1] * inv), pack_bf16x2(acc[e + 2] * inv, acc[e + 3] * inv),
+                    pack_bf16x2(acc[e + 4] * inv, acc[e + 5] * inv), pack_bf16x2(acc[e + 6] * inv, acc[e + 7] * inv));
+        }
+        if (!more) break;
+        lds_barrier();  // the merge buffer's reads are done before tiles are written again
     }
 }
 
@@ -630,15 +676,42 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_splitkv_kernel(PrefillP
 // 128-row kernel would leave CUs idle and be bound by its longest tile walk.
 constexpr uint32_t kSplitKvBelowWgs = 257;
 
+// Workgroups of the split kernel the device holds at once (CUs x resident
+// blocks per CU), queried once per device and variant; 256 CUs x 2 when no
+// device is visible.
+template <int D, bool FUSED>
+uint32_t splitkv_slots() {
+    static int cache[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
+        (void)hipGetLastError();
+        return 256 * 2;
+    }
+    int v = __atomic_load_n(&cache[dev], __ATOMIC_RELAXED);
+    if (v > 0) return (uint32_t)v;
+    int cus = 0, per = 0;
+    const hipError_t e1 = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+    const hipError_t e2 = hipOccupancyMaxActiveBlocksPerMultiprocessor(
+        &per, prefill_splitkv_kernel<D, FUSED>, kPfThreads, 0);
+    if (e1 != hipSuccess || e2 != hipSuccess || cus <= 0 || per <= 0) {
+        (void)hipGetLastError();
+        return 256 * 2;
+    }
+    v = cus * per;
+    __atomic_store_n(&cache[dev], v, __ATOMIC_RELAXED);
+    return (uint32_t)v;
+}
+
 template <int D, bool FUSED>
 hipError_t launch_t(const PrefillProblem& p, hipStream_t st) {
     const uint32_t n_qtiles = (p.s + kPfBM - 1) / kPfBM;
     const float sl2 = kLog2e / sqrtf((float)D);
     const bool split = p.variant == 1 || (p.variant == 0 && n_qtiles * p.hq < kSplitKvBelowWgs);
     if (split) {
-        const dim3 grid(((p.s + kSkBM - 1) / kSkBM) * p.hq);
+        const uint32_t items = ((p.s + kSkBM - 1) / kSkBM) * p.hq;
+        const dim3 grid(FUSED ? items : min(items, splitkv_slots<D, FUSED>()));
         hipLaunchKernelGGL((prefill_splitkv_kernel<D, FUSED>), grid, dim3(kPfThreads), 0, st, p,
-                           sl2);
+                           sl2, items);
     } else {
         const dim3 grid(n_qtiles * p.hq);
         hipLaunchKernelGGL((prefill_kernel<D, FUSED>), grid, dim3(kPfThreads), 0, st, p, sl2);

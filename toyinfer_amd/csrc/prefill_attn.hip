@@ -517,6 +517,11 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_splitkv_kernel(PrefillP
             for (int i = 0; i < 16; ++i) oacc[db][i] = 0.0f;
         float m_run = -INFINITY, l_run = 0.0f;
 
+        // Q and the first tile have landed before the loop (the first tile's
+        // stores need it anyway).  Without this explicit wait the compiler
+        // cannot tell, inside the loop, that Q is no longer in flight, and
+        // holds the QK products for the prefetch of the next tile.
+        __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
         for (uint32_t t = wave; t < n_tiles; t += 4) {
             {
                 const int row = lane / P::CPR, c = lane % P::CPR;

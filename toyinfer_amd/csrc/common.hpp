@@ -64,11 +64,16 @@ __device__ __forceinline__ float row16_sum(float x) {
     return x;
 }
 
-// Value held by lane (lane ^ 32).
-__device__ __forceinline__ float xor32(float x) {
-    const int lane = __lane_id();
-    return __builtin_bit_cast(
-        float, __builtin_amdgcn_ds_bpermute((lane ^ 32) << 2, __builtin_bit_cast(int, x)));
+// x of lanes l and l ^ 32 combined, in every lane.  v_permlane32_swap (a
+// VALU op, no LDS round trip) leaves lane l with r[0] = x(l & 31) and
+// r[1] = x(32 + (l & 31)); both lanes of a pair add in the same order.
+__device__ __forceinline__ float halves_sum(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float halves_max(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 
 // Full wave64 sum (every lane gets the result).
@@ -76,8 +81,7 @@ __device__ __forceinline__ float wave_sum(float x) {
     x = row16_sum(x);
     x += __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(((__lane_id() ^ 16) << 2),
                                                                 __builtin_bit_cast(int, x)));
-    x += xor32(x);
-    return x;
+    return halves_sum(x);
 }
 
 // Full wave64 max (every lane gets the result).
@@ -85,8 +89,7 @@ __device__ __forceinline__ float wave_max(float x) {
     x = row16_max(x);
     x = fmaxf(x, __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(
                                                ((__lane_id() ^ 16) << 2), __builtin_bit_cast(int, x))));
-    x = fmaxf(x, xor32(x));
-    return x;
+    return halves_max(x);
 }
 
 // acc + the sum of the eight bf16 values packed in v (v_dot2_f32_bf16 with ones).

@@ -193,7 +193,7 @@ __device__ __forceinline__ void load_q(bf16x8_t (&qf)[PfShape<D>::KSTEPS], const
                 ss += a * a;
                 ss += b * b;
             }
-        ss += xor32(ss);
+        ss = halves_sum(ss);
         const float inv = 1.0f / sqrtf(ss / (float)D + p.eps);
         // Chunk ks (dims < D/2) pairs with chunk ks + KS/2 (dims + D/2).
 #pragma unroll
@@ -328,7 +328,7 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(PrefillProblem p
                 mb = fmaxf(fmaxf(mb, st1[i]), st1[i + 1]);
             }
             float mx = fmaxf(ma, mb);
-            mx = fmaxf(mx, xor32(mx));
+            mx = halves_max(mx);
             const float mt = mx * scale_log2;
             const bool need = mt > m_run + kRescaleThreshold;
             if (__any(need)) {
@@ -389,7 +389,7 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(PrefillProblem p
         if (t + 1 < n_tiles) step(t + 1, s_k1, s_v1, s_k0, s_v0);
     }
 
-    const float l_tot = l_run + xor32(l_run);  // all lanes take part in the exchange
+    const float l_tot = halves_sum(l_run);  // all lanes take part in the exchange
     if (qq < p.s) {
         const float inv = 1.0f / l_tot;
         uint16_t* orow = p.o + ((int64_t)qq * p.hq + h) * D;
@@ -493,14 +493,21 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_splitkv_kernel(PrefillP
     __amdgpu_buffer_rsrc_t rv = make_rsrc(p.v + (int64_t)it.kvh * D, kv_bytes);
 
     uint4 kreg[P::LOADS], vreg[P::LOADS];
-    auto load = [&](uint32_t t) {
+    auto load_k = [&](uint32_t t) {
 #pragma unroll
-        for (int i = 0; i < P::LOADS; ++i) {
-            const uint32_t o = t * kSkBN * row_bytes + voff + i * P::ROWS_PER_LOAD * row_bytes;
-            kreg[i] = buf_load16(rk, o);
-            vreg[i] = buf_load16(rv, o);
-        }
+        for (int i = 0; i < P::LOADS; ++i)
+            kreg[i] = buf_load16(rk, t * kSkBN * row_bytes + voff + i * P::ROWS_PER_LOAD * row_bytes);
     };
+    auto load_v = [&](uint32_t t) {
+#pragma unroll
+        for (int i = 0; i < P::LOADS; ++i)
+            vreg[i] = buf_load16(rv, t * kSkBN * row_bytes + voff + i * P::ROWS_PER_LOAD * row_bytes);
+    };
+    auto load = [&](uint32_t t) {
+        load_k(t);
+        load_v(t);
+    };
+    const int st_row = lane / P::CPR, st_c = lane % P::CPR;  // this lane's chunk of a tile row
     // The first tile's loads go out before anything waits on Q (after the
     // fused prologue, whose loads need the registers, when FUSED).
     bf16x8_t qf[P::KSTEPS];
@@ -522,17 +529,14 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_splitkv_kernel(PrefillP
         // cannot tell, inside the loop, that Q is no longer in flight, and
         // holds the QK products for the prefetch of the next tile.
         __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+        // Per tile: K is stored (and its next tile requested) first, so the
+        // QK operand reads queue behind 8 KB of stores, not 16; V follows
+        // while the QK products run.
         for (uint32_t t = wave; t < n_tiles; t += 4) {
-            {
-                const int row = lane / P::CPR, c = lane % P::CPR;
 #pragma unroll
-                for (int i = 0; i < P::LOADS; ++i) {
-                    const int rr = row + i * P::ROWS_PER_LOAD;
-                    *reinterpret_cast<uint4*>(sk + rr * P::PK + 8 * c) = kreg[i];
-                    *reinterpret_cast<uint4*>(sv + rr * P::PV + 8 * c) = vreg[i];
-                }
-            }
-            if (t + 4 < n_tiles) load(t + 4);
+            for (int i = 0; i < P::LOADS; ++i)
+                *reinterpret_cast<uint4*>(sk + (st_row + i * P::ROWS_PER_LOAD) * P::PK + 8 * st_c) = kreg[i];
+            if (t + 4 < n_tiles) load_k(t + 4);
             const uint32_t n0 = t * kSkBN;
             f32x16_t st;
 #pragma unroll
@@ -541,6 +545,10 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_splitkv_kernel(PrefillP
 #pragma unroll
             for (int ks = 0; ks < P::KSTEPS; ++ks)
                 st = mfma32x32x16(as_bf16x8(*reinterpret_cast<const uint4*>(ka + 16 * ks)), qf[ks], st);
+#pragma unroll
+            for (int i = 0; i < P::LOADS; ++i)
+                *reinterpret_cast<uint4*>(sv + (st_row + i * P::ROWS_PER_LOAD) * P::PV + 8 * st_c) = vreg[i];
+            if (t + 4 < n_tiles) load_v(t + 4);
             if (n0 + kSkBN - 1 > q0) {
 #pragma unroll
                 for (int i = 0; i < 16; ++i) {
@@ -555,7 +563,7 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_splitkv_kernel(PrefillP
                 mb = fmaxf(fmaxf(mb, st[i + 8]), st[i + 9]);
             }
             float mx = fmaxf(ma, mb);
-            mx = fmaxf(mx, xor32(mx));
+            mx = halves_max(mx);
             const float mt = mx * scale_log2;
             const bool need = mt > m_run + kRescaleThreshold;
             if (__any(need)) {
@@ -614,7 +622,7 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_splitkv_kernel(PrefillP
         }
 
         // Merge the four waves' partials of the 32 rows.
-        const float l_tot = l_run + xor32(l_run);
+        const float l_tot = halves_sum(l_run);
         lds_barrier();  // all waves are done with their tile buffers
         float* s_o = reinterpret_cast<float*>(s_raw);  // [wave][row][OPITCH]
         // Each lane's accumulator values come in runs of four adjacent

@@ -48,22 +48,6 @@ constexpr int kDppXor2 = 0x4E;          // quad_perm [2,3,0,1]
 constexpr int kDppRowHalfMirror = 0x141;  // lane i <-> 7-i within 8
 constexpr int kDppRowMirror = 0x140;      // lane i <-> 15-i within 16
 
-// Reductions over the 16 lanes of a DPP row; every lane of the row gets the result.
-__device__ __forceinline__ float row16_max(float x) {
-    x = fmaxf(x, dpp_f32<kDppXor1>(x));
-    x = fmaxf(x, dpp_f32<kDppXor2>(x));
-    x = fmaxf(x, dpp_f32<kDppRowHalfMirror>(x));
-    x = fmaxf(x, dpp_f32<kDppRowMirror>(x));
-    return x;
-}
-__device__ __forceinline__ float row16_sum(float x) {
-    x += dpp_f32<kDppXor1>(x);
-    x += dpp_f32<kDppXor2>(x);
-    x += dpp_f32<kDppRowHalfMirror>(x);
-    x += dpp_f32<kDppRowMirror>(x);
-    return x;
-}
-
 // x of lanes l and l ^ 32 combined, in every lane.  v_permlane32_swap (a
 // VALU op, no LDS round trip) leaves lane l with r[0] = x(l & 31) and
 // r[1] = x(32 + (l & 31)); both lanes of a pair add in the same order.
@@ -74,22 +58,6 @@ __device__ __forceinline__ float halves_sum(float x) {
 __device__ __forceinline__ float halves_max(float x) {
     const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
     return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
-}
-
-// Full wave64 sum (every lane gets the result).
-__device__ __forceinline__ float wave_sum(float x) {
-    x = row16_sum(x);
-    x += __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(((__lane_id() ^ 16) << 2),
-                                                                __builtin_bit_cast(int, x)));
-    return halves_sum(x);
-}
-
-// Full wave64 max (every lane gets the result).
-__device__ __forceinline__ float wave_max(float x) {
-    x = row16_max(x);
-    x = fmaxf(x, __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(
-                                               ((__lane_id() ^ 16) << 2), __builtin_bit_cast(int, x))));
-    return halves_max(x);
 }
 
 // acc + the sum of the eight bf16 values packed in v (v_dot2_f32_bf16 with ones).

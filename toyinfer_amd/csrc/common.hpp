@@ -50,13 +50,23 @@ constexpr int kDppRowMirror = 0x140;      // lane i <-> 15-i within 16
 
 // x of lanes l and l ^ 32 combined, in every lane.  v_permlane32_swap (a
 // VALU op, no LDS round trip) leaves lane l with r[0] = x(l & 31) and
-// r[1] = x(32 + (l & 31)); both lanes of a pair add in the same order.
-__device__ __forceinline__ float halves_sum(float x) {
+// r[1] = x(32 + (l & 31)); both lanes of a pair combine in the same order.
+__device__ __forceinline__ float xor32_sum(float x) {
     const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
     return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
-__device__ __forceinline__ float halves_max(float x) {
+__device__ __forceinline__ float xor32_max(float x) {
     const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+// The same over lanes l and l ^ 16 with v_permlane16_swap:
+// r[0] = x(l & ~16), r[1] = x(l | 16).
+__device__ __forceinline__ float xor16_sum(float x) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float xor16_max(float x) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
     return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 

@@ -77,11 +77,6 @@ __device__ __forceinline__ v4i16_t ds_read_tr16(const uint16_t* p) {
         (__attribute__((address_space(3))) v4i16_t*)(p));
 }
 
-__device__ __forceinline__ float shfl_xor_f(float x, int m) {
-    return __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(((__lane_id() ^ m) << 2),
-                                                                   __builtin_bit_cast(int, x)));
-}
-
 constexpr int kMaxSplits = 1024;
 
 // Threads i = 0..T-1 of a block merge the splits of head bh for the DW dims
@@ -286,8 +281,7 @@ __global__ __launch_bounds__(256, 3) void decode_split_kernel(DecodeProblem p, D
                 if (t >= t_end) st[tt][r] = -INFINITY;
                 mx = fmaxf(mx, st[tt][r]);
             }
-        mx = fmaxf(mx, shfl_xor_f(mx, 16));
-        mx = fmaxf(mx, shfl_xor_f(mx, 32));
+        mx = xor32_max(xor16_max(mx));
         const float m_new = fmaxf(m_run, mx * scale_log2);
         if (m_new > m_run) {
             const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
@@ -319,38 +313,41 @@ __global__ __launch_bounds__(256, 3) void decode_split_kernel(DecodeProblem p, D
     }
 
     // Merge the four waves: per head n, l summed over the 4 lanes of the head.
-    l_run += shfl_xor_f(l_run, 16);
-    l_run += shfl_xor_f(l_run, 32);
+    l_run = xor32_sum(xor16_sum(l_run));
     __syncthreads();  // every wave is done with its V tile; s_raw becomes s_o
     float* s_o = reinterpret_cast<float*>(s_raw);  // [wave][head][D]
     if ((uint32_t)n < nh) {
 #pragma unroll
         for (int db = 0; db < NDB; ++db)
-#pragma unroll
-            for (int r = 0; r < 4; ++r)
-                s_o[(wave * kDecMaxHeads + n) * D + 16 * db + 4 * g + r] = acc[db][r];
+            *reinterpret_cast<f32x4_t*>(s_o + (wave * kDecMaxHeads + n) * D + 16 * db + 4 * g) = acc[db];
         if (g == 0) {
             s_ml[wave][n][0] = m_run;
             s_ml[wave][n][1] = l_run;
         }
     }
     __syncthreads();
-    for (int e = threadIdx.x; e < (int)nh * D; e += blockDim.x) {
-        const int hs = e / D, d = e % D;
+    // Four dims of one head per thread; every LDS load is unconditional (a
+    // wave that saw no row holds o = 0 and gets weight 0).
+    for (int e = threadIdx.x; e < (int)nh * (D / 4); e += blockDim.x) {
+        const int hs = e / (D / 4), d = 4 * (e % (D / 4));
         float M = -INFINITY;
 #pragma unroll
         for (int w = 0; w < kDecWaves; ++w) M = fmaxf(M, s_ml[w][hs][0]);
-        float o = 0.0f, l = 0.0f;
+        f32x4_t o = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+        float l = 0.0f;
 #pragma unroll
         for (int w = 0; w < kDecWaves; ++w) {
             const float mw = s_ml[w][hs][0];
-            if (mw == -INFINITY) continue;
-            const float sc = __builtin_amdgcn_exp2f(mw - M);
-            o = fmaf(sc, s_o[(w * kDecMaxHeads + hs) * D + d], o);
+            const float sc = mw == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mw - M);
+            o += sc * *reinterpret_cast<const f32x4_t*>(s_o + (w * kDecMaxHeads + hs) * D + d);
             l = fmaf(sc, s_ml[w][hs][1], l);
         }
         const int64_t bh = bh0 + hs;
-        part.o[bh * part.o_head + (int64_t)blockIdx.x * part.o_split + d] = o;
+        // Dword stores: the reference-contract layout keeps partials at
+        // 4-byte alignment only.
+        float* po = part.o + bh * part.o_head + (int64_t)blockIdx.x * part.o_split + d;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) po[r] = o[r];
         if (d == 0) {
             float* ml = part.ml + bh * part.ml_head + blockIdx.x * 2;
             ml[0] = M;
@@ -371,8 +368,7 @@ __device__ __forceinline__ float block_reduce(float x, bool is_max, float* s_red
     x = is_max ? fmaxf(x, dpp_f32<kDppXor2>(x)) : x + dpp_f32<kDppXor2>(x);
     x = is_max ? fmaxf(x, dpp_f32<kDppRowHalfMirror>(x)) : x + dpp_f32<kDppRowHalfMirror>(x);
     x = is_max ? fmaxf(x, dpp_f32<kDppRowMirror>(x)) : x + dpp_f32<kDppRowMirror>(x);
-    x = is_max ? fmaxf(x, shfl_xor_f(x, 16)) : x + shfl_xor_f(x, 16);
-    x = is_max ? fmaxf(x, shfl_xor_f(x, 32)) : x + shfl_xor_f(x, 32);
+    x = is_max ? xor32_max(xor16_max(x)) : xor32_sum(xor16_sum(x));
     const int wave = threadIdx.x >> 6;
     __syncthreads();
     if ((threadIdx.x & 63) == 0) s_red[wave] = x;

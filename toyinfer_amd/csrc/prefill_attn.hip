@@ -193,7 +193,7 @@ __device__ __forceinline__ void load_q(bf16x8_t (&qf)[PfShape<D>::KSTEPS], const
                 ss += a * a;
                 ss += b * b;
             }
-        ss = halves_sum(ss);
+        ss = xor32_sum(ss);
         const float inv = 1.0f / sqrtf(ss / (float)D + p.eps);
         // Chunk ks (dims < D/2) pairs with chunk ks + KS/2 (dims + D/2).
 #pragma unroll
@@ -328,7 +328,7 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(PrefillProblem p
                 mb = fmaxf(fmaxf(mb, st1[i]), st1[i + 1]);
             }
             float mx = fmaxf(ma, mb);
-            mx = halves_max(mx);
+            mx = xor32_max(mx);
             const float mt = mx * scale_log2;
             const bool need = mt > m_run + kRescaleThreshold;
             if (__any(need)) {
@@ -389,7 +389,7 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(PrefillProblem p
         if (t + 1 < n_tiles) step(t + 1, s_k1, s_v1, s_k0, s_v0);
     }
 
-    const float l_tot = halves_sum(l_run);  // all lanes take part in the exchange
+    const float l_tot = xor32_sum(l_run);  // all lanes take part in the exchange
     if (qq < p.s) {
         const float inv = 1.0f / l_tot;
         uint16_t* orow = p.o + ((int64_t)qq * p.hq + h) * D;
@@ -563,7 +563,7 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_splitkv_kernel(PrefillP
                 mb = fmaxf(fmaxf(mb, st[i + 8]), st[i + 9]);
             }
             float mx = fmaxf(ma, mb);
-            mx = halves_max(mx);
+            mx = xor32_max(mx);
             const float mt = mx * scale_log2;
             const bool need = mt > m_run + kRescaleThreshold;
             if (__any(need)) {
@@ -622,7 +622,7 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_splitkv_kernel(PrefillP
         }
 
         // Merge the four waves' partials of the 32 rows.
-        const float l_tot = halves_sum(l_run);
+        const float l_tot = xor32_sum(l_run);
         lds_barrier();  // all waves are done with their tile buffers
         float* s_o = reinterpret_cast<float*>(s_raw);  // [wave][row][OPITCH]
         // Each lane's accumulator values come in runs of four adjacent

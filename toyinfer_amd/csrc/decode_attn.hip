@@ -79,67 +79,6 @@ __device__ __forceinline__ v4i16_t ds_read_tr16(const uint16_t* p) {
 
 constexpr int kMaxSplits = 1024;
 
-// Threads i = 0..T-1 of a block merge the splits of head bh for the DW dims
-// [d0, d0 + DW) and write them as bf16.  Thread i covers dims
-// d0 + 4*(i % (DW/4)) .. +3 for the splits s = i / (DW/4) (mod SG),
-// SG = T / (DW/4) split groups, with an online softmax over its splits, so
-// all of its loads are independent of each other; the SG groups are then
-// merged through LDS (s_red: SG*(DW+2) floats).
-// Splits with m = -inf (no positions) get weight 0 and their o is not used.
-template <int DW, int T>
-__device__ void merge_head(const DecodePartials& part, int64_t bh, int d0, uint32_t splits, int i,
-                           float* s_red, uint16_t* out) {
-    constexpr int DG = DW / 4;
-    constexpr int SG = T / DG;
-    static_assert(SG >= 1 && T % DG == 0, "bad merge shape");
-    const int dg = i % DG, sg = i / DG;
-    const float* ml = part.ml + bh * part.ml_head;
-    const float* po = part.o + bh * part.o_head + d0 + 4 * dg;
-    float m = -INFINITY, l = 0.0f;
-    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll 8
-    for (uint32_t sp = sg; sp < splits; sp += SG) {
-        const float ms = ml[2 * sp];
-        const float ls = ml[2 * sp + 1];
-        const float4 v = *reinterpret_cast<const float4*>(po + (int64_t)sp * part.o_split);
-        const float os[4] = {v.x, v.y, v.z, v.w};
-        if (ms != -INFINITY) {
-            const float mn = fmaxf(m, ms);
-            const float a = __builtin_amdgcn_exp2f(m - mn), b = __builtin_amdgcn_exp2f(ms - mn);
-            l = fmaf(l, a, ls * b);
-#pragma unroll
-            for (int e = 0; e < 4; ++e) acc[e] = fmaf(acc[e], a, os[e] * b);
-            m = mn;
-        }
-    }
-    float* row = s_red + sg * (DW + 2);
-    if (dg == 0) {
-        row[DW] = m;
-        row[DW + 1] = l;
-    }
-#pragma unroll
-    for (int e = 0; e < 4; ++e) row[4 * dg + e] = acc[e];
-    __syncthreads();
-    if (sg != 0) return;
-    float M = -INFINITY;
-#pragma unroll
-    for (int g2 = 0; g2 < SG; ++g2) M = fmaxf(M, s_red[g2 * (DW + 2) + DW]);
-    float den = 0.0f, num[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-    for (int g2 = 0; g2 < SG; ++g2) {
-        const float* r = s_red + g2 * (DW + 2);
-        const float mg = r[DW];
-        if (mg == -INFINITY) continue;
-        const float w = __builtin_amdgcn_exp2f(mg - M);
-        den = fmaf(w, r[DW + 1], den);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) num[e] = fmaf(w, r[4 * dg + e], num[e]);
-    }
-    const float inv = den > 0.0f ? 1.0f / den : 0.0f;
-    const uint32_t lo = pack_bf16x2(num[0] * inv, num[1] * inv);
-    const uint32_t hi = pack_bf16x2(num[2] * inv, num[3] * inv);
-    *reinterpret_cast<uint2*>(out + d0 + 4 * dg) = make_uint2(lo, hi);
-}
 
 // Workgroup blockIdx.x takes a fixed slice [t_begin, t_end) of the positions
 // (split_range), its wave w the 32-row chunks w, w+4, ... of that slice.
@@ -361,7 +300,6 @@ __global__ __launch_bounds__(256, 3) void decode_split_kernel(DecodeProblem p, D
 // partial outputs is a set of independent loads.  Empty splits (m = -inf)
 // get weight 0 and their never-written o is not used.
 constexpr int kCombineThreads = 256;
-constexpr int kCombineDims = 32;  // dims per combine block: D/32 blocks per head
 
 __device__ __forceinline__ float block_reduce(float x, bool is_max, float* s_red) {
     x = is_max ? fmaxf(x, dpp_f32<kDppXor1>(x)) : x + dpp_f32<kDppXor1>(x);
@@ -419,15 +357,84 @@ __device__ float merge_splits(const DecodePartials& part, int64_t bh, uint32_t s
     return den > 0.0f ? tot / den : 0.0f;
 }
 
+// Combine for the batched path: block = (sequence, q-head) with W waves
+// (W = blockDim.x / 64, up to kCombineMaxWaves).  Every lane first takes
+// the maximum of m over a strided share of the splits (one round of loads),
+// then wave w merges the splits w, w+W, ... for every dim (lane l owns dims
+// DPL*l .. +DPL-1) and wave 0 adds the W partial sums.  All loads of a wave
+// are independent of each other and nothing branches on data: a split that
+// saw no position (m = -inf) gets weight 0 and its never-written o is not
+// used.
+constexpr int kCombineMaxWaves = 16;
+
 template <int D>
-__global__ __launch_bounds__(kCombineThreads) void decode_combine_kernel(DecodePartials part,
-                                                                         uint32_t splits,
-                                                                         uint16_t* o) {
-    constexpr int DW = kCombineDims;
-    __shared__ float s_red[kCombineThreads / (DW / 4) * (DW + 2)];
+__global__ __launch_bounds__(64 * kCombineMaxWaves) void decode_combine_kernel(DecodePartials part,
+                                                                             uint32_t splits,
+                                                                             uint16_t* o) {
+    constexpr int DPL = D / 64;
+    __shared__ float s_acc[kCombineMaxWaves][D];
+    __shared__ float s_red[kCombineMaxWaves];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int n_waves = blockDim.x >> 6;
     const int64_t bh = blockIdx.x;
-    merge_head<DW, kCombineThreads>(part, bh, DW * blockIdx.y, splits, threadIdx.x, s_red,
-                                    o + bh * D);
+    const float* ml = part.ml + bh * part.ml_head;
+
+    float mloc = -INFINITY;
+    for (uint32_t sp = threadIdx.x; sp < splits; sp += blockDim.x) mloc = fmaxf(mloc, ml[2 * sp]);
+    mloc = fmaxf(mloc, dpp_f32<kDppXor1>(mloc));
+    mloc = fmaxf(mloc, dpp_f32<kDppXor2>(mloc));
+    mloc = fmaxf(mloc, dpp_f32<kDppRowHalfMirror>(mloc));
+    mloc = fmaxf(mloc, dpp_f32<kDppRowMirror>(mloc));
+    mloc = xor32_max(xor16_max(mloc));
+    if (lane == 0) s_red[wave] = mloc;
+    __syncthreads();
+    float M = s_red[0];
+    for (int w = 1; w < n_waves; ++w) M = fmaxf(M, s_red[w]);
+
+    const float* po = part.o + bh * part.o_head + DPL * lane;
+    float den = 0.0f, acc[DPL];
+#pragma unroll
+    for (int e = 0; e < DPL; ++e) acc[e] = 0.0f;
+#pragma unroll 8
+    for (uint32_t sp = wave; sp < splits; sp += n_waves) {
+        const float ms = ml[2 * sp];
+        const float ls = ml[2 * sp + 1];
+        float v[DPL];
+        if constexpr (DPL == 2) {
+            const float2 x = *reinterpret_cast<const float2*>(po + (int64_t)sp * part.o_split);
+            v[0] = x.x;
+            v[1] = x.y;
+        } else {
+            v[0] = po[(int64_t)sp * part.o_split];
+        }
+        const float w = ms == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(ms - M);
+        den = fmaf(w, ls, den);
+#pragma unroll
+        for (int e = 0; e < DPL; ++e) {
+            const float t = fmaf(w, v[e], acc[e]);
+            acc[e] = w != 0.0f ? t : acc[e];
+        }
+    }
+#pragma unroll
+    for (int e = 0; e < DPL; ++e) s_acc[wave][DPL * lane + e] = acc[e];
+    __syncthreads();  // also: every wave has read s_red before it is reused
+    if (lane == 0) s_red[wave] = den;
+    __syncthreads();
+    if (wave != 0) return;
+    float tot[DPL], dsum = 0.0f;
+#pragma unroll
+    for (int e = 0; e < DPL; ++e) tot[e] = 0.0f;
+    for (int w = 0; w < n_waves; ++w) {
+        dsum += s_red[w];
+#pragma unroll
+        for (int e = 0; e < DPL; ++e) tot[e] += s_acc[w][DPL * lane + e];
+    }
+    const float inv = dsum > 0.0f ? 1.0f / dsum : 0.0f;
+    if constexpr (DPL == 2)
+        *reinterpret_cast<uint32_t*>(o + bh * D + 2 * lane) = pack_bf16x2(tot[0] * inv, tot[1] * inv);
+    else
+        o[bh * D + lane] = f32_to_bf16(tot[0] * inv);
 }
 
 // Reference-contract finaliser for one sequence: block h merges head h's
@@ -540,13 +547,17 @@ hipError_t launch_decode_split(const DecodeProblem& p, const DecodePartials& par
 
 hipError_t launch_decode_combine(const DecodeProblem& p, const DecodePartials& part, uint16_t* o,
                                  hipStream_t stream) {
-    const dim3 grid(p.batch * p.hq, p.d / kCombineDims);
+    // Enough waves per head that the grid holds about a thousand waves
+    // (four to sixteen per head): each wave then merges only a few splits.
+    const uint32_t heads = p.batch * p.hq;
+    uint32_t waves = heads >= 256 ? 4 : (1024 + heads - 1) / heads;
+    if (waves > kCombineMaxWaves) waves = kCombineMaxWaves;
+    if (waves < 4) waves = 4;
+    const dim3 grid(heads), block(64 * waves);
     if (p.d == 64)
-        hipLaunchKernelGGL(decode_combine_kernel<64>, grid, dim3(kCombineThreads), 0, stream, part,
-                           p.splits, o);
+        hipLaunchKernelGGL(decode_combine_kernel<64>, grid, block, 0, stream, part, p.splits, o);
     else
-        hipLaunchKernelGGL(decode_combine_kernel<128>, grid, dim3(kCombineThreads), 0, stream,
-                           part, p.splits, o);
+        hipLaunchKernelGGL(decode_combine_kernel<128>, grid, block, 0, stream, part, p.splits, o);
     return hipGetLastError();
 }
 

@@ -43,10 +43,10 @@ SEED = 2026
 # `bench.py --workload <name>`, scaled by what the same counters read for a
 # 256 MiB device-to-device copy (reads x2.0, writes x1.0); the summaries are
 # under profiles/.  (read KiB, write KiB) as the counters report them.
-PMC_KIB = {"prefill": (5558.0, 5484.0),            # prefill_splitkv_kernel<128,false>
-           "prefill_fused": (92071.2, 65536.6),    # prefill_kernel<128,true>
-           "decode_b8_l4096": (65859.9, 1633.4),   # decode_split_kernel<128>
-           "decode_b1_l32768": (65619.8, 1632.4)}  # decode_split_kernel<128>
+PMC_KIB = {"prefill": (5533.6, 5484.0),            # prefill_splitkv_kernel<128,false>
+           "prefill_fused": (92307.0, 65537.2),    # prefill_kernel<128,true>
+           "decode_b8_l4096": (65854.7, 1633.5),   # decode_split_kernel<128>
+           "decode_b1_l32768": (65615.3, 1632.4)}  # decode_split_kernel<128>
 FETCH_SCALE, WRITE_SCALE = 2.0, 1.0
 
 

@@ -458,11 +458,15 @@ __device__ __forceinline__ SkItem sk_item(const PrefillProblem& p, uint32_t i, u
     return it;
 }
 
-// Workgroup g of G takes, in round r, item r*G + g on even rounds and
-// r*G + G-1-g on odd ones: the heaviest item of one round pairs with the
-// lightest of the next.
+// Workgroup g of G takes, in round r, item r*G + g on even rounds and, on
+// odd ones, the mirror item in reverse order of g's block of eight (g % 8
+// kept): the heaviest item of one round pairs with the lightest of the
+// next, and a workgroup stays on the KV head (item % Hkv, with Hkv = 8) whose
+// K/V its XCD's L2 already holds (workgroups go to the XCDs round-robin).
 __device__ __forceinline__ uint32_t sk_item_index(uint32_t round, uint32_t g, uint32_t G) {
-    return round * G + ((round & 1) ? G - 1 - g : g);
+    if (!(round & 1)) return round * G + g;
+    const uint32_t m = G % 8 == 0 ? (G / 8 - 1 - g / 8) * 8 + g % 8 : G - 1 - g;
+    return round * G + m;
 }
 
 template <int D, bool FUSED>

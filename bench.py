@@ -54,7 +54,7 @@ def traffic_bytes(workload):
     r, w = PMC_KIB[workload]
     return int(round((r * FETCH_SCALE + w * WRITE_SCALE) * 1024))
 WORKLOADS = ("all", "prefill", "prefill_fused", "decode_b8_l4096", "decode_b1_l32768",
-             "copy_calibration")
+             "decode_step", "copy_calibration")
 
 
 def causal_flops(s, hq, d):
@@ -199,6 +199,50 @@ def bench_decode(dev, stream, steps, warmup, b, L, hq=32, hkv=8, d=128, sets=4):
                                  traffic_bytes(f"decode_b{b}_l{L}"))}
 
 
+def bench_decode_step(dev, stream, steps, warmup, hq=32, hkv=8, d=128, msl=40960, pos=4095):
+    """Decode-step pre-pass for one token (Qwen3-8B geometry): the fused
+    norm + RoPE + cache-write pass against the six drop-in ops of
+    src/transformer.cpp:535-552 on the same stream.  Both are launch-latency
+    bound (a few KiB move); the figure of merit is time per step."""
+    import torch
+
+    from toyinfer_amd import attn, synth
+
+    q = to_dev(synth.normal_bf16(SEED + 20, "q", (hq, d)), dev)
+    k = to_dev(synth.normal_bf16(SEED + 20, "k", (hkv, d)), dev)
+    v = to_dev(synth.normal_bf16(SEED + 20, "v", (hkv, d)), dev)
+    gq = to_dev(synth.uniform_bf16(SEED + 20, "gq", (d,), 0.9, 1.1), dev)
+    gk = to_dev(synth.uniform_bf16(SEED + 20, "gk", (d,), 0.9, 1.1), dev)
+    inv = torch.empty(d // 2, dtype=torch.float32, device=dev)
+    attn.precompute_freq_f32(inv, d, 1e6)
+    kc = torch.zeros((msl, hkv, d), dtype=torch.bfloat16, device=dev)
+    vc = torch.zeros_like(kc)
+    pos_d = torch.tensor([pos], dtype=torch.int32, device=dev)
+    qo = torch.empty_like(q)
+
+    def fused(i):
+        attn.decode_qkv_prologue_bf16(q, k, v, gq, gk, inv, pos_d, msl, 1e-6, qo, kc, vc, hq, hkv, d,
+                                      stream)
+
+    def six(i):
+        attn.multi_rmsnorm_bf16(q, gq, qo, 1e-6, hq, d, stream)
+        attn.multi_rmsnorm_bf16(k, gk, k, 1e-6, hkv, d, stream)
+        attn.rope_bf16_graph(qo, inv, pos_d, hq, d, stream)
+        attn.rope_bf16_graph(k, inv, pos_d, hkv, d, stream)
+        attn.write_kv_cache_bf16(k, kc, pos_d, hkv * d, stream)
+        attn.write_kv_cache_bf16(v, vc, pos_d, hkv * d, stream)
+
+    ms_f = time_steps(fused, steps, warmup, stream)
+    ms_6 = time_steps(six, steps, warmup, stream)
+    moved = (2 * hq * d + 2 * hkv * d * 2) * 2 + d * 2 * 2 + d * 2
+    return {"workload": f"decode_step_prologue_hq{hq}_hkv{hkv}_d{d}",
+            "entry": "toyinfer_decode_qkv_prologue_bf16", "steps": steps,
+            "ms_per_step": round(ms_f, 5), "value": round(ms_f * 1e3, 2), "unit": "us/step",
+            "higher_is_better": False, "six_op_sequence_us": round(ms_6 * 1e3, 2),
+            "note": f"one token: {moved} bytes move, so both paths are launch-latency bound; "
+                    "six_op_sequence_us = the reference's six launches through this library"}
+
+
 def bench_copy(dev, stream, steps, warmup, mib=256):
     """Device-to-device copy of `mib` MiB: a kernel with known HBM traffic (mib
     read + mib written per launch), the scale for the FETCH_SIZE / WRITE_SIZE
@@ -266,6 +310,7 @@ def main():
                                                        b=8, L=4096),
                "decode_b1_l32768": lambda: bench_decode(dev, stream, args.steps, args.warmup,
                                                         b=1, L=32768),
+               "decode_step": lambda: bench_decode_step(dev, stream, args.steps, args.warmup),
                "copy_calibration": lambda: bench_copy(dev, stream, args.steps, args.warmup)}
         print(json.dumps(one[args.workload]()), flush=True)
         return
@@ -287,6 +332,7 @@ def main():
         comps = [bench_prefill_fused(dev, stream, max(10, args.steps // 4), 3)]
         comps.append(bench_decode(dev, stream, max(50, args.steps * 2), 10, b=8, L=4096))
         comps.append(bench_decode(dev, stream, max(50, args.steps * 2), 10, b=1, L=32768))
+        comps.append(bench_decode_step(dev, stream, max(50, args.steps * 2), 10))
         line["components"] = comps
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(host_inputs, gpu_out, args.cpu_seconds)

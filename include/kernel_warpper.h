@@ -140,9 +140,55 @@ inline void batch_rope_bf16(bf16* qk_ptr, const float* __restrict__ inv_freq,
                    "batch_rope_bf16");
 }
 
+// include/kernel_warpper.h:79-81: in place, every head at position pos.
+inline void rope_bf16(bf16* qk_ptr, const float* __restrict__ inv_freq, uint32_t pos,
+                      const uint32_t nums_head, const uint32_t head_dim,
+                      hipStream_t stream_d = nullptr) {
+    TOYINFER_CHECK(toyinfer_rope_bf16(qk_ptr, inv_freq, pos, nums_head, head_dim, stream_d),
+                   "rope_bf16");
+}
+
+// include/kernel_warpper.h:83-86: the position is read from pos_d when the
+// kernel runs (graph replays see each new position).
+inline void rope_bf16_graph(bf16* qk_ptr, const float* __restrict__ inv_freq,
+                            const uint32_t* __restrict__ pos_d, const uint32_t nums_head,
+                            const uint32_t head_dim, hipStream_t stream_d = nullptr) {
+    TOYINFER_CHECK(toyinfer_rope_bf16_graph(qk_ptr, inv_freq, pos_d, nums_head, head_dim,
+                                            stream_d),
+                   "rope_bf16_graph");
+}
+
+// include/kernel_warpper.h:92-96: kv_dim values to cache row *pos_d.
+// NUM_THREADS does not change the kernel.
+template <const uint32_t NUM_THREADS>
+void write_kv_cache_bf16(const bf16* __restrict__ src, bf16* __restrict__ cache,
+                         const uint32_t* __restrict__ pos_d, const uint32_t kv_dim,
+                         hipStream_t stream_d = nullptr) {
+    static_assert(NUM_THREADS > 0 && NUM_THREADS <= 1024, "illegal launch shape");
+    TOYINFER_CHECK(toyinfer_write_kv_cache_bf16(src, cache, pos_d, kv_dim, stream_d),
+                   "write_kv_cache_bf16");
+}
+
 // ------------------------------------------------------------- extensions
-// Entry points with no counterpart in the reference: batched split-K decode
-// and the prefill with QK-RMSNorm + RoPE fused in front.
+// Entry points with no counterpart in the reference: batched split-K decode,
+// the prefill with QK-RMSNorm + RoPE fused in front, and the decode step's
+// norm/RoPE/cache-write pre-pass in one launch.
+
+// src/transformer.cpp:535-552 (multi_rmsnorm_bf16 x2, rope_bf16_graph x2,
+// write_kv_cache_bf16 x2) in one launch; pos = min(*pos_d, max_seq_len - 1).
+inline void decode_qkv_prologue_bf16(const bf16* q, const bf16* k, const bf16* v,
+                                     const bf16* q_norm_weight, const bf16* k_norm_weight,
+                                     const float* inv_freq, const uint32_t* pos_d,
+                                     uint32_t max_seq_len, float rms_norm_eps, bf16* q_out,
+                                     bf16* k_cache, bf16* v_cache, uint32_t num_q_heads,
+                                     uint32_t num_kv_heads, uint32_t head_dim,
+                                     hipStream_t stream_d = nullptr) {
+    TOYINFER_CHECK(toyinfer_decode_qkv_prologue_bf16(
+                       q, k, v, q_norm_weight, k_norm_weight, inv_freq, pos_d, max_seq_len,
+                       rms_norm_eps, q_out, k_cache, v_cache, num_q_heads, num_kv_heads, head_dim,
+                       stream_d),
+                   "decode_qkv_prologue_bf16");
+}
 
 // Rotary (cos, sin) table [num_positions][D/2][2], built once per model.
 inline void rope_cos_sin_f32(float* table, const float* inv_freq, uint32_t num_positions,

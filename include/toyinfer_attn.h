@@ -158,6 +158,41 @@ int toyinfer_qk_norm_rope_bf16(const void* input, const void* weight, void* outp
                                const float* inv_freq, float rms_norm_eps, uint32_t num_tokens,
                                uint32_t nums_head, uint32_t head_dim, void* stream);
 
+/* ------------------------------------------- decode-step pre-pass ops
+ * One decoded token: q [Hq][D], k and v [Hkv][D]; caches [positions][Hkv][D]
+ * (one layer's K or V cache base, as the reference passes them).  All bf16
+ * tensors 16-byte aligned; pos_d and inv_freq 4-byte aligned. */
+
+/* Rotate-half RoPE in place at position pos for all nums_head rows,
+ * angle = (float)pos * inv_freq[i].  Replaces toyinfer::rope_bf16
+ * (include/kernel_warpper.h:79-81; src/decode.cu:301-324, 353-361). */
+int toyinfer_rope_bf16(void* qk, const float* inv_freq, uint32_t pos, uint32_t nums_head,
+                       uint32_t head_dim, void* stream);
+/* The same with the position read from device memory (*pos_d) when the
+ * kernel runs, so a captured graph replays at each new position.  Replaces
+ * toyinfer::rope_bf16_graph (include/kernel_warpper.h:83-86;
+ * src/decode.cu:326-351, 363-372). */
+int toyinfer_rope_bf16_graph(void* qk, const float* inv_freq, const uint32_t* pos_d,
+                             uint32_t nums_head, uint32_t head_dim, void* stream);
+/* cache[*pos_d * kv_dim + i] = src[i], i < kv_dim (even).  *pos_d must be a
+ * row the cache holds, as in the reference.  Replaces
+ * toyinfer::write_kv_cache_bf16<NUM_THREADS> (include/kernel_warpper.h:92-96;
+ * src/decode.cu:374-397). */
+int toyinfer_write_kv_cache_bf16(const void* src, void* cache, const uint32_t* pos_d,
+                                 uint32_t kv_dim, void* stream);
+/* Fused decode-step pre-pass (extension): in one launch, per-head RMSNorm
+ * -> bf16 -> RoPE(pos) -> bf16 of q into q_out (q_out may equal q) and of k
+ * into row pos of k_cache, and v copied into row pos of v_cache, with
+ * pos = min(*pos_d, max_seq_len - 1) read on the device.  Replaces the six
+ * launches of src/transformer.cpp:535-552 (multi_rmsnorm_bf16 x2,
+ * rope_bf16_graph x2, write_kv_cache_bf16 x2) with the same rounding points. */
+int toyinfer_decode_qkv_prologue_bf16(const void* q, const void* k, const void* v,
+                                      const void* q_norm_weight, const void* k_norm_weight,
+                                      const float* inv_freq, const uint32_t* pos_d,
+                                      uint32_t max_seq_len, float rms_norm_eps, void* q_out,
+                                      void* k_cache, void* v_cache, uint32_t num_q_heads,
+                                      uint32_t num_kv_heads, uint32_t head_dim, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

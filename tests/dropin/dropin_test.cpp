@@ -12,6 +12,7 @@
 // every case passes.
 #include <hip/hip_runtime_api.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstdio>
 #include <cstring>
@@ -38,6 +39,10 @@ void or_decode_attention_f32(const float* qf, const float* kf, const float* vf, 
 void or_inv_freq(float* inv_freq, int d_head, float theta);
 void or_qk_norm_rope(float* x, const float* gamma, const float* inv_freq, uint32_t num_tokens,
                      uint32_t num_heads, uint32_t d_head, float eps);
+void or_multi_rmsnorm(const float* x, const float* w, float* out, uint32_t num_rows,
+                      uint32_t d_head, float eps);
+void or_rope(float* qk, const float* inv_freq, uint32_t num_tokens, uint32_t num_heads,
+             uint32_t d_head, uint32_t pos0);
 }
 
 namespace {
@@ -354,6 +359,75 @@ void prologue_cases() {
     check_bar(from_bits(get_bits(dout)), round_bf16(oref), "prefill_qknorm_rope_attention_bf16 O");
 }
 
+// ------------------------------------------------------ decode-step pre-pass
+
+void decode_step_cases() {
+    const uint32_t hq = 32, hkv = 8, d = 128, msl = 24, pos = 11;
+    const float eps = 1e-6f;
+    Dev<float> inv(d / 2);
+    toyinfer::precompute_freq_f32(inv.p, d, 1e6f);
+    hip_ok(hipDeviceSynchronize(), "sync");
+    const std::vector<float> inv_h = inv.get();
+    std::vector<float> q((size_t)hq * d), k((size_t)hkv * d), v(k.size()), gq(d), gk(d);
+    for (size_t i = 0; i < q.size(); ++i) q[i] = std::sin(0.29f * (float)i) * 1.5f;
+    for (size_t i = 0; i < k.size(); ++i) {
+        k[i] = std::cos(0.17f * (float)i) * 1.2f;
+        v[i] = std::sin(0.05f * (float)i + 1.0f);
+    }
+    for (uint32_t i = 0; i < d; ++i) {
+        gq[i] = 0.9f + 0.2f * (float)((i * 13) % 97) / 96.0f;
+        gk[i] = 1.1f - 0.2f * (float)((i * 7) % 89) / 88.0f;
+    }
+    const auto qb = to_bits(q), kb = to_bits(k), vb = to_bits(v), gqb = to_bits(gq), gkb = to_bits(gk);
+    // Expected: per-head RMSNorm -> bf16 -> RoPE at pos -> bf16.
+    std::vector<float> qe(q.size()), ke(k.size());
+    or_multi_rmsnorm(from_bits(qb).data(), from_bits(gqb).data(), qe.data(), hq, d, eps);
+    or_multi_rmsnorm(from_bits(kb).data(), from_bits(gkb).data(), ke.data(), hkv, d, eps);
+    or_rope(qe.data(), inv_h.data(), 1, hq, d, pos);
+    or_rope(ke.data(), inv_h.data(), 1, hkv, d, pos);
+
+    Dev<uint32_t> pos_d(1);
+    pos_d.put({pos});
+    Dev<bf16> dq(qb.size()), dk(kb.size()), dv(vb.size()), dgq(d), dgk(d);
+    Dev<bf16> kc((size_t)msl * hkv * d), vc((size_t)msl * hkv * d);
+    put_bits(dgq, gqb);
+    put_bits(dgk, gkb);
+    auto check_step = [&](const std::string& label, const std::vector<uint16_t>& q_got) {
+        const auto kcb = get_bits(kc), vcb = get_bits(vc);
+        const size_t row = (size_t)pos * hkv * d;
+        check_close(from_bits(q_got), qe, 2e-2f, 2e-2f, label + " q");
+        check_close(from_bits(std::vector<uint16_t>(kcb.begin() + row, kcb.begin() + row + kb.size())),
+                    ke, 2e-2f, 2e-2f, label + " k cache row");
+        report(std::equal(vb.begin(), vb.end(), vcb.begin() + row), label + " v cache row", "");
+    };
+
+    // The reference's decode step, src/transformer.cpp:535-552, on one stream.
+    hipStream_t stream;
+    hip_ok(hipStreamCreate(&stream), "stream");
+    put_bits(dq, qb);
+    put_bits(dk, kb);
+    put_bits(dv, vb);
+    toyinfer::multi_rmsnorm_bf16(dq.p, dgq.p, dq.p, eps, hq, d, stream);
+    toyinfer::multi_rmsnorm_bf16(dk.p, dgk.p, dk.p, eps, hkv, d, stream);
+    toyinfer::rope_bf16_graph(dq.p, inv.p, pos_d.p, hq, d, stream);
+    toyinfer::rope_bf16_graph(dk.p, inv.p, pos_d.p, hkv, d, stream);
+    toyinfer::write_kv_cache_bf16<256>(dk.p, kc.p, pos_d.p, hkv * d, stream);
+    toyinfer::write_kv_cache_bf16<256>(dv.p, vc.p, pos_d.p, hkv * d, stream);
+    hip_ok(hipStreamSynchronize(stream), "sync");
+    check_step("decode step (six reference ops)", get_bits(dq));
+
+    // The same step fused into one launch.
+    put_bits(dq, qb);
+    put_bits(dk, kb);
+    hip_ok(hipMemset(kc.p, 0, kc.n * 2), "memset");
+    hip_ok(hipMemset(vc.p, 0, vc.n * 2), "memset");
+    toyinfer::decode_qkv_prologue_bf16(dq.p, dk.p, dv.p, dgq.p, dgk.p, inv.p, pos_d.p, msl, eps,
+                                       dq.p, kc.p, vc.p, hq, hkv, d, stream);
+    hip_ok(hipStreamSynchronize(stream), "sync");
+    check_step("decode_qkv_prologue_bf16", get_bits(dq));
+    hip_ok(hipStreamDestroy(stream), "stream destroy");
+}
+
 }  // namespace
 
 int main() {
@@ -365,6 +439,7 @@ int main() {
     prefill_cases();
     decode_cases();
     prologue_cases();
+    decode_step_cases();
     std::printf("%s: %d failure(s)\n", g_failures ? "FAILED" : "ALL PASS", g_failures);
     return g_failures ? 1 : 0;
 }

@@ -127,6 +127,31 @@ def test_prologue_op_validation():
     assert L.toyinfer_qk_norm_rope_bf16(P, P, P + 4, P, 1e-6, 4, 8, 128, None) == INVALID
 
 
+def test_decode_step_op_validation():
+    """Bad arguments of the decode-step pre-pass ops are rejected before any launch."""
+    assert L.toyinfer_rope_bf16(None, P, 3, 8, 128, None) == INVALID
+    assert L.toyinfer_rope_bf16(P + 2, P, 3, 8, 128, None) == INVALID      # rows move 16 B at a time
+    assert L.toyinfer_rope_bf16(P, P, 3, 0, 128, None) == INVALID
+    assert L.toyinfer_rope_bf16(P, P, 3, 8, 80, None) == UNSUPPORTED
+    assert L.toyinfer_rope_bf16_graph(P, P, None, 8, 128, None) == INVALID  # no device pos
+    assert L.toyinfer_rope_bf16_graph(P, None, P, 8, 128, None) == INVALID
+    w = L.toyinfer_write_kv_cache_bf16
+    assert w(P, P, P, 7, None) == INVALID          # odd kv_dim: the reference moves bf16 pairs
+    assert w(P, P, P, 0, None) == INVALID
+    assert w(P, P + 2, P, 8, None) == INVALID      # cache rows need 4-byte alignment
+    assert w(P, P, None, 8, None) == INVALID
+    f = L.toyinfer_decode_qkv_prologue_bf16
+    args = [P] * 7 + [64, 1e-6] + [P] * 3 + [32, 8, 128, None]
+    a = list(args); a[7] = 0
+    assert f(*a) == INVALID                        # empty cache
+    a = list(args); a[2] = None
+    assert f(*a) == INVALID                        # no v
+    a = list(args); a[10] = P + 8
+    assert f(*a) == INVALID                        # misaligned k_cache
+    a = list(args); a[14] = 80
+    assert f(*a) == UNSUPPORTED
+
+
 def test_python_wrapper_raises_on_bad_status():
     class Fake:
         def __init__(self, addr):

@@ -51,6 +51,11 @@ SIGNATURES = {
     "toyinfer_batch_multi_rmsnorm_bf16": (_i32, [_vp, _vp, _vp, _f32, _u32, _u32, _u32, _vp]),
     "toyinfer_batch_rope_bf16": (_i32, [_vp, _vp, _u32, _u32, _u32, _vp]),
     "toyinfer_qk_norm_rope_bf16": (_i32, [_vp, _vp, _vp, _vp, _f32, _u32, _u32, _u32, _vp]),
+    "toyinfer_rope_bf16": (_i32, [_vp, _vp, _u32, _u32, _u32, _vp]),
+    "toyinfer_rope_bf16_graph": (_i32, [_vp, _vp, _vp, _u32, _u32, _vp]),
+    "toyinfer_write_kv_cache_bf16": (_i32, [_vp, _vp, _vp, _u32, _vp]),
+    "toyinfer_decode_qkv_prologue_bf16": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _u32, _f32,
+                                                 _vp, _vp, _vp, _u32, _u32, _u32, _vp]),
 }
 
 
@@ -243,3 +248,35 @@ def qk_norm_rope_bf16(input, weight, output, inv_freq, rms_norm_eps: float, num_
            LIB.toyinfer_qk_norm_rope_bf16(_ptr(input), _ptr(weight), _ptr(output), _ptr(inv_freq),
                                           rms_norm_eps, num_tokens, nums_head, head_dim,
                                           _stream(stream)))
+
+
+def rope_bf16(qk, inv_freq, pos: int, nums_head: int, head_dim: int, stream=None) -> None:
+    _check("rope_bf16",
+           LIB.toyinfer_rope_bf16(_ptr(qk), _ptr(inv_freq), pos, nums_head, head_dim,
+                                  _stream(stream)))
+
+
+def rope_bf16_graph(qk, inv_freq, pos_d, nums_head: int, head_dim: int, stream=None) -> None:
+    _check("rope_bf16_graph",
+           LIB.toyinfer_rope_bf16_graph(_ptr(qk), _ptr(inv_freq), _ptr(pos_d), nums_head, head_dim,
+                                        _stream(stream)))
+
+
+def write_kv_cache_bf16(src, cache, pos_d, kv_dim: int, stream=None) -> None:
+    _check("write_kv_cache_bf16",
+           LIB.toyinfer_write_kv_cache_bf16(_ptr(src), _ptr(cache), _ptr(pos_d), kv_dim,
+                                            _stream(stream)))
+
+
+def decode_qkv_prologue_bf16(q, k, v, q_norm_weight, k_norm_weight, inv_freq, pos_d,
+                             max_seq_len: int, rms_norm_eps: float, q_out, k_cache, v_cache,
+                             num_q_heads: int, num_kv_heads: int, head_dim: int,
+                             stream=None) -> None:
+    """Fused decode-step pre-pass: q_norm+RoPE of q into q_out, k_norm+RoPE of k
+    into row *pos_d of k_cache, v into row *pos_d of v_cache (one launch)."""
+    _check("decode_qkv_prologue_bf16",
+           LIB.toyinfer_decode_qkv_prologue_bf16(
+               _ptr(q), _ptr(k), _ptr(v), _ptr(q_norm_weight), _ptr(k_norm_weight),
+               _ptr(inv_freq), _ptr(pos_d), max_seq_len, rms_norm_eps, _ptr(q_out),
+               _ptr(k_cache), _ptr(v_cache), num_q_heads, num_kv_heads, head_dim,
+               _stream(stream)))

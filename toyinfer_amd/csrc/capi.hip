@@ -357,4 +357,86 @@ int toyinfer_qk_norm_rope_bf16(const void* input, const void* weight, void* outp
                   kRowNorm | kRowRope, stream);
 }
 
+// ----------------------------------------------- decode-step pre-pass ops
+
+static int token_rows(const TokenRowsArgs& a, uint32_t head_dim, void* stream) {
+    if (head_dim != 64 && head_dim != 128) return TOYINFER_ERR_UNSUPPORTED;
+    return from_hip(launch_token_rows(a, head_dim, as_stream(stream)));
+}
+
+static bool rows_ok(const void* p) { return p && aligned(p, 16); }
+
+int toyinfer_rope_bf16(void* qk, const float* inv_freq, uint32_t pos, uint32_t nums_head,
+                       uint32_t head_dim, void* stream) {
+    if (nums_head == 0 || !rows_ok(qk) || !inv_freq || !aligned(inv_freq, 4))
+        return TOYINFER_ERR_INVALID_ARGUMENT;
+    TokenRowsArgs a;
+    a.q = static_cast<const uint16_t*>(qk);
+    a.q_out = static_cast<uint16_t*>(qk);
+    a.inv_freq = inv_freq;
+    a.pos_host = pos;
+    a.pos_cap = 0xffffffffu;
+    a.hq = nums_head;
+    a.q_mode = kRowRope;
+    return token_rows(a, head_dim, stream);
+}
+
+int toyinfer_rope_bf16_graph(void* qk, const float* inv_freq, const uint32_t* pos_d,
+                             uint32_t nums_head, uint32_t head_dim, void* stream) {
+    if (nums_head == 0 || !rows_ok(qk) || !inv_freq || !aligned(inv_freq, 4) || !pos_d ||
+        !aligned(pos_d, 4))
+        return TOYINFER_ERR_INVALID_ARGUMENT;
+    TokenRowsArgs a;
+    a.q = static_cast<const uint16_t*>(qk);
+    a.q_out = static_cast<uint16_t*>(qk);
+    a.inv_freq = inv_freq;
+    a.pos_d = pos_d;
+    a.pos_cap = 0xffffffffu;
+    a.hq = nums_head;
+    a.q_mode = kRowRope;
+    return token_rows(a, head_dim, stream);
+}
+
+int toyinfer_write_kv_cache_bf16(const void* src, void* cache, const uint32_t* pos_d,
+                                 uint32_t kv_dim, void* stream) {
+    if (!src || !cache || !pos_d || kv_dim == 0 || kv_dim % 2 != 0 || !aligned(src, 4) ||
+        !aligned(cache, 4) || !aligned(pos_d, 4))
+        return TOYINFER_ERR_INVALID_ARGUMENT;
+    return from_hip(launch_kv_row_copy(static_cast<const uint16_t*>(src),
+                                       static_cast<uint16_t*>(cache), pos_d, kv_dim,
+                                       as_stream(stream)));
+}
+
+int toyinfer_decode_qkv_prologue_bf16(const void* q, const void* k, const void* v,
+                                      const void* q_norm_weight, const void* k_norm_weight,
+                                      const float* inv_freq, const uint32_t* pos_d,
+                                      uint32_t max_seq_len, float rms_norm_eps, void* q_out,
+                                      void* k_cache, void* v_cache, uint32_t num_q_heads,
+                                      uint32_t num_kv_heads, uint32_t head_dim, void* stream) {
+    if (num_q_heads == 0 || num_kv_heads == 0 || max_seq_len == 0)
+        return TOYINFER_ERR_INVALID_ARGUMENT;
+    if (!rows_ok(q) || !rows_ok(k) || !rows_ok(v) || !rows_ok(q_norm_weight) ||
+        !rows_ok(k_norm_weight) || !rows_ok(q_out) || !rows_ok(k_cache) || !rows_ok(v_cache) ||
+        !inv_freq || !aligned(inv_freq, 4) || !pos_d || !aligned(pos_d, 4))
+        return TOYINFER_ERR_INVALID_ARGUMENT;
+    TokenRowsArgs a;
+    a.q = static_cast<const uint16_t*>(q);
+    a.q_out = static_cast<uint16_t*>(q_out);
+    a.q_weight = static_cast<const uint16_t*>(q_norm_weight);
+    a.k = static_cast<const uint16_t*>(k);
+    a.k_cache = static_cast<uint16_t*>(k_cache);
+    a.k_weight = static_cast<const uint16_t*>(k_norm_weight);
+    a.v = static_cast<const uint16_t*>(v);
+    a.v_cache = static_cast<uint16_t*>(v_cache);
+    a.inv_freq = inv_freq;
+    a.pos_d = pos_d;
+    a.pos_cap = max_seq_len;
+    a.eps = rms_norm_eps;
+    a.hq = num_q_heads;
+    a.hkv = num_kv_heads;
+    a.q_mode = kRowNorm | kRowRope;
+    a.k_mode = kRowNorm | kRowRope;
+    return token_rows(a, head_dim, stream);
+}
+
 }  // extern "C"

@@ -87,5 +87,29 @@ hipError_t launch_row_norm_rope(const uint16_t* in, uint16_t* out, const uint16_
                                 hipStream_t stream);
 hipError_t launch_rope_table(float* table, const float* inv_freq, uint32_t num_pos, uint32_t d,
                              hipStream_t stream);
+// One decoded token's rows at a single position (device pos_d, else
+// pos_host; clamped below pos_cap): query heads transformed in place or to
+// q_out, key heads transformed into row pos of k_cache, value heads copied
+// into row pos of v_cache.  hq or hkv may be 0.
+struct TokenRowsArgs {
+    const uint16_t* q = nullptr;
+    uint16_t* q_out = nullptr;
+    const uint16_t* q_weight = nullptr;
+    const uint16_t* k = nullptr;
+    uint16_t* k_cache = nullptr;
+    const uint16_t* k_weight = nullptr;
+    const uint16_t* v = nullptr;
+    uint16_t* v_cache = nullptr;
+    const float* inv_freq = nullptr;
+    const uint32_t* pos_d = nullptr;
+    uint32_t pos_host = 0, pos_cap = 1;
+    float eps = 0.0f;
+    uint32_t hq = 0, hkv = 0;
+    int q_mode = 0, k_mode = 0;
+};
+hipError_t launch_token_rows(const TokenRowsArgs& a, uint32_t d, hipStream_t stream);
+// kv_dim (even) values from src to cache + (*pos_d) * kv_dim.
+hipError_t launch_kv_row_copy(const uint16_t* src, uint16_t* cache, const uint32_t* pos_d,
+                              uint32_t kv_dim, hipStream_t stream);
 
 }  // namespace tiattn

@@ -40,30 +40,34 @@ __global__ void rope_table_kernel(float2* table, const float* __restrict__ inv_f
     table[e] = make_float2(cs, sn);
 }
 
+// One D-element row handled by its LPR = D/16 lanes (lane c of the row owns
+// the RoPE pairs (8c + k, 8c + k + D/2), k < 8): mode bit kRowNorm applies
+// RMSNorm with `weight`, bit kRowRope RoPE at position t (angles from `table`
+// row t when non-null, else sincosf(t * inv_freq[i])); mode 0 copies the row
+// bit for bit.  in and out may alias.  All LPR lanes of the row must call it
+// (the sum of squares is reduced across them).
 template <int D>
-__global__ __launch_bounds__(256) void row_norm_rope_kernel(const uint16_t* in, uint16_t* out,
-                                                            const uint16_t* __restrict__ weight,
-                                                            const float* __restrict__ inv_freq,
-                                                            const float2* __restrict__ table,
-                                                            float eps, uint32_t rows,
-                                                            uint32_t nums_head, int mode) {
+__device__ __forceinline__ void norm_rope_row(const uint16_t* in, uint16_t* out,
+                                              const uint16_t* __restrict__ weight,
+                                              const float* __restrict__ inv_freq,
+                                              const float2* __restrict__ table, float eps,
+                                              uint32_t t, int c, int mode) {
 #pragma clang fp contract(off)
     constexpr int HALF = D / 2;
-    constexpr int LPR = HALF / 8;     // lanes per row; a lane owns the 8 pairs (8c + k, 8c + k + D/2)
-    constexpr int RPB = 256 / LPR;    // rows per block
-    const uint32_t row = blockIdx.x * RPB + threadIdx.x / LPR;
-    const int c = threadIdx.x % LPR;
-    if (row >= rows) return;  // the LPR lanes of a row exit together
-    const int64_t off = (int64_t)row * D + 8 * c;
+    constexpr int LPR = HALF / 8;
     // Every load goes out before the first use.
-    const uint4 xr = ldg16(in + off), xi = ldg16(in + off + HALF);
+    const uint4 xr = ldg16(in + 8 * c), xi = ldg16(in + 8 * c + HALF);
+    if (mode == 0) {
+        *reinterpret_cast<uint4*>(out + 8 * c) = xr;
+        *reinterpret_cast<uint4*>(out + 8 * c + HALF) = xi;
+        return;
+    }
     uint4 wr = make_uint4(0, 0, 0, 0), wi = wr;
     if (mode & kRowNorm) {
         wr = ldg16(weight + 8 * c);
         wi = ldg16(weight + 8 * c + HALF);
     }
     float4 cs[4];
-    const uint32_t t = row / nums_head;
     if ((mode & kRowRope) && table) {
         const float4* tp = reinterpret_cast<const float4*>(table + (uint64_t)t * HALF + 8 * c);
 #pragma unroll
@@ -127,8 +131,88 @@ __global__ __launch_bounds__(256) void row_norm_rope_kernel(const uint16_t* in, 
     oi.y = pack_bf16x2(im[2], im[3]);
     oi.z = pack_bf16x2(im[4], im[5]);
     oi.w = pack_bf16x2(im[6], im[7]);
-    *reinterpret_cast<uint4*>(out + off) = orr;
-    *reinterpret_cast<uint4*>(out + off + HALF) = oi;
+    *reinterpret_cast<uint4*>(out + 8 * c) = orr;
+    *reinterpret_cast<uint4*>(out + 8 * c + HALF) = oi;
+}
+
+// Rows (token, head) of a token-major [tokens][nums_head][D] tensor; RoPE
+// position = row / nums_head.
+template <int D>
+__global__ __launch_bounds__(256) void row_norm_rope_kernel(const uint16_t* in, uint16_t* out,
+                                                            const uint16_t* __restrict__ weight,
+                                                            const float* __restrict__ inv_freq,
+                                                            const float2* __restrict__ table,
+                                                            float eps, uint32_t rows,
+                                                            uint32_t nums_head, int mode) {
+    constexpr int LPR = D / 16;
+    constexpr int RPB = 256 / LPR;  // rows per block
+    const uint32_t row = blockIdx.x * RPB + threadIdx.x / LPR;
+    if (row >= rows) return;  // the LPR lanes of a row exit together
+    const int64_t off = (int64_t)row * D;
+    norm_rope_row<D>(in + off, out + off, weight, inv_freq, table, eps, row / nums_head,
+                     threadIdx.x % LPR, mode);
+}
+
+// One decoded token at position pos = min(*pos_d or pos_host, pos_cap - 1):
+// rows [0, hq) are its query heads (q -> q_out, q_mode), rows
+// [hq, hq + hkv) its key heads (k -> row pos of k_cache, k_mode), rows
+// [hq + hkv, hq + 2*hkv) its value heads (v -> row pos of v_cache, copied).
+// Caches are [positions][hkv][D].
+struct TokenRows {
+    const uint16_t* q;
+    uint16_t* q_out;
+    const uint16_t* q_weight;
+    const uint16_t* k;
+    uint16_t* k_cache;
+    const uint16_t* k_weight;
+    const uint16_t* v;
+    uint16_t* v_cache;
+    const float* inv_freq;
+    const uint32_t* pos_d;
+    uint32_t pos_host, pos_cap;
+    float eps;
+    uint32_t hq, hkv;
+    int q_mode, k_mode;
+};
+
+template <int D>
+__global__ __launch_bounds__(256) void token_rows_kernel(TokenRows a) {
+    constexpr int LPR = D / 16;
+    constexpr int RPB = 256 / LPR;
+    const uint32_t row = blockIdx.x * RPB + threadIdx.x / LPR;
+    if (row >= a.hq + 2 * a.hkv) return;
+    uint32_t pos = a.pos_d ? *a.pos_d : a.pos_host;
+    pos = min(pos, a.pos_cap - 1);
+    const int c = threadIdx.x % LPR;
+    if (row < a.hq) {
+        norm_rope_row<D>(a.q + (int64_t)row * D, a.q_out + (int64_t)row * D, a.q_weight, a.inv_freq,
+                         nullptr, a.eps, pos, c, a.q_mode);
+    } else if (row < a.hq + a.hkv) {
+        const uint32_t j = row - a.hq;
+        norm_rope_row<D>(a.k + (int64_t)j * D, a.k_cache + ((int64_t)pos * a.hkv + j) * D,
+                         a.k_weight, a.inv_freq, nullptr, a.eps, pos, c, a.k_mode);
+    } else {
+        const uint32_t j = row - a.hq - a.hkv;
+        norm_rope_row<D>(a.v + (int64_t)j * D, a.v_cache + ((int64_t)pos * a.hkv + j) * D, nullptr,
+                         nullptr, nullptr, 0.0f, pos, c, 0);
+    }
+}
+
+// Reference write_kv_cache_bf16 (src/decode.cu:374-397): kv_dim values to
+// cache + pos * kv_dim, bf16 pairs (kv_dim even), 16 bytes per lane where
+// both ends are 16-byte aligned.
+__global__ __launch_bounds__(256) void kv_row_copy_kernel(const uint16_t* __restrict__ src,
+                                                          uint16_t* __restrict__ cache,
+                                                          const uint32_t* __restrict__ pos_d,
+                                                          uint32_t kv_dim, int vec16) {
+    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    uint16_t* dst = cache + (int64_t)(*pos_d) * kv_dim;
+    if (vec16) {
+        if (8 * i < kv_dim)
+            *reinterpret_cast<uint4*>(dst + 8 * i) = *reinterpret_cast<const uint4*>(src + 8 * i);
+    } else if (2 * i < kv_dim) {
+        *reinterpret_cast<uint32_t*>(dst + 2 * i) = *reinterpret_cast<const uint32_t*>(src + 2 * i);
+    }
 }
 
 }  // namespace
@@ -145,6 +229,33 @@ hipError_t launch_rope_table(float* table, const float* inv_freq, uint32_t num_p
     const uint64_t n = (uint64_t)num_pos * (d / 2);
     hipLaunchKernelGGL(rope_table_kernel, dim3((uint32_t)((n + 255) / 256)), dim3(256), 0, stream,
                        reinterpret_cast<float2*>(table), inv_freq, num_pos, (int)(d / 2));
+    return hipGetLastError();
+}
+
+hipError_t launch_token_rows(const TokenRowsArgs& a, uint32_t d, hipStream_t stream) {
+    TokenRows k{};
+    k.q = a.q; k.q_out = a.q_out; k.q_weight = a.q_weight;
+    k.k = a.k; k.k_cache = a.k_cache; k.k_weight = a.k_weight;
+    k.v = a.v; k.v_cache = a.v_cache;
+    k.inv_freq = a.inv_freq; k.pos_d = a.pos_d; k.pos_host = a.pos_host; k.pos_cap = a.pos_cap;
+    k.eps = a.eps; k.hq = a.hq; k.hkv = a.hkv; k.q_mode = a.q_mode; k.k_mode = a.k_mode;
+    const uint32_t rows = a.hq + 2 * a.hkv;
+    const uint32_t rows_per_block = 256 / (d / 16);
+    const dim3 grid((rows + rows_per_block - 1) / rows_per_block);
+    if (d == 64)
+        hipLaunchKernelGGL(token_rows_kernel<64>, grid, dim3(256), 0, stream, k);
+    else
+        hipLaunchKernelGGL(token_rows_kernel<128>, grid, dim3(256), 0, stream, k);
+    return hipGetLastError();
+}
+
+hipError_t launch_kv_row_copy(const uint16_t* src, uint16_t* cache, const uint32_t* pos_d,
+                              uint32_t kv_dim, hipStream_t stream) {
+    const bool vec16 = kv_dim % 8 == 0 && reinterpret_cast<uintptr_t>(src) % 16 == 0 &&
+                       reinterpret_cast<uintptr_t>(cache) % 16 == 0;
+    const uint32_t lanes = vec16 ? kv_dim / 8 : kv_dim / 2;
+    hipLaunchKernelGGL(kv_row_copy_kernel, dim3((lanes + 255) / 256), dim3(256), 0, stream, src,
+                       cache, pos_d, kv_dim, vec16 ? 1 : 0);
     return hipGetLastError();
 }
 

@@ -517,6 +517,104 @@ uint32_t split_slots(uint32_t d) {
     return (uint32_t)v;
 }
 
+// Reference contract, split partials in the score rows (two or more
+// splits): the score rows hold partials until every head is merged, so the
+// work is three stream-ordered kernels after the split pass.
+//  1. decode_compat_merge_kernel (block = head): merges the head's partials,
+//     writes O_buffer, and leaves (M, 1/den) in the first 8 bytes of the
+//     head's O row (O is written last).
+//  2. decode_compat_score_kernel (block = 256 positions of one KV head):
+//     p = 2^(s*log2e/sqrt(D) - M) / den for its positions and all query
+//     heads of the group (s recomputed from Q and K), zeros past the
+//     length, over the whole score row.
+//  3. decode_compat_out_kernel: O = bf16(O_buffer).
+__device__ __forceinline__ void stash_put(uint16_t* o_row, float a, float b) {
+    const uint32_t ua = __float_as_uint(a), ub = __float_as_uint(b);
+    o_row[0] = (uint16_t)(ua & 0xffffu);
+    o_row[1] = (uint16_t)(ua >> 16);
+    o_row[2] = (uint16_t)(ub & 0xffffu);
+    o_row[3] = (uint16_t)(ub >> 16);
+}
+__device__ __forceinline__ float2 stash_get(const uint16_t* o_row) {
+    return make_float2(__uint_as_float((uint32_t)o_row[0] | ((uint32_t)o_row[1] << 16)),
+                       __uint_as_float((uint32_t)o_row[2] | ((uint32_t)o_row[3] << 16)));
+}
+
+template <int D>
+__global__ __launch_bounds__(kCombineThreads) void decode_compat_merge_kernel(
+    DecodeProblem p, DecodePartials part, float* o_buffer, uint16_t* o) {
+    const uint32_t h = blockIdx.x;
+    float M, den;
+    const float my_o = merge_splits<D>(part, h, p.splits, &M, &den);
+    if (threadIdx.x < D) o_buffer[(int64_t)h * D + threadIdx.x] = my_o;
+    if (threadIdx.x == 0)
+        stash_put(o + (int64_t)h * D, M == -INFINITY ? 0.0f : M, den > 0.0f ? 1.0f / den : 0.0f);
+}
+
+constexpr int kScoreRows = 256;  // positions per score block (one per thread)
+
+template <int D>
+__global__ __launch_bounds__(kScoreRows) void decode_compat_score_kernel(
+    DecodeProblem p, float* score, uint32_t msl, const uint16_t* o, float scale_log2) {
+    constexpr int MAXG = 16;
+    __shared__ float s_q[MAXG][D];
+    __shared__ float s_st[MAXG][2];
+    const uint32_t group = p.hq / p.hkv;
+    const uint32_t kvh = blockIdx.y;
+    const uint32_t L = seq_length(p, 0);
+    const uint32_t t = blockIdx.x * kScoreRows + threadIdx.x;
+    for (uint32_t g0 = 0; g0 < group; g0 += MAXG) {
+        const uint32_t ng = min((uint32_t)MAXG, group - g0);
+        const uint32_t h0 = kvh * group + g0;
+        __syncthreads();  // the previous head block's LDS reads are done
+        for (uint32_t e = threadIdx.x; e < ng * D; e += kScoreRows)
+            s_q[e / D][e % D] = bf16_to_f32(p.q[(int64_t)h0 * D + e]);
+        if (threadIdx.x < ng) {
+            const float2 st = stash_get(o + (int64_t)(h0 + threadIdx.x) * D);
+            s_st[threadIdx.x][0] = st.x;
+            s_st[threadIdx.x][1] = st.y;
+        }
+        __syncthreads();
+        if (t >= msl) continue;
+        float dot[MAXG];
+#pragma unroll
+        for (int g = 0; g < MAXG; ++g) dot[g] = 0.0f;
+        if (t < L) {
+            const uint16_t* kr = p.k + ((int64_t)t * p.hkv + kvh) * D;
+#pragma unroll 2
+            for (int c = 0; c < D / 8; ++c) {
+                const uint4 w = ldg16(kr + 8 * c);
+                float kv[8];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    kv[2 * e] = bf16_lo(word_of(w, e));
+                    kv[2 * e + 1] = bf16_hi(word_of(w, e));
+                }
+#pragma unroll
+                for (int g = 0; g < MAXG; ++g) {
+                    if ((uint32_t)g < ng) {
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) dot[g] = fmaf(s_q[g][8 * c + e], kv[e], dot[g]);
+                    }
+                }
+            }
+        }
+#pragma unroll
+        for (int g = 0; g < MAXG; ++g) {
+            if ((uint32_t)g < ng)
+                score[(int64_t)(h0 + g) * msl + t] =
+                    t < L ? __builtin_amdgcn_exp2f(fmaf(dot[g], scale_log2, -s_st[g][0])) * s_st[g][1]
+                          : 0.0f;
+        }
+    }
+}
+
+__global__ __launch_bounds__(256) void decode_compat_out_kernel(const float* o_buffer, uint16_t* o,
+                                                                uint32_t n) {
+    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) o[i] = f32_to_bf16(o_buffer[i]);
+}
+
 }  // namespace
 
 uint32_t decode_head_groups(uint32_t group) {
@@ -566,6 +664,26 @@ hipError_t launch_decode_finalize_compat(const DecodeProblem& p, const DecodePar
                                          uint16_t* o, hipStream_t stream) {
     const dim3 grid(p.hq);
     const float sl2 = kLog2e / sqrtf((float)p.d);
+    if (p.splits >= 2) {
+        // Partials in the score rows: merge, score pass, O (see the kernels).
+        if (p.d == 64)
+            hipLaunchKernelGGL(decode_compat_merge_kernel<64>, grid, dim3(kCombineThreads), 0,
+                               stream, p, part, o_buffer, o);
+        else
+            hipLaunchKernelGGL(decode_compat_merge_kernel<128>, grid, dim3(kCombineThreads), 0,
+                               stream, p, part, o_buffer, o);
+        const dim3 sgrid((msl + kScoreRows - 1) / kScoreRows, p.hkv);
+        if (p.d == 64)
+            hipLaunchKernelGGL(decode_compat_score_kernel<64>, sgrid, dim3(kScoreRows), 0, stream,
+                               p, score, msl, o, sl2);
+        else
+            hipLaunchKernelGGL(decode_compat_score_kernel<128>, sgrid, dim3(kScoreRows), 0, stream,
+                               p, score, msl, o, sl2);
+        const uint32_t n = p.hq * p.d;
+        hipLaunchKernelGGL(decode_compat_out_kernel, dim3((n + 255) / 256), dim3(256), 0, stream,
+                           o_buffer, o, n);
+        return hipGetLastError();
+    }
     if (p.d == 64)
         hipLaunchKernelGGL(decode_finalize_compat_kernel<64>, grid, dim3(kCombineThreads), 0,
                            stream, p, part, score, msl, o_buffer, o, sl2);

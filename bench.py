@@ -54,7 +54,7 @@ def traffic_bytes(workload):
     r, w = PMC_KIB[workload]
     return int(round((r * FETCH_SCALE + w * WRITE_SCALE) * 1024))
 WORKLOADS = ("all", "prefill", "prefill_fused", "decode_b8_l4096", "decode_b1_l32768",
-             "decode_step", "copy_calibration")
+             "decode_step", "decode_contract", "copy_calibration")
 
 
 def causal_flops(s, hq, d):
@@ -243,6 +243,41 @@ def bench_decode_step(dev, stream, steps, warmup, hq=32, hkv=8, d=128, msl=40960
                     "six_op_sequence_us = the reference's six launches through this library"}
 
 
+def bench_decode_contract(dev, stream, steps, warmup, hq=32, hkv=8, d=128, msl=40960, pos=32767,
+                          per_graph=10):
+    """The reference-contract decode the engine calls (attention_bf16_graph:
+    device position, score/O_buffer/O outputs, captured in a graph) at a 32k
+    position of a 40960-row cache; each replay runs `per_graph` calls."""
+    import torch
+
+    from toyinfer_amd import attn, synth
+
+    k = to_dev(synth.normal_bf16(SEED + 30, "k", (msl, hkv, d)), dev)
+    v = to_dev(synth.normal_bf16(SEED + 30, "v", (msl, hkv, d)), dev)
+    q = to_dev(synth.normal_bf16(SEED + 30, "q", (hq, d)), dev)
+    score = torch.empty((hq, msl), dtype=torch.float32, device=dev)
+    ob = torch.empty((hq, d), dtype=torch.float32, device=dev)
+    o = torch.empty((hq, d), dtype=torch.bfloat16, device=dev)
+    pos_d = torch.tensor([pos], dtype=torch.int32, device=dev)
+    with torch.cuda.stream(stream):
+        attn.attention_bf16_graph(q, k, v, score, ob, o, hq, hkv, d, pos_d, msl, stream)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        for _ in range(per_graph):
+            attn.attention_bf16_graph(q, k, v, score, ob, o, hq, hkv, d, pos_d, msl, stream)
+    ms = time_steps(lambda i: graph.replay(), max(5, steps // per_graph), warmup, stream) / per_graph
+    kv_bytes = 2.0 * (pos + 1) * hkv * d * 2
+    gbs = kv_bytes / (ms * 1e-3) / 1e9
+    return {"workload": f"decode_contract_graph_msl{msl}_pos{pos}_hq{hq}_hkv{hkv}_d{d}",
+            "entry": "toyinfer_attention_bf16_graph", "steps": steps,
+            "ms_per_step": round(ms, 5), "value": round(gbs, 1), "unit": "GB/s",
+            "note": "KV bytes attended per call / call time; the call also writes the "
+                    f"{hq}x{msl} fp32 probability rows the contract requires (re-reading K "
+                    "for them), O_buffer and O",
+            "roofline": roofline("hbm", gbs, PEAK_HBM_GBS, "GB/s")}
+
+
 def bench_copy(dev, stream, steps, warmup, mib=256):
     """Device-to-device copy of `mib` MiB: a kernel with known HBM traffic (mib
     read + mib written per launch), the scale for the FETCH_SIZE / WRITE_SIZE
@@ -311,6 +346,8 @@ def main():
                "decode_b1_l32768": lambda: bench_decode(dev, stream, args.steps, args.warmup,
                                                         b=1, L=32768),
                "decode_step": lambda: bench_decode_step(dev, stream, args.steps, args.warmup),
+               "decode_contract": lambda: bench_decode_contract(dev, stream, args.steps,
+                                                                args.warmup),
                "copy_calibration": lambda: bench_copy(dev, stream, args.steps, args.warmup)}
         print(json.dumps(one[args.workload]()), flush=True)
         return
@@ -333,6 +370,7 @@ def main():
         comps.append(bench_decode(dev, stream, max(50, args.steps * 2), 10, b=8, L=4096))
         comps.append(bench_decode(dev, stream, max(50, args.steps * 2), 10, b=1, L=32768))
         comps.append(bench_decode_step(dev, stream, max(50, args.steps * 2), 10))
+        comps.append(bench_decode_contract(dev, stream, max(50, args.steps * 2), 2))
         line["components"] = comps
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(host_inputs, gpu_out, args.cpu_seconds)

@@ -14,7 +14,11 @@ the north-star targets name, each with its own roofline block:
   * prefill_fused_s8192: configs[3], S=8192, 32/8, QK-RMSNorm + RoPE fused
     in front (toyinfer_prefill_qknorm_rope_attention_bf16), MFMA-bound;
   * decode_b8_l4096: configs[2], split-K decode over 128 MiB of KV, HBM-bound;
-  * decode_b1_l32768: the north-star 32k-token decode, 128 MiB of KV.
+  * decode_b1_l32768: the north-star 32k-token decode, 128 MiB of KV;
+  * decode_step / decode_contract: the decode-step pre-pass and the
+    reference-contract graph decode;
+  * proj_gemv / proj_gemm: the projections either side of attention (lm-head
+    GEMV, HBM-bound; a 4096-token prefill projection, MFMA-bound).
 Decode steps rotate over 4 independent KV sets (512 MiB) so every step reads
 KV that is not resident in the 256 MB Infinity Cache.
 
@@ -54,7 +58,7 @@ def traffic_bytes(workload):
     r, w = PMC_KIB[workload]
     return int(round((r * FETCH_SCALE + w * WRITE_SCALE) * 1024))
 WORKLOADS = ("all", "prefill", "prefill_fused", "decode_b8_l4096", "decode_b1_l32768",
-             "decode_step", "decode_contract", "copy_calibration")
+             "decode_step", "decode_contract", "proj_gemv", "proj_gemm", "copy_calibration")
 
 
 def causal_flops(s, hq, d):
@@ -278,6 +282,50 @@ def bench_decode_contract(dev, stream, steps, warmup, hq=32, hkv=8, d=128, msl=4
             "roofline": roofline("hbm", gbs, PEAK_HBM_GBS, "GB/s")}
 
 
+def bench_proj_gemv(dev, stream, steps, warmup, M=151936, N=4096):
+    """The lm-head projection of one decoded token (gemv_proj_bf162float,
+    src/transformer.cpp:630) at Qwen3-8B's vocabulary x hidden size: 1.16 GiB
+    of bf16 weights streamed once per call, HBM-bound."""
+    import torch
+
+    from toyinfer_amd import attn
+
+    g = torch.Generator(device=dev).manual_seed(SEED + 40)
+    w = torch.randn((M, N), generator=g, device=dev).to(torch.bfloat16)
+    x = torch.randn((N,), generator=g, device=dev).to(torch.bfloat16)
+    y = torch.empty((M,), dtype=torch.float32, device=dev)
+    ms = time_steps(lambda i: attn.gemv_proj_bf162float(w, x, y, M, N, stream), steps, warmup,
+                    stream)
+    nbytes = 2.0 * M * N + 2.0 * N + 4.0 * M
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    return {"workload": f"proj_gemv_lmhead_m{M}_n{N}", "entry": "toyinfer_gemv_proj_bf162float",
+            "steps": steps, "ms_per_step": round(ms, 5), "value": round(gbs, 1), "unit": "GB/s",
+            "note": "weights + x read, fp32 y written, per call / call time",
+            "roofline": roofline("hbm", gbs, PEAK_HBM_GBS, "GB/s")}
+
+
+def bench_proj_gemm(dev, stream, steps, warmup, T=4096, M=4096, N=4096):
+    """A prefill projection (batch_gemv_proj_bf16, src/transformer.cpp:370-378)
+    over 4096 tokens of Qwen3-8B's hidden size: the MFMA GEMM.  The note
+    carries torch.matmul (hipBLASLt) on the same operands for scale."""
+    import torch
+
+    from toyinfer_amd import attn
+
+    g = torch.Generator(device=dev).manual_seed(SEED + 41)
+    w = torch.randn((M, N), generator=g, device=dev).to(torch.bfloat16)
+    x = torch.randn((T, N), generator=g, device=dev).to(torch.bfloat16)
+    y = torch.empty((T, M), dtype=torch.bfloat16, device=dev)
+    ms = time_steps(lambda i: attn.batch_gemv_proj_bf16(w, x, y, T, M, N, stream), steps, warmup,
+                    stream)
+    ms_lib = time_steps(lambda i: torch.matmul(x, w.t()), steps, warmup, stream)
+    tf = 2.0 * T * M * N / (ms * 1e-3) / 1e12
+    return {"workload": f"proj_gemm_t{T}_m{M}_n{N}", "entry": "toyinfer_batch_gemv_proj_bf16",
+            "steps": steps, "ms_per_step": round(ms, 5), "value": round(tf, 1),
+            "unit": "TFLOP/s", "torch_matmul_tflops": round(2.0 * T * M * N / (ms_lib * 1e-3) / 1e12, 1),
+            "roofline": roofline("mfma", tf, PEAK_BF16_TFLOPS, "TFLOP/s")}
+
+
 def bench_copy(dev, stream, steps, warmup, mib=256):
     """Device-to-device copy of `mib` MiB: a kernel with known HBM traffic (mib
     read + mib written per launch), the scale for the FETCH_SIZE / WRITE_SIZE
@@ -348,6 +396,8 @@ def main():
                "decode_step": lambda: bench_decode_step(dev, stream, args.steps, args.warmup),
                "decode_contract": lambda: bench_decode_contract(dev, stream, args.steps,
                                                                 args.warmup),
+               "proj_gemv": lambda: bench_proj_gemv(dev, stream, args.steps, args.warmup),
+               "proj_gemm": lambda: bench_proj_gemm(dev, stream, args.steps, args.warmup),
                "copy_calibration": lambda: bench_copy(dev, stream, args.steps, args.warmup)}
         print(json.dumps(one[args.workload]()), flush=True)
         return
@@ -371,6 +421,8 @@ def main():
         comps.append(bench_decode(dev, stream, max(50, args.steps * 2), 10, b=1, L=32768))
         comps.append(bench_decode_step(dev, stream, max(50, args.steps * 2), 10))
         comps.append(bench_decode_contract(dev, stream, max(50, args.steps * 2), 2))
+        comps.append(bench_proj_gemv(dev, stream, max(50, args.steps), 10))
+        comps.append(bench_proj_gemm(dev, stream, max(200, args.steps), 50))
         line["components"] = comps
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(host_inputs, gpu_out, args.cpu_seconds)

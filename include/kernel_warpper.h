@@ -169,6 +169,37 @@ void write_kv_cache_bf16(const bf16* __restrict__ src, bf16* __restrict__ cache,
                    "write_kv_cache_bf16");
 }
 
+// include/kernel_warpper.h:53-57: y = W * hidden_states, bf16 out.
+// NUM_THREADS does not change the kernel.
+template <const uint32_t NUM_THREADS>
+void gemv_proj_bf16(const bf16* __restrict__ W, const bf16* __restrict__ hidden_states,
+                    bf16* __restrict__ y, const uint32_t M, const uint32_t N,
+                    hipStream_t stream_d = nullptr) {
+    static_assert(NUM_THREADS > 0 && NUM_THREADS <= 1024, "illegal launch shape");
+    TOYINFER_CHECK(toyinfer_gemv_proj_bf16(W, hidden_states, y, M, N, stream_d),
+                   "gemv_proj_bf16");
+}
+
+// include/kernel_warpper.h:59-64: num_tokens rows of hidden_states.
+template <const uint32_t NUM_THREADS>
+void batch_gemv_proj_bf16(const bf16* __restrict__ W, const bf16* __restrict__ hidden_states,
+                          bf16* __restrict__ y, const uint32_t num_tokens, const uint32_t M,
+                          const uint32_t N, hipStream_t stream_d = nullptr) {
+    static_assert(NUM_THREADS > 0 && NUM_THREADS <= 1024, "illegal launch shape");
+    TOYINFER_CHECK(toyinfer_batch_gemv_proj_bf16(W, hidden_states, y, num_tokens, M, N, stream_d),
+                   "batch_gemv_proj_bf16");
+}
+
+// include/kernel_warpper.h:66-70: fp32 out (the lm-head).
+template <const uint32_t NUM_THREADS>
+void gemv_proj_bf162float(const bf16* __restrict__ W, const bf16* __restrict__ hidden_states,
+                          float* __restrict__ y, const uint32_t M, const uint32_t N,
+                          hipStream_t stream_d = nullptr) {
+    static_assert(NUM_THREADS > 0 && NUM_THREADS <= 1024, "illegal launch shape");
+    TOYINFER_CHECK(toyinfer_gemv_proj_bf162float(W, hidden_states, y, M, N, stream_d),
+                   "gemv_proj_bf162float");
+}
+
 // ------------------------------------------------------------- extensions
 // Entry points with no counterpart in the reference: batched split-K decode,
 // the prefill with QK-RMSNorm + RoPE fused in front, and the decode step's

@@ -193,6 +193,30 @@ int toyinfer_decode_qkv_prologue_bf16(const void* q, const void* k, const void* 
                                       void* k_cache, void* v_cache, uint32_t num_q_heads,
                                       uint32_t num_kv_heads, uint32_t head_dim, void* stream);
 
+/* ---- Projections (the attention path's producers and consumer) ----
+ * W is [M][N] bf16 row-major, x is [num_tokens][N] bf16, y[t][m] =
+ * sum_n W[m][n] * x[t][n] accumulated in fp32 and rounded once.  Only
+ * y[0 .. num_tokens * M) is written.  M, N, num_tokens >= 1, N <= 2^22;
+ * pointers aligned to their element size (16-byte alignment and
+ * N % 8 == 0 select the vector path). */
+
+/* Decode projection, bf16 out.  Replaces toyinfer::gemv_proj_bf16<NUM_THREADS>
+ * (include/kernel_warpper.h:53-57; src/decode.cu:201-248). */
+int toyinfer_gemv_proj_bf16(const void* W, const void* hidden_states, void* y, uint32_t M,
+                            uint32_t N, void* stream);
+/* Decode projection, fp32 out (the lm-head).  Replaces
+ * toyinfer::gemv_proj_bf162float<NUM_THREADS> (include/kernel_warpper.h:66-70;
+ * src/decode.cu:250-298). */
+int toyinfer_gemv_proj_bf162float(const void* W, const void* hidden_states, float* y,
+                                  uint32_t M, uint32_t N, void* stream);
+/* Prefill projection over num_tokens rows, bf16 out: an MFMA GEMM when
+ * num_tokens > 4, N % 64 == 0 and W and hidden_states are 16-byte aligned,
+ * else the GEMV over groups of 4 tokens.  Replaces
+ * toyinfer::batch_gemv_proj_bf16<NUM_THREADS> (include/kernel_warpper.h:59-64;
+ * src/prefill.cu:124-174). */
+int toyinfer_batch_gemv_proj_bf16(const void* W, const void* hidden_states, void* y,
+                                  uint32_t num_tokens, uint32_t M, uint32_t N, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -67,6 +67,9 @@ def _load() -> ctypes.CDLL:
         "or_rope": (None, [_f32p, _f32p, _u32, _u32, _u32, _u32]),
         "or_inv_freq": (None, [_f32p, ctypes.c_int, _f32]),
         "or_qk_norm_rope": (None, [_f32p, _f32p, _f32p, _u32, _u32, _u32, _f32]),
+        "or_make_gemv_case": (None, [_u32, _u32, _f32, _f32, _f32p, _f32p]),
+        "or_make_batch_gemv_case": (None, [_u32, _u32, _u32, _f32, _f32, _f32p, _f32p]),
+        "or_gemv": (None, [_f32p, _f32p, _f32p, _u32, _u32, _u32, ctypes.c_int]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -277,3 +280,33 @@ def qk_norm_rope(x, gamma, inv_freq_arr, eps):
     out = _c32(x).copy()
     lib().or_qk_norm_rope(out.reshape(-1), _c32(gamma), _c32(inv_freq_arr), t, h, d, eps)
     return out
+
+
+# ----------------------------------------------------------- projections
+
+def make_gemv_case(M, N, x_phase, w_phase):
+    """tests/gemv_test_common.h:24-50 -> (x [N], w [M][N]) float."""
+    x = np.empty(N, np.float32)
+    w = np.empty((M, N), np.float32)
+    lib().or_make_gemv_case(M, N, x_phase, w_phase, x, w.reshape(-1))
+    return x, w
+
+
+def make_batch_gemv_case(batch, M, N, hidden_phase, w_phase):
+    """tests/test_batch_gemv_proj_bf16.cu:20-50 -> (hidden [B][N], w [M][N])."""
+    x = np.empty((batch, N), np.float32)
+    w = np.empty((M, N), np.float32)
+    lib().or_make_batch_gemv_case(batch, M, N, hidden_phase, w_phase, x.reshape(-1),
+                                  w.reshape(-1))
+    return x, w
+
+
+def gemv(w, x, nthreads: int = 0):
+    """y[t][m] = sum_n w[m][n] x[t][n] in float, in n order; x [N] or [T][N]."""
+    w = _c32(w)
+    x = _c32(x)
+    M, N = w.shape
+    tokens = x.size // N
+    y = np.empty(tokens * M, np.float32)
+    lib().or_gemv(w.reshape(-1), x.reshape(-1), y, tokens, M, N, nthreads)
+    return y.reshape(x.shape[:-1] + (M,)) if x.ndim > 1 else y

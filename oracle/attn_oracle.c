@@ -22,6 +22,9 @@
  *   RoPE ................. tests/rope_test_common.h:23-65 (single position)
  *                          src/prefill.cu:185-208 (batched: angle = token*f)
  *   inverse frequencies .. tests/precompute_freq_test_common.h:16-26
+ *   projections .......... tests/gemv_test_common.h:24-65 (GEMV case and
+ *                          reference sum), tests/test_batch_gemv_proj_bf16.cu:20-66
+ *                          (batched case and reference)
  *
  * Arithmetic follows the reference's host code operation by operation
  * (float vs double, accumulation order, where bf16 rounding happens).
@@ -476,4 +479,53 @@ void or_qk_norm_rope(float* x, const float* gamma, const float* inv_freq,
                      float eps) {
     or_multi_rmsnorm(x, gamma, x, num_tokens * num_heads, d_head, eps);
     or_rope(x, inv_freq, num_tokens, num_heads, d_head, 0);
+}
+
+/* ------------------------------------------------------------ projections */
+
+/* tests/gemv_test_common.h:24-50: x [N], w [M][N]. */
+void or_make_gemv_case(uint32_t M, uint32_t N, float x_phase, float w_phase, float* x, float* w) {
+    for (uint32_t i = 0; i < N; ++i)
+        x[i] = 0.45f * sinf((float)(i + 1) * x_phase) -
+               0.18f * cosf((float)(i + 3) * (x_phase * 0.7f)) + 0.01f * (float)(i % 5);
+    for (uint32_t r = 0; r < M; ++r)
+        for (uint32_t c = 0; c < N; ++c)
+            w[(size_t)r * N + c] = 0.35f * cosf((float)((r + 1) * (c + 1)) * w_phase) +
+                                   0.22f * sinf((float)(r + c + 3) * (w_phase * 0.6f)) -
+                                   0.015f * (float)((r * 7 + c * 3) % 9);
+}
+
+/* tests/test_batch_gemv_proj_bf16.cu:20-50: w [M][N], hidden [B][N]. */
+void or_make_batch_gemv_case(uint32_t batch, uint32_t M, uint32_t N, float hidden_phase,
+                             float w_phase, float* hidden, float* w) {
+    for (uint32_t r = 0; r < M; ++r)
+        for (uint32_t c = 0; c < N; ++c)
+            w[(size_t)r * N + c] = 0.33f * cosf((float)((r + 1) * (c + 1)) * w_phase) +
+                                   0.21f * sinf((float)((r + 2) * (c + 3)) * (w_phase * 0.5f)) -
+                                   0.012f * (float)((r * 5 + c * 7) % 11);
+    for (uint32_t b = 0; b < batch; ++b)
+        for (uint32_t c = 0; c < N; ++c) {
+            const uint32_t idx = b * N + c;
+            hidden[idx] = 0.47f * sinf((float)(idx + 1) * hidden_phase) -
+                          0.18f * cosf((float)(idx + c + 3) * (hidden_phase * 0.9f)) +
+                          0.02f * (float)((b + c) % 6);
+        }
+}
+
+/* tests/gemv_test_common.h:52-65 and tests/test_batch_gemv_proj_bf16.cu:52-66:
+ * y[t][r] = sum over c in order of w[r][c] * x[t][c], float accumulation
+ * (the caller rounds to bf16 where the projection outputs bf16).  Tokens are
+ * independent; `nthreads` > 0 spreads them and the rows over OpenMP threads. */
+void or_gemv(const float* w, const float* x, float* y, uint32_t tokens, uint32_t M, uint32_t N,
+             int nthreads) {
+    const int64_t total = (int64_t)tokens * M;
+#pragma omp parallel for schedule(static) num_threads(nthreads > 0 ? nthreads : 1) if (nthreads > 1)
+    for (int64_t i = 0; i < total; ++i) {
+        const uint32_t t = (uint32_t)(i / M), r = (uint32_t)(i % M);
+        const float* wr = w + (size_t)r * N;
+        const float* xt = x + (size_t)t * N;
+        float sum = 0.0f;
+        for (uint32_t c = 0; c < N; ++c) sum += wr[c] * xt[c];
+        y[i] = sum;
+    }
 }

@@ -43,6 +43,9 @@ void or_multi_rmsnorm(const float* x, const float* w, float* out, uint32_t num_r
                       uint32_t d_head, float eps);
 void or_rope(float* qk, const float* inv_freq, uint32_t num_tokens, uint32_t num_heads,
              uint32_t d_head, uint32_t pos0);
+void or_make_gemv_case(uint32_t M, uint32_t N, float x_phase, float w_phase, float* x, float* w);
+void or_gemv(const float* w, const float* x, float* y, uint32_t tokens, uint32_t M, uint32_t N,
+             int nthreads);
 }
 
 namespace {
@@ -428,6 +431,50 @@ void decode_step_cases() {
     hip_ok(hipStreamDestroy(stream), "stream destroy");
 }
 
+// The projections as src/transformer.cpp calls them: gemv_proj_bf16<256> for
+// the decode q/k/v projections (:521-533), gemv_proj_bf162float<256> for the
+// lm-head (:630), batch_gemv_proj_bf16<256> for prefill (:370-378), against
+// the oracle's float sums at the reference tests' bar (8e-2 / 5e-2).
+void projection_cases() {
+    hipStream_t stream;
+    hip_ok(hipStreamCreate(&stream), "stream");
+    struct Shape {
+        uint32_t tokens, M, N;
+    };
+    for (const Shape sh : {Shape{1, 1024, 4096}, Shape{1, 300, 514}, Shape{3, 96, 256},
+                           Shape{37, 200, 256}, Shape{300, 1000, 1024}}) {
+        std::vector<float> x1, w((size_t)sh.M * sh.N), x((size_t)sh.tokens * sh.N);
+        x1.resize(sh.N);
+        or_make_gemv_case(sh.M, sh.N, 0.05f, 0.004f, x1.data(), w.data());
+        for (uint32_t t = 0; t < sh.tokens; ++t)
+            for (uint32_t c = 0; c < sh.N; ++c)
+                x[(size_t)t * sh.N + c] = x1[c] * (1.0f - 0.01f * (float)t) + 0.001f * (float)(t % 5);
+        const auto wb = to_bits(w), xb = to_bits(x);
+        std::vector<float> exp((size_t)sh.tokens * sh.M);
+        or_gemv(from_bits(wb).data(), from_bits(xb).data(), exp.data(), sh.tokens, sh.M, sh.N, 8);
+        Dev<bf16> dw(wb.size()), dx(xb.size()), dy(exp.size());
+        put_bits(dw, wb);
+        put_bits(dx, xb);
+        const std::string shape = std::to_string(sh.tokens) + "x" + std::to_string(sh.M) + "x" +
+                                  std::to_string(sh.N);
+        if (sh.tokens == 1) {
+            toyinfer::gemv_proj_bf16<256>(dw.p, dx.p, dy.p, sh.M, sh.N, stream);
+            Dev<float> df(sh.M);
+            toyinfer::gemv_proj_bf162float<256>(dw.p, dx.p, df.p, sh.M, sh.N, stream);
+            hip_ok(hipStreamSynchronize(stream), "sync");
+            check_close(df.get(), exp, 5e-2f, 5e-2f, "gemv_proj_bf162float " + shape);
+            check_close(from_bits(get_bits(dy)), round_bf16(exp), 8e-2f, 8e-2f,
+                        "gemv_proj_bf16 " + shape);
+        } else {
+            toyinfer::batch_gemv_proj_bf16<256>(dw.p, dx.p, dy.p, sh.tokens, sh.M, sh.N, stream);
+            hip_ok(hipStreamSynchronize(stream), "sync");
+            check_close(from_bits(get_bits(dy)), round_bf16(exp), 8e-2f, 8e-2f,
+                        "batch_gemv_proj_bf16 " + shape);
+        }
+    }
+    hip_ok(hipStreamDestroy(stream), "stream destroy");
+}
+
 }  // namespace
 
 int main() {
@@ -440,6 +487,7 @@ int main() {
     decode_cases();
     prologue_cases();
     decode_step_cases();
+    projection_cases();
     std::printf("%s: %d failure(s)\n", g_failures ? "FAILED" : "ALL PASS", g_failures);
     return g_failures ? 1 : 0;
 }

@@ -152,6 +152,21 @@ def test_decode_step_op_validation():
     assert f(*a) == UNSUPPORTED
 
 
+def test_projection_validation():
+    """Bad arguments of the projection ops are rejected before any launch."""
+    g, gf, b = (L.toyinfer_gemv_proj_bf16, L.toyinfer_gemv_proj_bf162float,
+                L.toyinfer_batch_gemv_proj_bf16)
+    assert g(None, P, P, 8, 8, None) == INVALID
+    assert g(P, P, P, 0, 8, None) == INVALID
+    assert g(P, P, P, 8, 0, None) == INVALID
+    assert g(P, P, P, 8, (1 << 22) + 1, None) == INVALID   # 32-bit byte offsets
+    assert g(P + 1, P, P, 8, 8, None) == INVALID           # bf16 needs 2-byte alignment
+    assert gf(P, P, P + 2, 8, 8, None) == INVALID          # fp32 out needs 4
+    assert gf(P, None, P, 8, 8, None) == INVALID
+    assert b(P, P, P, 0, 8, 8, None) == INVALID
+    assert b(P, P, None, 3, 8, 8, None) == INVALID
+
+
 def test_python_wrapper_raises_on_bad_status():
     class Fake:
         def __init__(self, addr):

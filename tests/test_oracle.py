@@ -320,3 +320,49 @@ def test_qk_norm_rope_and_fused_attention_vs_golden():
     o = oracle.round_bf16(oracle.flash_reference(qn, kn, oracle.bf16_to_f32(vb)))
     H.check_bar(o, H.bf16_bits_to_f32(g["o_bf16"]), "fused oracle vs golden",
                 max_abs=1e-2, mean_abs=2e-4)
+
+
+# ------------------------------------------------------------ projections
+
+def test_gemv_case_generators_literal_values():
+    """The case generators against the formulas of tests/gemv_test_common.h:33-48
+    and tests/test_batch_gemv_proj_bf16.cu:31-49 evaluated in float64."""
+    import math
+    x, w = oracle.make_gemv_case(5, 7, 0.17, 0.01)
+    for i in (0, 3, 6):
+        e = 0.45 * math.sin((i + 1) * 0.17) - 0.18 * math.cos((i + 3) * 0.17 * 0.7) + 0.01 * (i % 5)
+        assert abs(x[i] - e) < 1e-6
+    for r, c in ((0, 0), (4, 6), (2, 5)):
+        e = (0.35 * math.cos((r + 1) * (c + 1) * 0.01) + 0.22 * math.sin((r + c + 3) * 0.006)
+             - 0.015 * ((r * 7 + c * 3) % 9))
+        assert abs(w[r, c] - e) < 1e-6
+    h, w = oracle.make_batch_gemv_case(3, 4, 6, 0.19, 0.12)
+    for b, c in ((0, 0), (2, 5), (1, 3)):
+        idx = b * 6 + c
+        e = (0.47 * math.sin((idx + 1) * 0.19) - 0.18 * math.cos((idx + c + 3) * 0.19 * 0.9)
+             + 0.02 * ((b + c) % 6))
+        assert abs(h[b, c] - e) < 1e-6
+    for r, c in ((0, 0), (3, 5)):
+        e = (0.33 * math.cos((r + 1) * (c + 1) * 0.12) + 0.21 * math.sin((r + 2) * (c + 3) * 0.06)
+             - 0.012 * ((r * 5 + c * 7) % 11))
+        assert abs(w[r, c] - e) < 1e-6
+
+
+def test_gemv_vs_float64_and_closed_forms():
+    """Float accumulation in column order stays within float rounding of the
+    float64 product; unit rows pick one element exactly; token rows are
+    independent; the OpenMP split gives the same bits."""
+    x, w = oracle.make_gemv_case(513, 514, 0.05, 0.004)
+    y = oracle.gemv(w, x)
+    ref = w.astype(np.float64) @ x.astype(np.float64)
+    bound = 514 * 2.0 ** -23 * (np.abs(w).astype(np.float64) @ np.abs(x).astype(np.float64))
+    assert (np.abs(y - ref) <= bound + 1e-30).all()
+    eye = np.zeros((4, 514), np.float32)
+    for k, col in enumerate((0, 7, 300, 513)):
+        eye[k, col] = 1.0
+    assert np.array_equal(oracle.gemv(eye, x), x[[0, 7, 300, 513]])
+    xs = np.stack([x, -x, 2 * x])
+    ys = oracle.gemv(w, xs)
+    assert np.array_equal(ys[0], y) and np.array_equal(ys[1], -y) and np.array_equal(ys[2], 2 * y)
+    assert np.array_equal(oracle.gemv(w, xs, nthreads=4), ys)
+

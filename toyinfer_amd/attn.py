@@ -54,6 +54,9 @@ SIGNATURES = {
     "toyinfer_rope_bf16": (_i32, [_vp, _vp, _u32, _u32, _u32, _vp]),
     "toyinfer_rope_bf16_graph": (_i32, [_vp, _vp, _vp, _u32, _u32, _vp]),
     "toyinfer_write_kv_cache_bf16": (_i32, [_vp, _vp, _vp, _u32, _vp]),
+    "toyinfer_gemv_proj_bf16": (_i32, [_vp, _vp, _vp, _u32, _u32, _vp]),
+    "toyinfer_gemv_proj_bf162float": (_i32, [_vp, _vp, _vp, _u32, _u32, _vp]),
+    "toyinfer_batch_gemv_proj_bf16": (_i32, [_vp, _vp, _vp, _u32, _u32, _u32, _vp]),
     "toyinfer_decode_qkv_prologue_bf16": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _u32, _f32,
                                                  _vp, _vp, _vp, _u32, _u32, _u32, _vp]),
 }
@@ -280,3 +283,27 @@ def decode_qkv_prologue_bf16(q, k, v, q_norm_weight, k_norm_weight, inv_freq, po
                _ptr(inv_freq), _ptr(pos_d), max_seq_len, rms_norm_eps, _ptr(q_out),
                _ptr(k_cache), _ptr(v_cache), num_q_heads, num_kv_heads, head_dim,
                _stream(stream)))
+
+
+# ------------------------------------------------------------ projections
+
+def gemv_proj_bf16(W, hidden_states, y, M: int, N: int, stream=None) -> None:
+    """y[m] = sum_n W[m][n] hidden_states[n] (bf16 out): include/kernel_warpper.h:53-57."""
+    _check("gemv_proj_bf16",
+           LIB.toyinfer_gemv_proj_bf16(_ptr(W), _ptr(hidden_states), _ptr(y), M, N,
+                                       _stream(stream)))
+
+
+def gemv_proj_bf162float(W, hidden_states, y, M: int, N: int, stream=None) -> None:
+    """The same with fp32 out (lm-head): include/kernel_warpper.h:66-70."""
+    _check("gemv_proj_bf162float",
+           LIB.toyinfer_gemv_proj_bf162float(_ptr(W), _ptr(hidden_states), _ptr(y), M, N,
+                                             _stream(stream)))
+
+
+def batch_gemv_proj_bf16(W, hidden_states, y, num_tokens: int, M: int, N: int,
+                         stream=None) -> None:
+    """y[t][m] = sum_n W[m][n] hidden_states[t][n]: include/kernel_warpper.h:59-64."""
+    _check("batch_gemv_proj_bf16",
+           LIB.toyinfer_batch_gemv_proj_bf16(_ptr(W), _ptr(hidden_states), _ptr(y),
+                                             num_tokens, M, N, _stream(stream)))

@@ -439,4 +439,43 @@ int toyinfer_decode_qkv_prologue_bf16(const void* q, const void* k, const void* 
     return token_rows(a, head_dim, stream);
 }
 
+static int proj_args(const void* W, const void* x, const void* y, size_t y_align,
+                     uint32_t tokens, uint32_t M, uint32_t N) {
+    if (!W || !x || !y || tokens == 0 || M == 0 || N == 0 || N > kProjMaxN)
+        return TOYINFER_ERR_INVALID_ARGUMENT;
+    if (!aligned(W, 2) || !aligned(x, 2) || !aligned(y, y_align)) return TOYINFER_ERR_INVALID_ARGUMENT;
+    if ((uint64_t)tokens * M > 0xffffffffull * 64) return TOYINFER_ERR_INVALID_ARGUMENT;
+    return TOYINFER_OK;
+}
+
+int toyinfer_gemv_proj_bf16(const void* W, const void* hidden_states, void* y, uint32_t M,
+                            uint32_t N, void* stream) {
+    const int st = proj_args(W, hidden_states, y, 2, 1, M, N);
+    if (st != TOYINFER_OK) return st;
+    return from_hip(launch_gemv_bf16(static_cast<const uint16_t*>(W),
+                                     static_cast<const uint16_t*>(hidden_states),
+                                     static_cast<uint16_t*>(y), M, N, as_stream(stream)));
+}
+
+int toyinfer_gemv_proj_bf162float(const void* W, const void* hidden_states, float* y,
+                                  uint32_t M, uint32_t N, void* stream) {
+    const int st = proj_args(W, hidden_states, y, 4, 1, M, N);
+    if (st != TOYINFER_OK) return st;
+    return from_hip(launch_gemv_f32(static_cast<const uint16_t*>(W),
+                                    static_cast<const uint16_t*>(hidden_states), y, M, N,
+                                    as_stream(stream)));
+}
+
+int toyinfer_batch_gemv_proj_bf16(const void* W, const void* hidden_states, void* y,
+                                  uint32_t num_tokens, uint32_t M, uint32_t N, void* stream) {
+    const int st = proj_args(W, hidden_states, y, 2, num_tokens, M, N);
+    if (st != TOYINFER_OK) return st;
+    if (num_tokens > 65535u * 4 && !proj_uses_gemm(num_tokens, N, W, hidden_states))
+        return TOYINFER_ERR_UNSUPPORTED;
+    return from_hip(launch_batch_proj_bf16(static_cast<const uint16_t*>(W),
+                                           static_cast<const uint16_t*>(hidden_states),
+                                           static_cast<uint16_t*>(y), num_tokens, M, N,
+                                           as_stream(stream)));
+}
+
 }  // extern "C"

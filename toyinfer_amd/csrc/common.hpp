@@ -70,6 +70,34 @@ __device__ __forceinline__ float xor16_max(float x) {
     return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 
+// Barrier for LDS hand-offs only: waits for this wave's LDS operations but
+// leaves its global loads in flight (a plain __syncthreads also drains them).
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// Buffer resource over [base, base + bytes): loads outside return 0.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
+                                             0x00020000);
+}
+
+// The whole byte offset goes in the VGPR operand (soffset = 0), so that the
+// hardware range check sees all of it and returns zeros past the end.
+__device__ __forceinline__ uint4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t voff) {
+    return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, 0, 0));
+}
+
+// 16 bytes from global memory into LDS at `lds` (buffer-load DMA: the 64
+// lanes' 16-byte chunks land contiguously in lane order from the wave's
+// first lane's address).
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, uint16_t* lds, uint32_t voff) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16,
+                                             voff, 0, 0, 0);
+}
+
 // acc + the sum of the eight bf16 values packed in v (v_dot2_f32_bf16 with ones).
 __device__ __forceinline__ float sum_bf16x8(uint4 v, float acc) {
     typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));

@@ -112,4 +112,18 @@ hipError_t launch_token_rows(const TokenRowsArgs& a, uint32_t d, hipStream_t str
 hipError_t launch_kv_row_copy(const uint16_t* src, uint16_t* cache, const uint32_t* pos_d,
                               uint32_t kv_dim, hipStream_t stream);
 
+// ------------------------------------------------------------ projections
+// y[t][m] = sum_n W[m][n] x[t][n]; W [M][N], x [T][N], y [T][M], fp32
+// accumulation.  Batches above kGemvMaxTokens tokens with N % 64 == 0 and
+// 16-byte aligned W and x run on the MFMA GEMM, the rest on the GEMV.
+constexpr uint32_t kGemvMaxTokens = 4;
+constexpr uint32_t kProjMaxN = 1u << 22;  // keeps every byte offset in 32 bits
+hipError_t launch_gemv_bf16(const uint16_t* W, const uint16_t* x, uint16_t* y, uint32_t M,
+                            uint32_t N, hipStream_t stream);
+hipError_t launch_gemv_f32(const uint16_t* W, const uint16_t* x, float* y, uint32_t M, uint32_t N,
+                           hipStream_t stream);
+hipError_t launch_batch_proj_bf16(const uint16_t* W, const uint16_t* x, uint16_t* y, uint32_t T,
+                                  uint32_t M, uint32_t N, hipStream_t stream);
+bool proj_uses_gemm(uint32_t T, uint32_t N, const void* W, const void* x);
+
 }  // namespace tiattn

@@ -109,18 +109,6 @@ __device__ __forceinline__ v4i16_t ds_read_tr16(const uint16_t* p) {
         (__attribute__((address_space(3))) v4i16_t*)(p));
 }
 
-// Buffer resource over [base, base + bytes): loads outside return 0.
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
-                                             0x00020000);
-}
-
-// The whole byte offset goes in the VGPR operand (soffset = 0), so that the
-// hardware range check sees all of it and returns zeros past the end.
-__device__ __forceinline__ uint4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t voff) {
-    return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, 0, 0));
-}
-
 // Tile starting at byte `tile_off` of K and V into registers; voff is this
 // thread's byte offset of its first chunk within a tile.
 template <int D>
@@ -431,14 +419,6 @@ struct SkShape {
     static constexpr int DBLK = D / 32;
     static constexpr int OPITCH = D + 4;              // merge buffer pitch (floats, 16-byte rows)
 };
-
-// Barrier for LDS hand-offs only: waits for this wave's LDS operations but
-// leaves its global loads in flight (a plain __syncthreads also drains them).
-__device__ __forceinline__ void lds_barrier() {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-    __builtin_amdgcn_s_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-}
 
 // Work item i = (query head, 32-row query tile), heaviest (last) tiles first;
 // consecutive items walk the KV heads, so with Hkv = 8 each XCD sees one KV

@@ -1,0 +1,369 @@
+// Projections around the attention path: y = W·x for one decoded token
+// (bf16 or fp32 out) and y[t] = W·x[t] for a prefill batch.
+//
+// W is [M][N] bf16 row-major (one output per row, as the reference stores
+// its projection weights), x is [T][N] bf16, y is [T][M].  Every product is
+// accumulated in fp32 and rounded once at the store.
+//
+//  * gemv_kernel: HBM-bound.  A workgroup of 256 lanes owns RB output rows
+//    and TB tokens; each lane walks 16-byte chunks of the rows (chunk c =
+//    lane + 256 j), loads the token chunk once and reuses it for all RB rows,
+//    and keeps TB x RB fp32 partials.  Partials are reduced in the wave
+//    (DPP rows, then v_permlane16/32_swap) and across the four waves in LDS.
+//    Buffer loads with an exact range return zeros past the last row or
+//    token, so the tails need no branches.
+//  * gemm_kernel: MFMA-bound (prefill, T > kGemvMaxTokens).  K in 64-wide
+//    slices double-buffered in LDS by buffer-load DMA, v_mfma_f32_32x32x16_bf16
+//    on 32 x 32 blocks.  256 x 256 tiles (8 waves of 128 x 64) when they
+//    alone fill every CU, else 128 x 128 tiles (4 waves of 64 x 64, two
+//    workgroups per CU).  Tiles are ordered in 8 x 8 groups and the groups
+//    are dealt to XCDs in contiguous runs, so the blocks resident on one XCD
+//    share W and x slices in that XCD's L2.
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace tiattn {
+namespace {
+
+// ------------------------------------------------------------------ GEMV
+
+constexpr int kGvThreads = 256;
+constexpr uint32_t kOob = 0xF0000000u;  // a byte offset past every range below
+
+__device__ __forceinline__ float wave_sum(float x) {
+    x += dpp_f32<kDppXor1>(x);
+    x += dpp_f32<kDppXor2>(x);
+    x += dpp_f32<kDppRowHalfMirror>(x);
+    x += dpp_f32<kDppRowMirror>(x);
+    x = xor16_sum(x);
+    return xor32_sum(x);
+}
+
+// E bf16 values per load: 8 (16-byte chunks), 2 (bf16 pairs) or 1.
+template <int E>
+struct GvChunk {
+    static constexpr int WORDS = E == 8 ? 4 : 1;
+    uint32_t w[WORDS];
+};
+
+template <int E>
+__device__ __forceinline__ GvChunk<E> gv_load(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    GvChunk<E> c;
+    if constexpr (E == 8) {
+        const uint4 v = buf_load16(r, off);
+        c.w[0] = v.x; c.w[1] = v.y; c.w[2] = v.z; c.w[3] = v.w;
+    } else if constexpr (E == 2) {
+        c.w[0] = __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
+    } else {
+        c.w[0] = __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0);
+    }
+    return c;
+}
+
+template <int E>
+__device__ __forceinline__ float gv_dot(const GvChunk<E>& w, const GvChunk<E>& x, float acc) {
+    if constexpr (E == 1) {
+        return fmaf(bf16_lo(w.w[0]), bf16_lo(x.w[0]), acc);
+    } else {
+#pragma unroll
+        for (int i = 0; i < GvChunk<E>::WORDS; ++i)
+            acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, w.w[i]),
+                                                  __builtin_bit_cast(bf16x2_t, x.w[i]), acc, false);
+        return acc;
+    }
+}
+
+__device__ __forceinline__ void gv_store(uint16_t* y, size_t i, float v) { y[i] = f32_to_bf16(v); }
+__device__ __forceinline__ void gv_store(float* y, size_t i, float v) { y[i] = v; }
+
+template <int E, int RB, int TB, typename OutT>
+__global__ __launch_bounds__(kGvThreads) void gemv_kernel(const uint16_t* __restrict__ W,
+                                                          const uint16_t* __restrict__ x,
+                                                          OutT* __restrict__ y, uint32_t T,
+                                                          uint32_t M, uint32_t N) {
+    const uint32_t r0 = blockIdx.x * RB, t0 = blockIdx.y * TB;
+    const uint32_t nrows = min((uint32_t)RB, M - r0), ntok = min((uint32_t)TB, T - t0);
+    const uint32_t row_bytes = 2 * N;
+    const auto rw = make_rsrc(W + (size_t)r0 * N, nrows * row_bytes);
+    const auto rx = make_rsrc(x + (size_t)t0 * N, ntok * row_bytes);
+    const uint32_t nchunk = N / E;
+
+    float acc[TB][RB];
+#pragma unroll
+    for (int t = 0; t < TB; ++t)
+#pragma unroll
+        for (int r = 0; r < RB; ++r) acc[t][r] = 0.0f;
+
+    // Two chunks per lane per trip; the second one's offset is pushed out of
+    // range (zeros) when it is past the row.
+    for (uint32_t c = threadIdx.x; c < nchunk; c += 2 * kGvThreads) {
+        const uint32_t c2 = c + kGvThreads;
+        const uint32_t off[2] = {c * 2 * E, c2 < nchunk ? c2 * 2 * E : kOob};
+        GvChunk<E> xv[2][TB], wv[2][RB];
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+#pragma unroll
+            for (int t = 0; t < TB; ++t) xv[u][t] = gv_load<E>(rx, t * row_bytes + off[u]);
+#pragma unroll
+            for (int r = 0; r < RB; ++r) wv[u][r] = gv_load<E>(rw, r * row_bytes + off[u]);
+        }
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+#pragma unroll
+            for (int t = 0; t < TB; ++t)
+#pragma unroll
+                for (int r = 0; r < RB; ++r) acc[t][r] = gv_dot<E>(wv[u][r], xv[u][t], acc[t][r]);
+    }
+
+    __shared__ float red[kGvThreads / 64][TB * RB];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+    for (int t = 0; t < TB; ++t)
+#pragma unroll
+        for (int r = 0; r < RB; ++r) {
+            const float s = wave_sum(acc[t][r]);
+            if (lane == 0) red[wave][t * RB + r] = s;
+        }
+    __syncthreads();
+    if (threadIdx.x < TB * RB) {
+        const uint32_t t = threadIdx.x / RB, r = threadIdx.x % RB;
+        float s = 0.0f;
+#pragma unroll
+        for (int w = 0; w < kGvThreads / 64; ++w) s += red[w][threadIdx.x];
+        if (t < ntok && r < nrows) gv_store(y, (size_t)(t0 + t) * M + r0 + r, s);
+    }
+}
+
+template <int E, int RB, int TB, typename OutT>
+hipError_t gemv_launch(const uint16_t* W, const uint16_t* x, OutT* y, uint32_t T, uint32_t M,
+                       uint32_t N, hipStream_t stream) {
+    const dim3 grid((M + RB - 1) / RB, (T + TB - 1) / TB);
+    gemv_kernel<E, RB, TB, OutT><<<grid, kGvThreads, 0, stream>>>(W, x, y, T, M, N);
+    return hipGetLastError();
+}
+
+// Rows per workgroup: enough workgroups (about two per CU) for small M,
+// more reuse of each token chunk for large M.
+template <int E, int TB, typename OutT>
+hipError_t gemv_rows(const uint16_t* W, const uint16_t* x, OutT* y, uint32_t T, uint32_t M,
+                     uint32_t N, hipStream_t stream) {
+    if constexpr (E != 8) {
+        return gemv_launch<E, 4, TB>(W, x, y, T, M, N, stream);
+    } else {
+        if (M >= 4096) return gemv_launch<E, 8, TB>(W, x, y, T, M, N, stream);
+        if (M >= 2048) return gemv_launch<E, 4, TB>(W, x, y, T, M, N, stream);
+        if (M >= 1024) return gemv_launch<E, 2, TB>(W, x, y, T, M, N, stream);
+        return gemv_launch<E, 1, TB>(W, x, y, T, M, N, stream);
+    }
+}
+
+template <int TB, typename OutT>
+hipError_t gemv_any(const uint16_t* W, const uint16_t* x, OutT* y, uint32_t T, uint32_t M,
+                    uint32_t N, hipStream_t stream) {
+    const uintptr_t a = (uintptr_t)W | (uintptr_t)x;
+    if (N % 8 == 0 && a % 16 == 0) return gemv_rows<8, TB>(W, x, y, T, M, N, stream);
+    if (N % 2 == 0 && a % 4 == 0) return gemv_rows<2, TB>(W, x, y, T, M, N, stream);
+    return gemv_rows<1, TB>(W, x, y, T, M, N, stream);
+}
+
+// ------------------------------------------------------------------ GEMM
+
+constexpr int kGmBK = 64;
+constexpr int kGmGroup = 8;  // tile groups of 8 x 8
+
+// Block tile BM (tokens) x BN (outputs) on a WGM x WGN grid of waves; each
+// wave owns IM x JN blocks of 32 x 32.
+template <int BM_, int BN_, int WGM_, int WGN_, int MINB_>
+struct GmCfg {
+    static constexpr int BM = BM_, BN = BN_, WGM = WGM_, WGN = WGN_, MINB = MINB_;
+    static constexpr int WAVES = WGM * WGN, THREADS = 64 * WAVES;
+    static constexpr int IM = BM / WGM / 32, JN = BN / WGN / 32;
+    static constexpr int A_ELEMS = BM * kGmBK, B_ELEMS = BN * kGmBK;
+    static constexpr int A_DMA = BM / 8 / WAVES, B_DMA = BN / 8 / WAVES;  // per wave
+    static_assert(A_DMA * 8 * WAVES == BM && B_DMA * 8 * WAVES == BN, "DMA split");
+};
+using GmSmall = GmCfg<128, 128, 2, 2, 2>;  // 4 waves of 64 x 64, 2 workgroups per CU
+using GmLarge = GmCfg<256, 256, 2, 4, 1>;  // 8 waves of 128 x 64
+
+// LDS rows of 64 bf16 (128 bytes = 8 chunks); chunk c of row r sits at
+// c ^ (r & 7), which makes the MFMA operand reads (8 rows x 16 bytes per
+// cycle) bank-conflict free.  One DMA instruction fills 8 rows: lane l
+// loads row l / 8, physical chunk l % 8, i.e. logical chunk (l % 8) ^ (l / 8).
+template <int WAVES, int BLOCKS>
+__device__ __forceinline__ void gm_dma(__amdgpu_buffer_rsrc_t r, uint32_t row_bytes, uint32_t k_off,
+                                       uint16_t* lds) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint32_t logical = (lane & 7) ^ (lane >> 3);
+#pragma unroll
+    for (int j = 0; j < BLOCKS; ++j) {
+        const int blk = wave + WAVES * j;
+        const uint32_t row = 8 * blk + (lane >> 3);
+        dma16(r, lds + 512 * blk, row * row_bytes + k_off + 16 * logical);
+    }
+}
+
+struct GmTile {
+    uint32_t tt, tm;  // token tile, output tile
+};
+
+// Grouped order (8 output tiles x 8 token tiles per group, token-major
+// inside a group), and consecutive group positions on one XCD: hardware
+// deals workgroup b to XCD b % 8, so b -> (b % 8) * (n / 8) + b / 8 gives
+// XCD x the run [x n / 8, (x + 1) n / 8) when n % 8 == 0.
+__device__ __forceinline__ GmTile gm_tile(uint32_t b, uint32_t n_tt, uint32_t n_tm) {
+    const uint32_t n = n_tt * n_tm;
+    const uint32_t g = n % 8 == 0 ? (b % 8) * (n / 8) + b / 8 : b;
+    const uint32_t per_group = kGmGroup * n_tt;
+    const uint32_t first_tm = (g / per_group) * kGmGroup;
+    const uint32_t gsize = min((uint32_t)kGmGroup, n_tm - first_tm);
+    const uint32_t in = g % per_group;
+    return {in / gsize, first_tm + in % gsize};
+}
+
+template <typename C>
+__global__ __launch_bounds__(C::THREADS, C::MINB) void gemm_kernel(const uint16_t* __restrict__ W,
+                                                          const uint16_t* __restrict__ x,
+                                                          uint16_t* __restrict__ y, uint32_t T,
+                                                          uint32_t M, uint32_t N) {
+    constexpr int IM = C::IM, JN = C::JN;
+    // One array per stage (A rows, then B rows), so that the compiler can
+    // tell the stage being read from the one the DMA is filling.
+    __shared__ __align__(1024) uint16_t s_0[C::A_ELEMS + C::B_ELEMS];
+    __shared__ __align__(1024) uint16_t s_1[C::A_ELEMS + C::B_ELEMS];
+    const uint32_t n_tt = (T + C::BM - 1) / C::BM, n_tm = (M + C::BN - 1) / C::BN;
+    const GmTile tile = gm_tile(blockIdx.x, n_tt, n_tm);
+    const uint32_t t0 = tile.tt * C::BM, m0 = tile.tm * C::BN;
+    const uint32_t row_bytes = 2 * N;
+    const auto ra = make_rsrc(x + (size_t)t0 * N, min((uint32_t)C::BM, T - t0) * row_bytes);
+    const auto rb = make_rsrc(W + (size_t)m0 * N, min((uint32_t)C::BN, M - m0) * row_bytes);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int wr = wave / C::WGN, wc = wave % C::WGN;
+
+    // Operand read offsets (elements) inside a stage for block 0, per
+    // k-step; block i adds 32 i rows.
+    int a_off[4], b_off[4];
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+        const int chunk = (2 * s + (lane >> 5)) ^ (lane & 7);
+        a_off[s] = (32 * IM * wr + (lane & 31)) * kGmBK + 8 * chunk;
+        b_off[s] = C::A_ELEMS + (32 * JN * wc + (lane & 31)) * kGmBK + 8 * chunk;
+    }
+
+    f32x16_t acc[IM][JN];
+#pragma unroll
+    for (int i = 0; i < IM; ++i)
+#pragma unroll
+        for (int j = 0; j < JN; ++j)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
+
+    const uint32_t nk = N / kGmBK;
+    auto dma_slice = [&](uint32_t kt, uint16_t* st) __attribute__((always_inline)) {
+        gm_dma<C::WAVES, C::A_DMA>(ra, row_bytes, kt * kGmBK * 2, st);
+        gm_dma<C::WAVES, C::B_DMA>(rb, row_bytes, kt * kGmBK * 2, st + C::A_ELEMS);
+    };
+    // Step kt: wait for slice kt, barrier, start slice kt + 1 into the stage
+    // step kt - 1 read, then four k-steps of MFMAs from stage kt % 2.
+    auto step = [&](uint32_t kt, const uint16_t* cur, uint16_t* nxt) __attribute__((always_inline)) {
+        __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+        // The reads of step kt - 1 have all been consumed by its MFMAs; the
+        // memory clobber keeps this step's reads and DMA below the barrier.
+        asm volatile("s_barrier" ::: "memory");
+        if (kt + 1 < nk) dma_slice(kt + 1, nxt);
+        // Operands of k-step s + 1 are read while the MFMAs of k-step s run
+        // (two register sets).
+        bf16x8_t a[2][IM], b[2][JN];
+        auto read = [&](int s) __attribute__((always_inline)) {
+#pragma unroll
+            for (int i = 0; i < IM; ++i)
+                a[s & 1][i] = as_bf16x8(*reinterpret_cast<const uint4*>(cur + a_off[s] + 32 * kGmBK * i));
+#pragma unroll
+            for (int j = 0; j < JN; ++j)
+                b[s & 1][j] = as_bf16x8(*reinterpret_cast<const uint4*>(cur + b_off[s] + 32 * kGmBK * j));
+        };
+        read(0);
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            if (s < 3) read(s + 1);
+#pragma unroll
+            for (int i = 0; i < IM; ++i)
+#pragma unroll
+                for (int j = 0; j < JN; ++j)
+                    acc[i][j] = mfma32x32x16(a[s & 1][i], b[s & 1][j], acc[i][j]);
+        }
+        // Schedule: reads of k-steps 0 and 1, then each k-step's MFMAs
+        // followed by the reads of the k-step after the next.
+        __builtin_amdgcn_sched_group_barrier(0x100, 2 * (IM + JN), 0);
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            __builtin_amdgcn_sched_group_barrier(0x008, IM * JN, 0);
+            if (s < 2) __builtin_amdgcn_sched_group_barrier(0x100, IM + JN, 0);
+        }
+    };
+    dma_slice(0, s_0);
+    for (uint32_t kt = 0; kt < nk; kt += 2) {
+        step(kt, s_0, s_1);
+        if (kt + 1 < nk) step(kt + 1, s_1, s_0);
+    }
+
+    // C block (i, j): lane l value v is token row 8 (v / 4) + 4 (l / 32) + v % 4,
+    // output column l % 32.
+#pragma unroll
+    for (int i = 0; i < IM; ++i)
+#pragma unroll
+        for (int j = 0; j < JN; ++j) {
+            const uint32_t m = m0 + 32 * (JN * wc + j) + (lane & 31);
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                const uint32_t t = t0 + 32 * (IM * wr + i) + 8 * (v / 4) + 4 * (lane >> 5) + (v % 4);
+                if (t < T && m < M) y[(size_t)t * M + m] = f32_to_bf16(acc[i][j][v]);
+            }
+        }
+}
+
+template <typename C>
+hipError_t gemm_launch(const uint16_t* W, const uint16_t* x, uint16_t* y, uint32_t T, uint32_t M,
+                       uint32_t N, hipStream_t stream) {
+    const uint32_t tiles = ((T + C::BM - 1) / C::BM) * ((M + C::BN - 1) / C::BN);
+    gemm_kernel<C><<<tiles, C::THREADS, 0, stream>>>(W, x, y, T, M, N);
+    return hipGetLastError();
+}
+
+int gemm_cus() {
+    static int cus = [] {
+        int dev = 0, n = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+            return 256;
+        return n;
+    }();
+    return cus;
+}
+
+}  // namespace
+
+hipError_t launch_gemv_bf16(const uint16_t* W, const uint16_t* x, uint16_t* y, uint32_t M,
+                            uint32_t N, hipStream_t stream) {
+    return gemv_any<1>(W, x, y, 1, M, N, stream);
+}
+
+hipError_t launch_gemv_f32(const uint16_t* W, const uint16_t* x, float* y, uint32_t M, uint32_t N,
+                           hipStream_t stream) {
+    return gemv_any<1>(W, x, y, 1, M, N, stream);
+}
+
+bool proj_uses_gemm(uint32_t T, uint32_t N, const void* W, const void* x) {
+    return T > kGemvMaxTokens && N % kGmBK == 0 && ((uintptr_t)W | (uintptr_t)x) % 16 == 0;
+}
+
+hipError_t launch_batch_proj_bf16(const uint16_t* W, const uint16_t* x, uint16_t* y, uint32_t T,
+                                  uint32_t M, uint32_t N, hipStream_t stream) {
+    if (T == 1) return gemv_any<1>(W, x, y, T, M, N, stream);
+    if (!proj_uses_gemm(T, N, W, x)) return gemv_any<4>(W, x, y, T, M, N, stream);
+    // 256 x 256 tiles when they alone fill every CU once, else 128 x 128.
+    const uint32_t large = ((T + 255) / 256) * ((M + 255) / 256);
+    if (large >= (uint32_t)gemm_cus()) return gemm_launch<GmLarge>(W, x, y, T, M, N, stream);
+    return gemm_launch<GmSmall>(W, x, y, T, M, N, stream);
+}
+
+}  // namespace tiattn

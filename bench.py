@@ -68,8 +68,10 @@ def causal_flops(s, hq, d):
 def parse():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=100)
-    ap.add_argument("--warmup", type=int, default=10)
+    # The headline step is ~20 us, and the MFMA clock settles over the first
+    # few milliseconds of sustained launches: defaults give it ~4 ms to settle.
+    ap.add_argument("--steps", type=int, default=500)
+    ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--no-components", action="store_true",
                     help="only the headline workload")
     ap.add_argument("--no-cpu", action="store_true", help="skip the cpu_baseline leg")
@@ -416,7 +418,7 @@ def main():
                              traffic_bytes("prefill")),
     }
     if not args.no_components:
-        comps = [bench_prefill_fused(dev, stream, max(10, args.steps // 4), 3)]
+        comps = [bench_prefill_fused(dev, stream, max(10, args.steps // 4), 10)]
         comps.append(bench_decode(dev, stream, max(50, args.steps * 2), 10, b=8, L=4096))
         comps.append(bench_decode(dev, stream, max(50, args.steps * 2), 10, b=1, L=32768))
         comps.append(bench_decode_step(dev, stream, max(50, args.steps * 2), 10))

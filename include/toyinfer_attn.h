@@ -217,6 +217,52 @@ int toyinfer_gemv_proj_bf162float(const void* W, const void* hidden_states, floa
 int toyinfer_batch_gemv_proj_bf16(const void* W, const void* hidden_states, void* y,
                                   uint32_t num_tokens, uint32_t M, uint32_t N, void* stream);
 
+/* ---- The rest of a Qwen3 decoder layer (for the model harness) ----
+ * bf16 tensors need 4-byte alignment (16 bytes and sizes % 8 == 0 take the
+ * vector path); sizes are even, as the reference's bf16x2 kernels assume. */
+
+/* output = bf16(input * rsqrt(sum/size + eps) * weight) over one row of
+ * `size`; *sum = the row's sum of squares (fp32).  Replaces
+ * toyinfer::rmsnorm_bf16<NUM_THREADS> (include/kernel_warpper.h:25-29;
+ * src/decode.cu:67-142), one launch instead of memset + two kernels. */
+int toyinfer_rmsnorm_bf16(const void* input, const void* weight, void* output, float* sum,
+                          float rms_norm_eps, uint32_t size, void* stream);
+/* The same per row of num_tokens rows; sum[t] per row.  Replaces
+ * toyinfer::batch_rmsnorm_bf16<NUM_THREADS> (include/kernel_warpper.h:31-36;
+ * src/prefill.cu:42-112). */
+int toyinfer_batch_rmsnorm_bf16(const void* input, const void* weight, void* output, float* sum,
+                                float rms_norm_eps, uint32_t num_tokens, uint32_t size,
+                                void* stream);
+/* hidden_state = bf16(hidden_state + residual).  Replaces
+ * toyinfer::residual_add_bf16<NUM_THREADS> (include/kernel_warpper.h:12-15;
+ * src/decode.cu:7-33). */
+int toyinfer_residual_add_bf16(const void* residual, void* hidden_state, uint32_t size,
+                               void* stream);
+/* Over num_tokens * size values.  Replaces toyinfer::batch_residual_add_bf16
+ * (include/kernel_warpper.h:17-21; src/prefill.cu:176-183). */
+int toyinfer_batch_residual_add_bf16(const void* residual, void* hidden_state,
+                                     uint32_t num_tokens, uint32_t size, void* stream);
+/* intermedia = bf16(up * gate / (1 + exp(-gate))).  Replaces
+ * toyinfer::swiglu_bf16x2<NUM_THREADS> (include/kernel_warpper.h:116-119;
+ * src/decode.cu:746-775). */
+int toyinfer_swiglu_bf16x2(const void* gate, const void* up, void* intermedia, uint32_t size,
+                           void* stream);
+/* Over num_tokens * size values.  Replaces toyinfer::batch_swiglu_bf16x2
+ * (include/kernel_warpper.h:121-126; src/prefill.cu:397-405). */
+int toyinfer_batch_swiglu_bf16x2(const void* gate, const void* up, void* intermedia,
+                                 uint32_t num_tokens, uint32_t size, void* stream);
+/* hidden_states[t] = embedding_table[token_ids[t]] (token_ids in device
+ * memory); ids >= vocab_size give zero rows (vocab_size = 0xFFFFFFFF: no
+ * check, as the reference).  Replaces toyinfer::gather_embedding_bf16
+ * (include/kernel_warpper.h:71-77; src/prefill.cu:6-36). */
+int toyinfer_gather_embedding_bf16(const void* embedding_table, const uint32_t* token_ids,
+                                   void* hidden_states, uint32_t num_tokens,
+                                   uint32_t hidden_size, uint32_t vocab_size, void* stream);
+/* *out_index = the first index of the maximum of logits[0..n) under strict
+ * '>' from -FLT_MAX (UINT32_MAX if none), on the device.  Extension: the
+ * reference's greedy sampler does this on the host (src/sampler.cpp:71-82). */
+int toyinfer_argmax_f32(const float* logits, uint32_t n, uint32_t* out_index, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -70,6 +70,13 @@ def _load() -> ctypes.CDLL:
         "or_make_gemv_case": (None, [_u32, _u32, _f32, _f32, _f32p, _f32p]),
         "or_make_batch_gemv_case": (None, [_u32, _u32, _u32, _f32, _f32, _f32p, _f32p]),
         "or_gemv": (None, [_f32p, _f32p, _f32p, _u32, _u32, _u32, ctypes.c_int]),
+        "or_make_rmsnorm_row_case": (None, [_u32, _u32, _f32, _f32, _f32p, _f32p]),
+        "or_make_batch_row_rmsnorm_case": (None, [_u32, _u32, _f32, _f32, _f32p, _f32p]),
+        "or_make_swiglu_case": (None, [_u32, _u32, _f32, _f32, _f32p, _f32p]),
+        "or_make_add_case": (None, [_u32, _u32, _f32, _f32, _f32, _f32p, _f32p]),
+        "or_residual_add": (None, [_f32p, _f32p, _f32p, ctypes.c_int64]),
+        "or_swiglu": (None, [_f32p, _f32p, _f32p, ctypes.c_int64]),
+        "or_argmax": (_u32, [_f32p, _u32]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -310,3 +317,65 @@ def gemv(w, x, nthreads: int = 0):
     y = np.empty(tokens * M, np.float32)
     lib().or_gemv(w.reshape(-1), x.reshape(-1), y, tokens, M, N, nthreads)
     return y.reshape(x.shape[:-1] + (M,)) if x.ndim > 1 else y
+
+
+# ------------------------------------------------- rest of a decoder layer
+
+def make_rmsnorm_row_case(size, buffer_size, input_phase, weight_phase):
+    """tests/rmsnorm_test_common.h:24-42 -> (input, weight), buffer_size each."""
+    x = np.empty(buffer_size, np.float32)
+    w = np.empty(buffer_size, np.float32)
+    lib().or_make_rmsnorm_row_case(size, buffer_size, input_phase, weight_phase, x, w)
+    return x, w
+
+
+def make_batch_row_rmsnorm_case(batch, size, input_phase, weight_phase):
+    """tests/test_batch_rmsnorm_bf16.cu:20-46 -> (input [B][size], weight [size])."""
+    x = np.empty((batch, size), np.float32)
+    w = np.empty(size, np.float32)
+    lib().or_make_batch_row_rmsnorm_case(batch, size, input_phase, weight_phase, x.reshape(-1),
+                                         w)
+    return x, w
+
+
+def make_swiglu_case(size, buffer_size, gate_phase, up_phase):
+    g = np.empty(buffer_size, np.float32)
+    u = np.empty(buffer_size, np.float32)
+    lib().or_make_swiglu_case(size, buffer_size, gate_phase, up_phase, g, u)
+    return g, u
+
+
+def make_add_case(size, buffer_size, residual_phase, hidden_phase, tail_bias):
+    r = np.empty(buffer_size, np.float32)
+    h = np.empty(buffer_size, np.float32)
+    lib().or_make_add_case(size, buffer_size, residual_phase, hidden_phase, tail_bias, r, h)
+    return r, h
+
+
+def rmsnorm_rows(x, w, eps):
+    """Full-row RMSNorm of every row of x ([..., size]); bf16-valued float32."""
+    x = _c32(x)
+    size = x.shape[-1]
+    out = np.empty_like(x)
+    lib().or_multi_rmsnorm(x.reshape(-1), _c32(w), out.reshape(-1), x.size // size, size, eps)
+    return out
+
+
+def residual_add(hidden, residual):
+    h, r = _c32(hidden), _c32(residual)
+    out = np.empty_like(h)
+    lib().or_residual_add(h.reshape(-1), r.reshape(-1), out.reshape(-1), h.size)
+    return out
+
+
+def swiglu(gate, up):
+    g, u = _c32(gate), _c32(up)
+    out = np.empty_like(g)
+    lib().or_swiglu(g.reshape(-1), u.reshape(-1), out.reshape(-1), g.size)
+    return out
+
+
+def argmax(logits):
+    x = _c32(logits).reshape(-1)
+    return int(lib().or_argmax(x, x.size))
+

@@ -25,6 +25,9 @@
  *   projections .......... tests/gemv_test_common.h:24-65 (GEMV case and
  *                          reference sum), tests/test_batch_gemv_proj_bf16.cu:20-66
  *                          (batched case and reference)
+ *   row RMSNorm, residual  tests/rmsnorm_test_common.h, tests/add_test_common.h,
+ *   add, SwiGLU, argmax .. tests/swiglu_test_common.h, the batch tests, and
+ *                          src/sampler.cpp:71-82
  *
  * Arithmetic follows the reference's host code operation by operation
  * (float vs double, accumulation order, where bf16 rounding happens).
@@ -529,3 +532,99 @@ void or_gemv(const float* w, const float* x, float* y, uint32_t tokens, uint32_t
         y[i] = sum;
     }
 }
+
+/* ------------------------------------------------- rest of a decoder layer */
+/* Full-row RMSNorm is or_multi_rmsnorm with one "head" of `size` values per
+ * row: tests/rmsnorm_test_common.h:44-66 and
+ * tests/test_batch_rmsnorm_bf16.cu:52-71 perform the same operations (float
+ * sum of squares in order, 1/sqrt(sum/size + eps), x*inv*w rounded). */
+
+/* tests/rmsnorm_test_common.h:24-42 (input, weight over buffer_size). */
+void or_make_rmsnorm_row_case(uint32_t size, uint32_t buffer_size, float input_phase,
+                              float weight_phase, float* input, float* weight) {
+    for (uint32_t i = 0; i < size; ++i) {
+        input[i] = 0.48f * sinf((float)(i + 1) * input_phase) -
+                   0.22f * cosf((float)(i + 3) * input_phase * 0.7f) + 0.013f * (float)(i % 7);
+        weight[i] = 0.72f + 0.18f * sinf((float)(i + 5) * weight_phase) -
+                    0.04f * (float)((i * 3) % 5);
+    }
+    for (uint32_t i = size; i < buffer_size; ++i) {
+        input[i] = -0.75f + 0.05f * (float)(i - size);
+        weight[i] = 0.95f - 0.03f * (float)(i - size);
+    }
+}
+
+/* tests/test_batch_rmsnorm_bf16.cu:20-46: input [batch][size], weight [size]. */
+void or_make_batch_row_rmsnorm_case(uint32_t batch, uint32_t size, float input_phase,
+                                    float weight_phase, float* input, float* weight) {
+    for (uint32_t b = 0; b < batch; ++b)
+        for (uint32_t i = 0; i < size; ++i) {
+            const uint32_t idx = b * size + i;
+            input[idx] = 0.43f * sinf((float)(idx + 1) * input_phase) -
+                         0.27f * cosf((float)(i + 2) * input_phase * 0.4f) +
+                         0.02f * (float)((b + i) % 7);
+        }
+    for (uint32_t i = 0; i < size; ++i)
+        weight[i] = 0.72f + 0.18f * sinf((float)(i + 5) * weight_phase) -
+                    0.04f * (float)((i * 3) % 5);
+}
+
+/* tests/swiglu_test_common.h:22-43 (gate, up over buffer_size). */
+void or_make_swiglu_case(uint32_t size, uint32_t buffer_size, float gate_phase, float up_phase,
+                         float* gate, float* up) {
+    for (uint32_t i = 0; i < size; ++i) {
+        gate[i] = 0.9f * sinf((float)(i + 1) * gate_phase) -
+                  0.7f * cosf((float)(i + 3) * gate_phase * 0.5f);
+        up[i] = 0.42f * cosf((float)(i + 5) * up_phase) -
+                0.31f * sinf((float)(i + 1) * up_phase * 0.8f) - 0.02f * (float)(i % 6);
+    }
+    for (uint32_t i = size; i < buffer_size; ++i) {
+        gate[i] = -1.2f + 0.07f * (float)(i - size);
+        up[i] = 0.95f - 0.05f * (float)(i - size);
+    }
+}
+
+/* tests/add_test_common.h:25-51 (residual, hidden over buffer_size). */
+void or_make_add_case(uint32_t size, uint32_t buffer_size, float residual_phase,
+                      float hidden_phase, float tail_bias, float* residual, float* hidden) {
+    for (uint32_t i = 0; i < size; ++i) {
+        residual[i] = 0.23f * sinf((float)(i + 1) * residual_phase) -
+                      0.08f * cosf((float)(i + 5) * residual_phase * 0.7f) +
+                      0.01f * (float)(i % 5);
+        hidden[i] = -0.27f * cosf((float)(i + 3) * hidden_phase) +
+                    0.19f * sinf((float)(i + 1) * hidden_phase * 0.6f) -
+                    0.012f * (float)((i * 7) % 9);
+    }
+    for (uint32_t i = size; i < buffer_size; ++i) {
+        residual[i] = tail_bias + 0.03f * (float)(i - size);
+        hidden[i] = -tail_bias - 0.02f * (float)(i - size);
+    }
+}
+
+/* tests/add_test_common.h:53-59: out = round_bf16(hidden + residual). */
+void or_residual_add(const float* hidden, const float* residual, float* out, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) out[i] = or_round_to_bf16(hidden[i] + residual[i]);
+}
+
+/* tests/swiglu_test_common.h:45-53 with tests/test_helpers.h:177-179:
+ * out = round_bf16(up * (gate * (1 / (1 + exp(-gate))))), float exp. */
+void or_swiglu(const float* gate, const float* up, float* out, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) {
+        const float sig = 1.0f / (1.0f + expf(-gate[i]));
+        out[i] = or_round_to_bf16(up[i] * (gate[i] * sig));
+    }
+}
+
+/* src/sampler.cpp:71-82: first index whose value exceeds every earlier one,
+ * starting from -FLT_MAX; UINT32_MAX if none. */
+uint32_t or_argmax(const float* logits, uint32_t n) {
+    float best = -3.402823466e38f;
+    uint32_t idx = 0xffffffffu;
+    for (uint32_t i = 0; i < n; ++i)
+        if (logits[i] > best) {
+            best = logits[i];
+            idx = i;
+        }
+    return idx;
+}
+

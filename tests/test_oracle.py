@@ -366,3 +366,78 @@ def test_gemv_vs_float64_and_closed_forms():
     assert np.array_equal(ys[0], y) and np.array_equal(ys[1], -y) and np.array_equal(ys[2], 2 * y)
     assert np.array_equal(oracle.gemv(w, xs, nthreads=4), ys)
 
+
+# ------------------------------------------------- rest of a decoder layer
+
+def test_layer_op_case_generators_literal_values():
+    """Case formulas of tests/rmsnorm_test_common.h:33-41,
+    tests/swiglu_test_common.h:33-42, tests/add_test_common.h:36-50 and
+    tests/test_batch_rmsnorm_bf16.cu:31-44 evaluated in float64."""
+    import math
+    x, w = oracle.make_rmsnorm_row_case(258, 264, 0.11, 0.07)
+    for i in (0, 100, 257):
+        e = 0.48 * math.sin((i + 1) * 0.11) - 0.22 * math.cos((i + 3) * 0.11 * 0.7) + 0.013 * (i % 7)
+        assert abs(x[i] - e) < 1e-6
+        e = 0.72 + 0.18 * math.sin((i + 5) * 0.07) - 0.04 * ((i * 3) % 5)
+        assert abs(w[i] - e) < 1e-6
+    assert abs(x[260] - (-0.75 + 0.05 * 2)) < 1e-6 and abs(w[263] - (0.95 - 0.03 * 5)) < 1e-6
+    g, u = oracle.make_swiglu_case(514, 520, 0.08, 0.05)
+    for i in (0, 513):
+        assert abs(g[i] - (0.9 * math.sin((i + 1) * 0.08) - 0.7 * math.cos((i + 3) * 0.04))) < 1e-6
+        assert abs(u[i] - (0.42 * math.cos((i + 5) * 0.05) - 0.31 * math.sin((i + 1) * 0.04)
+                           - 0.02 * (i % 6))) < 1e-6
+    assert abs(g[515] - (-1.2 + 0.07)) < 1e-6
+    r, h = oracle.make_add_case(514, 520, 0.09, 0.07, 0.6)
+    for i in (0, 513):
+        assert abs(r[i] - (0.23 * math.sin((i + 1) * 0.09) - 0.08 * math.cos((i + 5) * 0.063)
+                           + 0.01 * (i % 5))) < 1e-6
+        assert abs(h[i] - (-0.27 * math.cos((i + 3) * 0.07) + 0.19 * math.sin((i + 1) * 0.042)
+                           - 0.012 * ((i * 7) % 9))) < 1e-6
+    assert abs(r[514] - 0.6) < 1e-6 and abs(h[519] - (-0.6 - 0.1)) < 1e-6
+    xb, wb = oracle.make_batch_row_rmsnorm_case(3, 32, 0.08, 0.12)
+    for b, i in ((0, 0), (2, 31)):
+        idx = b * 32 + i
+        e = (0.43 * math.sin((idx + 1) * 0.08) - 0.27 * math.cos((i + 2) * 0.08 * 0.4)
+             + 0.02 * ((b + i) % 7))
+        assert abs(xb[b, i] - e) < 1e-6
+
+
+def test_residual_add_and_swiglu_vs_torch_bf16():
+    """Residual add against torch's bf16 addition (float sum, one rounding),
+    SwiGLU against torch's silu in float64 then bf16 (within one bf16 step),
+    plus closed forms: silu(0) = 0, silu(g) -> g for large g, -> 0 for very
+    negative g."""
+    import torch
+    rng = np.random.default_rng(7)
+    h = oracle.round_bf16(rng.normal(size=4096).astype(np.float32))
+    r = oracle.round_bf16(rng.normal(size=4096).astype(np.float32))
+    exp = (torch.from_numpy(h).to(torch.bfloat16) + torch.from_numpy(r).to(torch.bfloat16))
+    assert np.array_equal(oracle.residual_add(h, r), exp.float().numpy())
+    g = oracle.round_bf16(rng.normal(scale=3.0, size=4096).astype(np.float32))
+    u = oracle.round_bf16(rng.normal(size=4096).astype(np.float32))
+    ref = torch.from_numpy(u).double() * torch.nn.functional.silu(torch.from_numpy(g).double())
+    ref_b = ref.float().to(torch.bfloat16).float().numpy()
+    got = oracle.swiglu(g, u)
+    step = np.maximum(np.abs(ref_b), 1e-30) * 2.0 ** -7
+    assert (np.abs(got - ref_b) <= step + 1e-12).all()
+    z = np.zeros(4, np.float32)
+    assert np.array_equal(oracle.swiglu(z, np.ones(4, np.float32)), z)
+    big = np.array([20.0, 40.0], np.float32)
+    assert np.array_equal(oracle.swiglu(big, np.array([1.0, 0.5], np.float32)),
+                          oracle.round_bf16(np.array([20.0, 20.0], np.float32)))
+    assert np.abs(oracle.swiglu(-big, np.ones(2, np.float32))).max() < 1e-6
+
+
+def test_argmax_first_maximum_and_nan():
+    """First index of the maximum (numpy.argmax on NaN-free input); NaN never
+    wins; nothing above -FLT_MAX gives UINT32_MAX."""
+    rng = np.random.default_rng(8)
+    for n in (1, 7, 1000, 151936):
+        x = rng.normal(size=n).astype(np.float32)
+        assert oracle.argmax(x) == int(np.argmax(x))
+    x = np.array([1.0, 5.0, 5.0, 2.0], np.float32)
+    assert oracle.argmax(x) == 1
+    x = np.array([np.nan, -1.0, np.nan, 3.0, np.nan], np.float32)
+    assert oracle.argmax(x) == 3
+    assert oracle.argmax(np.array([-np.inf, np.nan], np.float32)) == 0xFFFFFFFF
+

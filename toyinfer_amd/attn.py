@@ -57,6 +57,14 @@ SIGNATURES = {
     "toyinfer_gemv_proj_bf16": (_i32, [_vp, _vp, _vp, _u32, _u32, _vp]),
     "toyinfer_gemv_proj_bf162float": (_i32, [_vp, _vp, _vp, _u32, _u32, _vp]),
     "toyinfer_batch_gemv_proj_bf16": (_i32, [_vp, _vp, _vp, _u32, _u32, _u32, _vp]),
+    "toyinfer_rmsnorm_bf16": (_i32, [_vp, _vp, _vp, _vp, _f32, _u32, _vp]),
+    "toyinfer_batch_rmsnorm_bf16": (_i32, [_vp, _vp, _vp, _vp, _f32, _u32, _u32, _vp]),
+    "toyinfer_residual_add_bf16": (_i32, [_vp, _vp, _u32, _vp]),
+    "toyinfer_batch_residual_add_bf16": (_i32, [_vp, _vp, _u32, _u32, _vp]),
+    "toyinfer_swiglu_bf16x2": (_i32, [_vp, _vp, _vp, _u32, _vp]),
+    "toyinfer_batch_swiglu_bf16x2": (_i32, [_vp, _vp, _vp, _u32, _u32, _vp]),
+    "toyinfer_gather_embedding_bf16": (_i32, [_vp, _vp, _vp, _u32, _u32, _u32, _vp]),
+    "toyinfer_argmax_f32": (_i32, [_vp, _u32, _vp, _vp]),
     "toyinfer_decode_qkv_prologue_bf16": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _u32, _f32,
                                                  _vp, _vp, _vp, _u32, _u32, _u32, _vp]),
 }
@@ -307,3 +315,57 @@ def batch_gemv_proj_bf16(W, hidden_states, y, num_tokens: int, M: int, N: int,
     _check("batch_gemv_proj_bf16",
            LIB.toyinfer_batch_gemv_proj_bf16(_ptr(W), _ptr(hidden_states), _ptr(y),
                                              num_tokens, M, N, _stream(stream)))
+
+
+# ------------------------------------------------- rest of a decoder layer
+
+def rmsnorm_bf16(input, weight, output, sum, eps: float, size: int, stream=None) -> None:
+    """include/kernel_warpper.h:25-29; sum may be None."""
+    _check("rmsnorm_bf16", LIB.toyinfer_rmsnorm_bf16(_ptr(input), _ptr(weight), _ptr(output),
+                                                     _ptr(sum), eps, size, _stream(stream)))
+
+
+def batch_rmsnorm_bf16(input, weight, output, sum, eps: float, num_tokens: int, size: int,
+                       stream=None) -> None:
+    """include/kernel_warpper.h:31-36; sum may be None."""
+    _check("batch_rmsnorm_bf16",
+           LIB.toyinfer_batch_rmsnorm_bf16(_ptr(input), _ptr(weight), _ptr(output), _ptr(sum),
+                                           eps, num_tokens, size, _stream(stream)))
+
+
+def residual_add_bf16(residual, hidden_state, size: int, stream=None) -> None:
+    _check("residual_add_bf16",
+           LIB.toyinfer_residual_add_bf16(_ptr(residual), _ptr(hidden_state), size,
+                                          _stream(stream)))
+
+
+def batch_residual_add_bf16(residual, hidden_state, num_tokens: int, size: int,
+                            stream=None) -> None:
+    _check("batch_residual_add_bf16",
+           LIB.toyinfer_batch_residual_add_bf16(_ptr(residual), _ptr(hidden_state), num_tokens,
+                                                size, _stream(stream)))
+
+
+def swiglu_bf16x2(gate, up, intermedia, size: int, stream=None) -> None:
+    _check("swiglu_bf16x2", LIB.toyinfer_swiglu_bf16x2(_ptr(gate), _ptr(up), _ptr(intermedia),
+                                                       size, _stream(stream)))
+
+
+def batch_swiglu_bf16x2(gate, up, intermedia, num_tokens: int, size: int, stream=None) -> None:
+    _check("batch_swiglu_bf16x2",
+           LIB.toyinfer_batch_swiglu_bf16x2(_ptr(gate), _ptr(up), _ptr(intermedia), num_tokens,
+                                            size, _stream(stream)))
+
+
+def gather_embedding_bf16(table, token_ids, hidden_states, num_tokens: int, hidden_size: int,
+                          vocab_size: int = 0xFFFFFFFF, stream=None) -> None:
+    _check("gather_embedding_bf16",
+           LIB.toyinfer_gather_embedding_bf16(_ptr(table), _ptr(token_ids), _ptr(hidden_states),
+                                              num_tokens, hidden_size, vocab_size,
+                                              _stream(stream)))
+
+
+def argmax_f32(logits, n: int, out_index, stream=None) -> None:
+    _check("argmax_f32", LIB.toyinfer_argmax_f32(_ptr(logits), n, _ptr(out_index),
+                                                 _stream(stream)))
+

@@ -478,4 +478,71 @@ int toyinfer_batch_gemv_proj_bf16(const void* W, const void* hidden_states, void
                                            as_stream(stream)));
 }
 
+static bool bf16_ok(const void* p) { return p && aligned(p, 4); }
+
+int toyinfer_rmsnorm_bf16(const void* input, const void* weight, void* output, float* sum,
+                          float rms_norm_eps, uint32_t size, void* stream) {
+    return toyinfer_batch_rmsnorm_bf16(input, weight, output, sum, rms_norm_eps, 1, size, stream);
+}
+
+int toyinfer_batch_rmsnorm_bf16(const void* input, const void* weight, void* output, float* sum,
+                                float rms_norm_eps, uint32_t num_tokens, uint32_t size,
+                                void* stream) {
+    if (!bf16_ok(input) || !bf16_ok(weight) || !bf16_ok(output) || (sum && !aligned(sum, 4)) ||
+        num_tokens == 0 || size == 0 || size % 2 != 0)
+        return TOYINFER_ERR_INVALID_ARGUMENT;
+    return from_hip(launch_rmsnorm_rows(static_cast<const uint16_t*>(input),
+                                        static_cast<const uint16_t*>(weight),
+                                        static_cast<uint16_t*>(output), sum, rms_norm_eps,
+                                        num_tokens, size, as_stream(stream)));
+}
+
+int toyinfer_residual_add_bf16(const void* residual, void* hidden_state, uint32_t size,
+                               void* stream) {
+    return toyinfer_batch_residual_add_bf16(residual, hidden_state, 1, size, stream);
+}
+
+int toyinfer_batch_residual_add_bf16(const void* residual, void* hidden_state,
+                                     uint32_t num_tokens, uint32_t size, void* stream) {
+    const size_t n = (size_t)num_tokens * size;
+    if (!bf16_ok(residual) || !bf16_ok(hidden_state) || n == 0 || n % 2 != 0)
+        return TOYINFER_ERR_INVALID_ARGUMENT;
+    return from_hip(launch_residual_add(static_cast<const uint16_t*>(residual),
+                                        static_cast<uint16_t*>(hidden_state), n,
+                                        as_stream(stream)));
+}
+
+int toyinfer_swiglu_bf16x2(const void* gate, const void* up, void* intermedia, uint32_t size,
+                           void* stream) {
+    return toyinfer_batch_swiglu_bf16x2(gate, up, intermedia, 1, size, stream);
+}
+
+int toyinfer_batch_swiglu_bf16x2(const void* gate, const void* up, void* intermedia,
+                                 uint32_t num_tokens, uint32_t size, void* stream) {
+    const size_t n = (size_t)num_tokens * size;
+    if (!bf16_ok(gate) || !bf16_ok(up) || !bf16_ok(intermedia) || n == 0 || n % 2 != 0)
+        return TOYINFER_ERR_INVALID_ARGUMENT;
+    return from_hip(launch_swiglu(static_cast<const uint16_t*>(gate),
+                                  static_cast<const uint16_t*>(up),
+                                  static_cast<uint16_t*>(intermedia), n, as_stream(stream)));
+}
+
+int toyinfer_gather_embedding_bf16(const void* embedding_table, const uint32_t* token_ids,
+                                   void* hidden_states, uint32_t num_tokens,
+                                   uint32_t hidden_size, uint32_t vocab_size, void* stream) {
+    if (!bf16_ok(embedding_table) || !token_ids || !aligned(token_ids, 4) ||
+        !bf16_ok(hidden_states) || num_tokens == 0 || num_tokens > 65535u || hidden_size == 0 ||
+        hidden_size % 2 != 0 || vocab_size == 0 || 2ull * hidden_size > 0xffffffffull)
+        return TOYINFER_ERR_INVALID_ARGUMENT;
+    return from_hip(launch_gather_rows(static_cast<const uint16_t*>(embedding_table), token_ids,
+                                       static_cast<uint16_t*>(hidden_states), num_tokens,
+                                       hidden_size, vocab_size, as_stream(stream)));
+}
+
+int toyinfer_argmax_f32(const float* logits, uint32_t n, uint32_t* out_index, void* stream) {
+    if (!logits || !aligned(logits, 4) || !out_index || !aligned(out_index, 4) || n == 0)
+        return TOYINFER_ERR_INVALID_ARGUMENT;
+    return from_hip(launch_argmax(logits, n, out_index, nullptr, 1, as_stream(stream)));
+}
+
 }  // extern "C"

@@ -70,6 +70,17 @@ __device__ __forceinline__ float xor16_max(float x) {
     return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 
+// Sum over the 64 lanes of a wave, in every lane: DPP row steps, then the
+// lane^16 and lane^32 exchanges.
+__device__ __forceinline__ float wave_sum(float x) {
+    x += dpp_f32<kDppXor1>(x);
+    x += dpp_f32<kDppXor2>(x);
+    x += dpp_f32<kDppRowHalfMirror>(x);
+    x += dpp_f32<kDppRowMirror>(x);
+    x = xor16_sum(x);
+    return xor32_sum(x);
+}
+
 // Barrier for LDS hand-offs only: waits for this wave's LDS operations but
 // leaves its global loads in flight (a plain __syncthreads also drains them).
 __device__ __forceinline__ void lds_barrier() {

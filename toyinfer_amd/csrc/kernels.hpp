@@ -126,4 +126,27 @@ hipError_t launch_batch_proj_bf16(const uint16_t* W, const uint16_t* x, uint16_t
                                   uint32_t M, uint32_t N, hipStream_t stream);
 bool proj_uses_gemm(uint32_t T, uint32_t N, const void* W, const void* x);
 
+// ------------------------------------------------------------ model ops
+// rows x size RMSNorm (size even); sum_out[row] = sum of squares (nullable).
+hipError_t launch_rmsnorm_rows(const uint16_t* x, const uint16_t* w, uint16_t* y, float* sum_out,
+                               float eps, uint32_t rows, uint32_t size, hipStream_t stream);
+// hidden = bf16(hidden + residual) over n (even) values.
+hipError_t launch_residual_add(const uint16_t* residual, uint16_t* hidden, size_t n,
+                               hipStream_t stream);
+// out = bf16(up * silu(gate)) over n (even) values.
+hipError_t launch_swiglu(const uint16_t* gate, const uint16_t* up, uint16_t* out, size_t n,
+                         hipStream_t stream);
+// out[t] = table[ids[t]] for rows of `size` (even) values; ids >= vocab give zeros.
+hipError_t launch_gather_rows(const uint16_t* table, const uint32_t* ids, uint16_t* out,
+                              uint32_t tokens, uint32_t size, uint32_t vocab, hipStream_t stream);
+// First maximum of logits[0..n) -> out[0]; with pos_d, -> out[*pos_d + 1]
+// (if below out_cap) and *pos_d += 1.
+hipError_t launch_argmax(const float* logits, uint32_t n, uint32_t* out, uint32_t* pos_d,
+                         uint32_t out_cap, hipStream_t stream);
+// hidden = table[ids[p]], seq_len_d[0] = p + 1, p = min(*pos_d, cap - 1).
+hipError_t launch_decode_step_setup(const uint16_t* table, const uint32_t* ids,
+                                    const uint32_t* pos_d, uint16_t* hidden, uint32_t* seq_len_d,
+                                    uint32_t size, uint32_t vocab, uint32_t cap,
+                                    hipStream_t stream);
+
 }  // namespace tiattn

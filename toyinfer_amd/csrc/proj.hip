@@ -30,15 +30,6 @@ namespace {
 constexpr int kGvThreads = 256;
 constexpr uint32_t kOob = 0xF0000000u;  // a byte offset past every range below
 
-__device__ __forceinline__ float wave_sum(float x) {
-    x += dpp_f32<kDppXor1>(x);
-    x += dpp_f32<kDppXor2>(x);
-    x += dpp_f32<kDppRowHalfMirror>(x);
-    x += dpp_f32<kDppRowMirror>(x);
-    x = xor16_sum(x);
-    return xor32_sum(x);
-}
-
 // E bf16 values per load: 8 (16-byte chunks), 2 (bf16 pairs) or 1.
 template <int E>
 struct GvChunk {

@@ -1,0 +1,97 @@
+/* Minimal Qwen3 forward on one MI355X for the end-to-end configuration:
+ * prefill of a prompt, then greedy decode steps whose body (all layers, the
+ * lm-head, argmax and the position advance) can be captured once in a
+ * hipGraph and replayed, reading the position and the current token on the
+ * device.  This re-creates the part of the reference's Transformer that the
+ * attention path sits in (src/transformer.cpp:320-681): the prefill layer
+ * loop (:320-470), the decode body with its three-stream fork/join
+ * (:483-628) and the graph capture/replay (:630-681).  Weights are the
+ * caller's device buffers, laid out as the reference's loader produces them
+ * (projections [out][in] row-major bf16, norms [dim] bf16, tied or separate
+ * lm-head [vocab][hidden]).
+ *
+ * The model object owns its state (KV cache [layers][max_seq_len][Hkv*D],
+ * activations, rotary table, token list) in one device allocation made at
+ * create time, three streams (default priority) and the graph; no call
+ * after create allocates. */
+#ifndef TOYINFER_QWEN3_H_
+#define TOYINFER_QWEN3_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct toyinfer_qwen3_config {
+    uint32_t num_layers;
+    uint32_t hidden_size;
+    uint32_t num_q_heads;
+    uint32_t num_kv_heads;
+    uint32_t head_dim;           /* 64 or 128 */
+    uint32_t intermediate_size;
+    uint32_t vocab_size;
+    uint32_t max_seq_len;        /* KV-cache rows and the token list length */
+    uint32_t max_prefill_tokens; /* sizes the prefill activations */
+    float rms_norm_eps;
+    float rope_theta;
+} toyinfer_qwen3_config;
+
+typedef struct toyinfer_qwen3_layer {
+    const void* input_layernorm;          /* [hidden] */
+    const void* q_proj;                   /* [Hq*D][hidden] */
+    const void* k_proj;                   /* [Hkv*D][hidden] */
+    const void* v_proj;                   /* [Hkv*D][hidden] */
+    const void* q_norm;                   /* [D] */
+    const void* k_norm;                   /* [D] */
+    const void* o_proj;                   /* [hidden][Hq*D] */
+    const void* post_attention_layernorm; /* [hidden] */
+    const void* gate_proj;                /* [inter][hidden] */
+    const void* up_proj;                  /* [inter][hidden] */
+    const void* down_proj;                /* [hidden][inter] */
+} toyinfer_qwen3_layer;
+
+typedef struct toyinfer_qwen3 toyinfer_qwen3;
+
+/* Device bytes create() allocates for this configuration. */
+size_t toyinfer_qwen3_state_bytes(const toyinfer_qwen3_config* cfg);
+
+/* Checks the configuration and pointers, allocates the state, builds the
+ * inverse frequencies and rotary table.  `layers` (num_layers entries) is
+ * copied.  Returns a status of include/toyinfer_attn.h. */
+int toyinfer_qwen3_create(const toyinfer_qwen3_config* cfg, const void* embed_tokens,
+                          const void* final_norm, const void* lm_head,
+                          const toyinfer_qwen3_layer* layers, toyinfer_qwen3** out);
+void toyinfer_qwen3_destroy(toyinfer_qwen3* m);
+
+/* Runs the prompt token_ids_d[0..num_tokens) (device memory) through every
+ * layer (KV cache rows 0..num_tokens-1 written), the final norm and the
+ * lm-head on the last token, and the greedy pick: afterwards the logits,
+ * tokens[num_tokens] and the device position (= num_tokens) are set.
+ * Enqueued on the model's stream; returns without waiting. */
+int toyinfer_qwen3_prefill(toyinfer_qwen3* m, const uint32_t* token_ids_d, uint32_t num_tokens);
+
+/* `steps` greedy decode steps from the device position: each runs the token
+ * at tokens[pos] through the layers (KV row pos), writes tokens[pos + 1] and
+ * advances pos.  With use_graph the step body is captured on first use and
+ * replayed (one graph launch per step); without it the same kernels are
+ * launched directly.  pos + steps must stay below max_seq_len. */
+int toyinfer_qwen3_decode(toyinfer_qwen3* m, uint32_t steps, int use_graph);
+
+/* Waits for the model's stream. */
+int toyinfer_qwen3_synchronize(toyinfer_qwen3* m);
+
+/* Device views of the state: logits [vocab] fp32 of the last forward, the
+ * token list [max_seq_len] (prompt, then generated), the position. */
+const float* toyinfer_qwen3_logits(const toyinfer_qwen3* m);
+const uint32_t* toyinfer_qwen3_tokens(const toyinfer_qwen3* m);
+const uint32_t* toyinfer_qwen3_position(const toyinfer_qwen3* m);
+/* The hipStream_t the model enqueues on (stream 0 of its three). */
+void* toyinfer_qwen3_stream(const toyinfer_qwen3* m);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TOYINFER_QWEN3_H_ */

@@ -379,3 +379,62 @@ def argmax(logits):
     x = _c32(logits).reshape(-1)
     return int(lib().or_argmax(x, x.size))
 
+
+# ------------------------------------------------------------ Qwen3 forward
+
+class Qwen3Reference:
+    """The reference's Qwen3 forward (src/transformer.cpp:320-470 prefill,
+    :483-628 decode body, :625-630 final norm + lm-head) composed from the
+    restated kernels above, with the same rounding points: every projection,
+    norm, RoPE, attention, residual add and SwiGLU output rounded to bf16;
+    logits fp32.  Weights are float32 arrays holding bf16 values (dict as in
+    toyinfer_amd.qwen3, plus "inv_freq").  Caches [layers][max_seq_len][Hkv][D]."""
+
+    def __init__(self, cfg: dict, weights: dict):
+        self.cfg = cfg
+        self.w = weights
+        L, msl = cfg["num_layers"], cfg["max_seq_len"]
+        shape = (L, msl, cfg["num_kv_heads"], cfg["head_dim"])
+        self.kc = np.zeros(shape, np.float32)
+        self.vc = np.zeros(shape, np.float32)
+
+    def _layer(self, l, x, pos0):
+        c, W = self.cfg, self.w["layers"][l]
+        T = x.shape[0]
+        hq, hkv, d, eps = c["num_q_heads"], c["num_kv_heads"], c["head_dim"], c["rms_norm_eps"]
+        xn = rmsnorm_rows(x, W["input_layernorm"], eps)
+        q = round_bf16(gemv(W["q_proj"], xn))
+        k = round_bf16(gemv(W["k_proj"], xn))
+        v = round_bf16(gemv(W["v_proj"], xn))
+        q = rope(multi_rmsnorm(q, W["q_norm"], d, eps), self.w["inv_freq"], T, hq, d, pos0)
+        k = rope(multi_rmsnorm(k, W["k_norm"], d, eps), self.w["inv_freq"], T, hkv, d, pos0)
+        self.kc[l, pos0:pos0 + T] = k.reshape(T, hkv, d)
+        self.vc[l, pos0:pos0 + T] = v.reshape(T, hkv, d)
+        if T > 1:
+            assert pos0 == 0
+            o = round_bf16(flash_reference(q.reshape(T, hq, d), k.reshape(T, hkv, d),
+                                           v.reshape(T, hkv, d), nthreads=8))
+        else:
+            _, _, ob = decode_attention(q.reshape(hq, d), self.kc[l], self.vc[l], pos0,
+                                        c["max_seq_len"])
+            o = bf16_to_f32(ob)
+        a = round_bf16(gemv(W["o_proj"], o.reshape(T, hq * d)))
+        x = residual_add(x, a)
+        xn = rmsnorm_rows(x, W["post_attention_layernorm"], eps)
+        g = round_bf16(gemv(W["gate_proj"], xn))
+        u = round_bf16(gemv(W["up_proj"], xn))
+        dn = round_bf16(gemv(W["down_proj"], swiglu(g, u)))
+        return residual_add(x, dn)
+
+    def _logits(self, x_last):
+        xn = rmsnorm_rows(x_last[None, :], self.w["norm"], self.cfg["rms_norm_eps"])
+        return gemv(self.w["lm_head"], xn)[0]
+
+    def forward(self, token_ids, pos0):
+        """Tokens at positions pos0.. (a prompt from 0, or one decode token)
+        -> fp32 logits of the last one."""
+        x = self.w["embed_tokens"][np.asarray(token_ids, np.int64)]
+        for l in range(self.cfg["num_layers"]):
+            x = self._layer(l, x, pos0)
+        return self._logits(x[-1])
+

@@ -38,6 +38,49 @@ def test_every_declared_function_is_exported_and_bound():
     assert set(names) == set(attn.SIGNATURES), set(names) ^ set(attn.SIGNATURES)
 
 
+def test_model_header_functions_exported_and_bound():
+    """include/toyinfer_qwen3.h: every function exported and bound by
+    toyinfer_amd/qwen3.py (importing it binds them; no GPU call)."""
+    from toyinfer_amd import qwen3
+    text = re.sub(r"/\*.*?\*/", "", open(os.path.join(ROOT, "include", "toyinfer_qwen3.h")).read(),
+                  flags=re.S)
+    names = set(re.findall(r"\b(toyinfer_\w+)\s*\(", text))
+    assert len(names) == 10
+    out = subprocess.run(["nm", "-D", "--defined-only", attn.LIB_PATH], capture_output=True,
+                         text=True, check=True).stdout
+    assert names <= set(re.findall(r"\bT (toyinfer_\w+)", out))
+    assert names == set(qwen3._SIGS)
+
+
+def test_model_config_validation():
+    """Configuration and pointer checks run before any allocation."""
+    import ctypes
+
+    from toyinfer_amd import qwen3
+    good = dict(num_layers=2, hidden_size=256, num_q_heads=4, num_kv_heads=2, head_dim=64,
+                intermediate_size=512, vocab_size=1000, max_seq_len=64, max_prefill_tokens=32,
+                rms_norm_eps=1e-6, rope_theta=1e6)
+    cfg = qwen3.Config(**good)
+    assert L.toyinfer_qwen3_state_bytes(ctypes.byref(cfg)) > 2 * 2 * 64 * 128 * 2
+    for bad in (dict(head_dim=96), dict(num_kv_heads=3), dict(max_prefill_tokens=64),
+                dict(hidden_size=100), dict(rms_norm_eps=0.0), dict(num_layers=0)):
+        c = qwen3.Config(**dict(good, **bad))
+        assert L.toyinfer_qwen3_state_bytes(ctypes.byref(c)) == 0, bad
+    layers = (qwen3.Layer * 2)()
+    for i in range(2):
+        for n in qwen3.LAYER_FIELDS:
+            setattr(layers[i], n, P)
+    h = ctypes.c_void_p()
+    create = L.toyinfer_qwen3_create
+    layers[1].down_proj = P + 8                            # weights need 16-byte alignment
+    assert create(ctypes.byref(cfg), P, P, P, layers, ctypes.byref(h)) == INVALID
+    assert create(ctypes.byref(cfg), None, P, P, layers, ctypes.byref(h)) == INVALID
+    c = qwen3.Config(**dict(good, head_dim=96))
+    assert create(ctypes.byref(c), P, P, P, layers, ctypes.byref(h)) == UNSUPPORTED
+    assert L.toyinfer_qwen3_prefill(None, P, 4) == INVALID
+    assert L.toyinfer_qwen3_decode(None, 1, 1) == INVALID
+
+
 def test_abi_version_and_status_strings():
     assert L.toyinfer_abi_version() == 1
     assert attn.status_string(0) == "ok"

@@ -1,0 +1,152 @@
+"""The Qwen3 model harness (include/toyinfer_qwen3.h) on a small random model:
+prefill and greedy decode against the oracle's forward (oracle.Qwen3Reference,
+the reference's operation order and rounding points), and the hipGraph decode
+against the same steps launched directly.
+
+Bars: logits within LOGIT_MAX_ABS / LOGIT_MEAN_ABS of the oracle's (both are
+fp32 sums over bf16 activations; the GEMV/GEMM/attention reduction orders
+differ, so a bf16 activation can land one rounding step apart and carry that
+through the later layers; on this model the logits spread 0.8 and the
+measured differences are a few thousandths on average, under 2e-2 at most);
+the device argmax equal to the oracle's argmax of the device logits (exact);
+graph and direct decode bit-identical.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from tests import helpers as H
+from toyinfer_amd import qwen3, synth
+
+pytestmark = pytest.mark.gpu
+
+LOGIT_MAX_ABS = 5e-2   # measured: 1.1-1.8e-2
+LOGIT_MEAN_ABS = 1e-2  # measured: 2.7-3.8e-3
+
+TINY = dict(num_layers=2, hidden_size=256, num_q_heads=4, num_kv_heads=2, head_dim=64,
+            intermediate_size=512, vocab_size=1000, max_seq_len=64, max_prefill_tokens=32,
+            rms_norm_eps=1e-6, rope_theta=1e6)
+
+
+def scaled_bf16(seed, name, shape, std):
+    bits = synth.normal_bf16(seed, name, shape)
+    return oracle.f32_to_bf16(H.bf16_bits_to_f32(bits) * np.float32(std))
+
+
+def make_weights(cfg, dev, seed=50, tied=False):
+    """Random-init weights (projections N(0, 0.05^2), embeddings N(0, 1),
+    norms U(0.8, 1.2)): (float32 host dict for the oracle, device dict)."""
+    shapes = qwen3.layer_shapes(qwen3.Config(**cfg))
+    host = {"layers": []}
+    dev_w = {"layers": []}
+    for l in range(cfg["num_layers"]):
+        hl, dl = {}, {}
+        for n, shp in shapes.items():
+            if len(shp) == 1:
+                b = synth.uniform_bf16(seed, f"{l}.{n}", shp, 0.8, 1.2)
+            else:
+                b = scaled_bf16(seed, f"{l}.{n}", shp, 0.05)
+            hl[n] = H.bf16_bits_to_f32(b)
+            dl[n] = H.to_dev_bf16(b, dev)
+        host["layers"].append(hl)
+        dev_w["layers"].append(dl)
+    V, Hd = cfg["vocab_size"], cfg["hidden_size"]
+    emb = synth.normal_bf16(seed, "embed", (V, Hd))
+    norm = synth.uniform_bf16(seed, "norm", (Hd,), 0.8, 1.2)
+    head = emb if tied else scaled_bf16(seed, "lm_head", (V, Hd), 0.05)
+    for n, b in (("embed_tokens", emb), ("norm", norm), ("lm_head", head)):
+        host[n] = H.bf16_bits_to_f32(b)
+        dev_w[n] = H.to_dev_bf16(b, dev)
+    host["inv_freq"] = oracle.inv_freq(cfg["head_dim"], cfg["rope_theta"])
+    return host, dev_w
+
+
+def prompt(n, vocab, seed=51):
+    rng = np.random.default_rng(seed)
+    return rng.integers(0, vocab, size=n).astype(np.uint32)
+
+
+def ids_dev(ids, dev):
+    return torch.from_numpy(ids.view(np.int32)).to(dev)
+
+
+def check_logits(got, exp, label):
+    d = np.abs(got.astype(np.float64) - exp)
+    assert np.isfinite(got).all(), f"{label}: non-finite logits"
+    assert d.max() <= LOGIT_MAX_ABS and d.mean() <= LOGIT_MEAN_ABS, \
+        f"{label}: max {d.max():.3g} mean {d.mean():.3g} (logit std {exp.std():.3g})"
+
+
+@pytest.mark.parametrize("T", [1, 20, 32])
+def test_prefill_vs_oracle(dev, T):
+    print(f"[step] qwen3 prefill T={T}", flush=True)
+    cfg = TINY
+    host, dw = make_weights(cfg, dev)
+    ids = prompt(T, cfg["vocab_size"])
+    m = qwen3.Qwen3(qwen3.Config(**cfg), dw)
+    H.sync()
+    m.prefill(ids_dev(ids, dev), T)
+    got = m.logits_host()
+    ref = oracle.Qwen3Reference(cfg, host)
+    check_logits(got, ref.forward(ids, 0), f"prefill T={T}")
+    toks = m.tokens_host(T + 1)
+    assert np.array_equal(toks[:T], ids)
+    assert toks[T] == oracle.argmax(got), "device argmax"
+    assert m.position_host() == T
+    m.close()
+
+
+@pytest.mark.parametrize("graph", [False, True])
+def test_decode_vs_oracle(dev, graph):
+    """Greedy steps after a 12-token prompt; each step's logits against the
+    oracle fed the same tokens (so a near-tie cannot derail the comparison)."""
+    print(f"[step] qwen3 decode graph={graph}", flush=True)
+    cfg = TINY
+    host, dw = make_weights(cfg, dev)
+    T, steps = 12, 6
+    ids = prompt(T, cfg["vocab_size"])
+    m = qwen3.Qwen3(qwen3.Config(**cfg), dw)
+    H.sync()
+    m.prefill(ids_dev(ids, dev), T)
+    ref = oracle.Qwen3Reference(cfg, host)
+    ref.forward(ids, 0)
+    for s in range(steps):
+        m.decode(1, graph)
+        got = m.logits_host()
+        toks = m.tokens_host(T + s + 2)
+        exp = ref.forward([toks[T + s]], T + s)
+        check_logits(got, exp, f"step {s}")
+        assert toks[T + s + 1] == oracle.argmax(got), f"step {s} device argmax"
+    assert m.position_host() == T + steps
+    m.close()
+
+
+def test_graph_equals_direct_launches(dev):
+    """Two models, same weights and prompt: 3 + 5 graph replays (one capture)
+    vs 8 directly launched steps give the same tokens and identical logits."""
+    cfg = dict(TINY, num_layers=3)
+    _, dw = make_weights(cfg, dev, seed=52, tied=True)
+    T = 9
+    ids = prompt(T, cfg["vocab_size"], seed=53)
+    a = qwen3.Qwen3(qwen3.Config(**cfg), dw)
+    b = qwen3.Qwen3(qwen3.Config(**cfg), dw)
+    H.sync()
+    for m in (a, b):
+        m.prefill(ids_dev(ids, dev), T)
+    a.decode(8, False)
+    b.decode(3, True)
+    b.decode(5, True)
+    assert np.array_equal(a.tokens_host(T + 9), b.tokens_host(T + 9))
+    assert np.array_equal(a.logits_host().view(np.uint32), b.logits_host().view(np.uint32))
+    assert a.position_host() == b.position_host() == T + 8
+    a.close()
+    b.close()
+
+
+def test_create_rejects_bad_config(dev):
+    _, dw = make_weights(TINY, dev)
+    for bad in (dict(head_dim=96), dict(num_kv_heads=3), dict(max_prefill_tokens=64),
+                dict(hidden_size=100)):
+        with pytest.raises(Exception):
+            qwen3.Qwen3(qwen3.Config(**dict(TINY, **bad)), dw)

@@ -143,6 +143,8 @@ hipError_t launch_gather_rows(const uint16_t* table, const uint32_t* ids, uint16
 // (if below out_cap) and *pos_d += 1.
 hipError_t launch_argmax(const float* logits, uint32_t n, uint32_t* out, uint32_t* pos_d,
                          uint32_t out_cap, hipStream_t stream);
+// *p = value, as a one-lane kernel (stream-ordered, capturable).
+hipError_t launch_set_u32(uint32_t* p, uint32_t value, hipStream_t stream);
 // hidden = table[ids[p]], seq_len_d[0] = p + 1, p = min(*pos_d, cap - 1).
 hipError_t launch_decode_step_setup(const uint16_t* table, const uint32_t* ids,
                                     const uint32_t* pos_d, uint16_t* hidden, uint32_t* seq_len_d,

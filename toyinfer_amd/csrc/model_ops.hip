@@ -227,6 +227,8 @@ __global__ void decode_step_setup_kernel(const uint16_t* __restrict__ table,
     }
 }
 
+__global__ void set_u32_kernel(uint32_t* p, uint32_t v) { *p = v; }
+
 bool vec8_ok(uint32_t size, std::initializer_list<const void*> ptrs) {
     if (size % 8 != 0) return false;
     for (const void* p : ptrs)
@@ -295,6 +297,11 @@ hipError_t launch_decode_step_setup(const uint16_t* table, const uint32_t* ids,
     else
         decode_step_setup_kernel<2><<<(size / 2 + kT - 1) / kT, kT, 0, stream>>>(
             table, ids, pos_d, hidden, seq_len_d, size, vocab, cap);
+    return hipGetLastError();
+}
+
+hipError_t launch_set_u32(uint32_t* p, uint32_t value, hipStream_t stream) {
+    set_u32_kernel<<<1, 1, 0, stream>>>(p, value);
     return hipGetLastError();
 }
 

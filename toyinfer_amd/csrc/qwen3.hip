@@ -1,0 +1,349 @@
+// Minimal Qwen3 forward (include/toyinfer_qwen3.h): the prefill layer loop
+// and the greedy decode body around the attention path, with the decode body
+// captured once in a hipGraph and replayed.
+//
+// Reference: src/transformer.cpp:320-470 (prefill), :483-628 (decode body,
+// three-stream fork/join), :630-681 (graph capture / replay).  Differences,
+// all keeping the reference's rounding points:
+//  * prefill: q_norm/k_norm + RoPE are fused into the attention call, which
+//    writes the normalised, rotated K straight into the layer's cache rows;
+//    the V projection writes straight into the cache rows (no D2D copies);
+//    the residual stream stays in `hidden` (no residual copy);
+//  * decode: the six pre-attention launches are one (decode_qkv_prologue),
+//    attention is the split-K kernel with the length read on the device, and
+//    the body ends with a device argmax that appends the next token and
+//    advances the position, so consecutive graph replays need no host work;
+//  * no memset nodes (the reference's rmsnorm clears its sum with one).
+#include <hip/hip_runtime.h>
+
+#include <new>
+#include <vector>
+
+#include "../../include/toyinfer_attn.h"
+#include "../../include/toyinfer_qwen3.h"
+#include "kernels.hpp"
+
+using namespace tiattn;
+
+struct toyinfer_qwen3 {
+    toyinfer_qwen3_config cfg{};
+    const void* embed = nullptr;
+    const void* final_norm = nullptr;
+    const void* lm_head = nullptr;
+    std::vector<toyinfer_qwen3_layer> layers;
+
+    char* mem = nullptr;
+    uint32_t* tokens = nullptr;
+    uint32_t* pos = nullptr;
+    uint32_t* seq_len = nullptr;
+    float* inv_freq = nullptr;
+    float* rope = nullptr;
+    float* logits = nullptr;
+    uint16_t* k_cache = nullptr;
+    uint16_t* v_cache = nullptr;
+    // prefill activations, [max_prefill_tokens][...]
+    uint16_t *p_hidden, *p_xn, *p_q, *p_k, *p_o, *p_tmp, *p_gate, *p_up, *p_inter;
+    // decode activations, one token
+    uint16_t *d_hidden, *d_xn, *d_q, *d_k, *d_v, *d_o, *d_tmp, *d_gate, *d_up, *d_inter;
+    void* attn_ws = nullptr;
+    size_t attn_ws_bytes = 0;
+    uint32_t splits = 0;
+
+    hipStream_t s[3] = {nullptr, nullptr, nullptr};
+    hipEvent_t ev[3] = {nullptr, nullptr, nullptr};
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+};
+
+namespace {
+
+#define TRY(x)                                   \
+    do {                                         \
+        const int st_ = (x);                     \
+        if (st_ != TOYINFER_OK) return st_;      \
+    } while (0)
+#define TRYH(x)                                                   \
+    do {                                                          \
+        if ((x) != hipSuccess) return TOYINFER_ERR_HIP;           \
+    } while (0)
+
+size_t up256(size_t x) { return (x + 255) / 256 * 256; }
+
+// Offsets of every state buffer in the one allocation (dry run when m is null).
+size_t carve(const toyinfer_qwen3_config& c, uint32_t splits, toyinfer_qwen3* m) {
+    size_t off = 0;
+    auto take = [&](size_t bytes) {
+        const size_t o = off;
+        off = up256(off + bytes);
+        return o;
+    };
+    const size_t kv = (size_t)c.num_kv_heads * c.head_dim, qd = (size_t)c.num_q_heads * c.head_dim;
+    const size_t P = c.max_prefill_tokens, H = c.hidden_size, F = c.intermediate_size;
+    const size_t o_tokens = take(4ull * c.max_seq_len);
+    const size_t o_pos = take(4), o_len = take(4);
+    const size_t o_inv = take(4ull * c.head_dim / 2);
+    const size_t o_rope = take(4ull * c.max_seq_len * c.head_dim);
+    const size_t o_logits = take(4ull * c.vocab_size);
+    const size_t o_kc = take(2ull * c.num_layers * c.max_seq_len * kv);
+    const size_t o_vc = take(2ull * c.num_layers * c.max_seq_len * kv);
+    size_t o_p[9], o_d[10];
+    const size_t p_sizes[9] = {P * H, P * H, P * qd, P * kv, P * qd, P * H, P * F, P * F, P * F};
+    for (int i = 0; i < 9; ++i) o_p[i] = take(2 * p_sizes[i]);
+    const size_t d_sizes[10] = {H, H, qd, kv, kv, qd, H, F, F, F};
+    for (int i = 0; i < 10; ++i) o_d[i] = take(2 * d_sizes[i]);
+    const size_t ws = toyinfer_decode_workspace_bytes(1, c.num_q_heads, c.head_dim, splits);
+    const size_t o_ws = take(ws);
+    if (m) {
+        char* b = m->mem;
+        m->tokens = reinterpret_cast<uint32_t*>(b + o_tokens);
+        m->pos = reinterpret_cast<uint32_t*>(b + o_pos);
+        m->seq_len = reinterpret_cast<uint32_t*>(b + o_len);
+        m->inv_freq = reinterpret_cast<float*>(b + o_inv);
+        m->rope = reinterpret_cast<float*>(b + o_rope);
+        m->logits = reinterpret_cast<float*>(b + o_logits);
+        m->k_cache = reinterpret_cast<uint16_t*>(b + o_kc);
+        m->v_cache = reinterpret_cast<uint16_t*>(b + o_vc);
+        uint16_t** pp[9] = {&m->p_hidden, &m->p_xn, &m->p_q, &m->p_k, &m->p_o,
+                            &m->p_tmp, &m->p_gate, &m->p_up, &m->p_inter};
+        for (int i = 0; i < 9; ++i) *pp[i] = reinterpret_cast<uint16_t*>(b + o_p[i]);
+        uint16_t** dp[10] = {&m->d_hidden, &m->d_xn, &m->d_q, &m->d_k, &m->d_v,
+                             &m->d_o, &m->d_tmp, &m->d_gate, &m->d_up, &m->d_inter};
+        for (int i = 0; i < 10; ++i) *dp[i] = reinterpret_cast<uint16_t*>(b + o_d[i]);
+        m->attn_ws = b + o_ws;
+        m->attn_ws_bytes = ws;
+    }
+    return off;
+}
+
+bool a16(const void* p) { return p && ((uintptr_t)p & 15) == 0; }
+
+int check_config(const toyinfer_qwen3_config* c) {
+    if (!c) return TOYINFER_ERR_INVALID_ARGUMENT;
+    if (c->head_dim != 64 && c->head_dim != 128) return TOYINFER_ERR_UNSUPPORTED;
+    if (c->num_layers == 0 || c->num_q_heads == 0 || c->num_kv_heads == 0 ||
+        c->num_q_heads % c->num_kv_heads != 0 || c->num_q_heads > 64 ||
+        c->hidden_size == 0 || c->hidden_size % 64 != 0 || c->intermediate_size == 0 ||
+        c->intermediate_size % 64 != 0 || c->vocab_size == 0 || c->max_seq_len < 2 ||
+        c->max_prefill_tokens == 0 || c->max_prefill_tokens >= c->max_seq_len ||
+        c->max_prefill_tokens > 65535u || c->hidden_size > (1u << 22) ||
+        c->intermediate_size > (1u << 22) || !(c->rms_norm_eps > 0.0f) ||
+        !(c->rope_theta > 0.0f))
+        return TOYINFER_ERR_INVALID_ARGUMENT;
+    return TOYINFER_OK;
+}
+
+hipStream_t S(const toyinfer_qwen3* m, int i) { return m->s[i]; }
+
+// One decode step for the token at tokens[*pos]; ends with tokens[*pos + 1]
+// and *pos += 1.  Only kernel launches and event record/wait: capturable.
+int decode_body(toyinfer_qwen3* m) {
+    const toyinfer_qwen3_config& c = m->cfg;
+    const uint32_t H = c.hidden_size, F = c.intermediate_size, V = c.vocab_size;
+    const uint32_t hq = c.num_q_heads, hkv = c.num_kv_heads, d = c.head_dim;
+    const uint32_t qd = hq * d, kv = hkv * d, msl = c.max_seq_len;
+    const float eps = c.rms_norm_eps;
+    void* s0 = S(m, 0);
+    void* s1 = S(m, 1);
+    void* s2 = S(m, 2);
+    TRYH(launch_decode_step_setup(static_cast<const uint16_t*>(m->embed), m->tokens, m->pos,
+                                  m->d_hidden, m->seq_len, H, V, msl, S(m, 0)));
+    for (uint32_t l = 0; l < c.num_layers; ++l) {
+        const toyinfer_qwen3_layer& L = m->layers[l];
+        uint16_t* kc = m->k_cache + (size_t)l * msl * kv;
+        uint16_t* vc = m->v_cache + (size_t)l * msl * kv;
+        TRY(toyinfer_rmsnorm_bf16(m->d_hidden, L.input_layernorm, m->d_xn, nullptr, eps, H, s0));
+        // q on stream 0, k and v on streams 1 and 2 (src/transformer.cpp:513-533).
+        TRYH(hipEventRecord(m->ev[0], S(m, 0)));
+        TRYH(hipStreamWaitEvent(S(m, 1), m->ev[0], 0));
+        TRYH(hipStreamWaitEvent(S(m, 2), m->ev[0], 0));
+        TRY(toyinfer_gemv_proj_bf16(L.q_proj, m->d_xn, m->d_q, qd, H, s0));
+        TRY(toyinfer_gemv_proj_bf16(L.k_proj, m->d_xn, m->d_k, kv, H, s1));
+        TRY(toyinfer_gemv_proj_bf16(L.v_proj, m->d_xn, m->d_v, kv, H, s2));
+        TRYH(hipEventRecord(m->ev[1], S(m, 1)));
+        TRYH(hipEventRecord(m->ev[2], S(m, 2)));
+        TRYH(hipStreamWaitEvent(S(m, 0), m->ev[1], 0));
+        TRYH(hipStreamWaitEvent(S(m, 0), m->ev[2], 0));
+        TRY(toyinfer_decode_qkv_prologue_bf16(m->d_q, m->d_k, m->d_v, L.q_norm, L.k_norm,
+                                              m->inv_freq, m->pos, msl, eps, m->d_q, kc, vc, hq,
+                                              hkv, d, s0));
+        TRY(toyinfer_decode_attention_bf16(m->d_q, kc, vc, m->d_o, 1, hq, hkv, d, m->seq_len, msl,
+                                           0, m->splits, m->attn_ws, m->attn_ws_bytes, s0));
+        TRY(toyinfer_gemv_proj_bf16(L.o_proj, m->d_o, m->d_tmp, H, qd, s0));
+        TRY(toyinfer_residual_add_bf16(m->d_tmp, m->d_hidden, H, s0));
+        TRY(toyinfer_rmsnorm_bf16(m->d_hidden, L.post_attention_layernorm, m->d_xn, nullptr, eps,
+                                  H, s0));
+        // gate on stream 0, up on stream 1 (src/transformer.cpp:595-610).
+        TRYH(hipEventRecord(m->ev[0], S(m, 0)));
+        TRYH(hipStreamWaitEvent(S(m, 1), m->ev[0], 0));
+        TRY(toyinfer_gemv_proj_bf16(L.gate_proj, m->d_xn, m->d_gate, F, H, s0));
+        TRY(toyinfer_gemv_proj_bf16(L.up_proj, m->d_xn, m->d_up, F, H, s1));
+        TRYH(hipEventRecord(m->ev[1], S(m, 1)));
+        TRYH(hipStreamWaitEvent(S(m, 0), m->ev[1], 0));
+        TRY(toyinfer_swiglu_bf16x2(m->d_gate, m->d_up, m->d_inter, F, s0));
+        TRY(toyinfer_gemv_proj_bf16(L.down_proj, m->d_inter, m->d_tmp, H, F, s0));
+        TRY(toyinfer_residual_add_bf16(m->d_tmp, m->d_hidden, H, s0));
+    }
+    TRY(toyinfer_rmsnorm_bf16(m->d_hidden, m->final_norm, m->d_xn, nullptr, eps, H, s0));
+    TRY(toyinfer_gemv_proj_bf162float(m->lm_head, m->d_xn, m->logits, V, H, s0));
+    TRYH(launch_argmax(m->logits, V, m->tokens, m->pos, msl, S(m, 0)));
+    return TOYINFER_OK;
+}
+
+void release(toyinfer_qwen3* m) {
+    if (!m) return;
+    if (m->exec) (void)hipGraphExecDestroy(m->exec);
+    if (m->graph) (void)hipGraphDestroy(m->graph);
+    for (int i = 0; i < 3; ++i) {
+        if (m->ev[i]) (void)hipEventDestroy(m->ev[i]);
+        if (m->s[i]) (void)hipStreamDestroy(m->s[i]);
+    }
+    if (m->mem) (void)hipFree(m->mem);
+    delete m;
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t toyinfer_qwen3_state_bytes(const toyinfer_qwen3_config* cfg) {
+    if (check_config(cfg) != TOYINFER_OK) return 0;
+    const uint32_t splits = toyinfer_decode_default_splits(1, cfg->num_q_heads, cfg->num_kv_heads,
+                                                           cfg->head_dim, cfg->max_seq_len);
+    return carve(*cfg, splits, nullptr);
+}
+
+int toyinfer_qwen3_create(const toyinfer_qwen3_config* cfg, const void* embed_tokens,
+                          const void* final_norm, const void* lm_head,
+                          const toyinfer_qwen3_layer* layers, toyinfer_qwen3** out) {
+    if (!out) return TOYINFER_ERR_INVALID_ARGUMENT;
+    *out = nullptr;
+    TRY(check_config(cfg));
+    if (!a16(embed_tokens) || !a16(final_norm) || !a16(lm_head) || !layers)
+        return TOYINFER_ERR_INVALID_ARGUMENT;
+    for (uint32_t l = 0; l < cfg->num_layers; ++l) {
+        const toyinfer_qwen3_layer& L = layers[l];
+        const void* w[11] = {L.input_layernorm, L.q_proj,  L.k_proj, L.v_proj,
+                             L.q_norm,          L.k_norm,  L.o_proj, L.post_attention_layernorm,
+                             L.gate_proj,       L.up_proj, L.down_proj};
+        for (const void* p : w)
+            if (!a16(p)) return TOYINFER_ERR_INVALID_ARGUMENT;
+    }
+    toyinfer_qwen3* m = new (std::nothrow) toyinfer_qwen3();
+    if (!m) return TOYINFER_ERR_HIP;
+    m->cfg = *cfg;
+    m->embed = embed_tokens;
+    m->final_norm = final_norm;
+    m->lm_head = lm_head;
+    m->layers.assign(layers, layers + cfg->num_layers);
+    m->splits = toyinfer_decode_default_splits(1, cfg->num_q_heads, cfg->num_kv_heads,
+                                               cfg->head_dim, cfg->max_seq_len);
+    const size_t bytes = carve(*cfg, m->splits, nullptr);
+    bool ok = hipMalloc(&m->mem, bytes) == hipSuccess;
+    for (int i = 0; ok && i < 3; ++i)
+        ok = hipStreamCreateWithFlags(&m->s[i], hipStreamNonBlocking) == hipSuccess &&
+             hipEventCreateWithFlags(&m->ev[i], hipEventDisableTiming) == hipSuccess;
+    if (!ok) {
+        release(m);
+        return TOYINFER_ERR_HIP;
+    }
+    carve(*cfg, m->splits, m);
+    int st = toyinfer_precompute_freq_f32(m->inv_freq, (int)cfg->head_dim, cfg->rope_theta, m->s[0]);
+    if (st == TOYINFER_OK)
+        st = toyinfer_rope_cos_sin_f32(m->rope, m->inv_freq, cfg->max_seq_len, cfg->head_dim,
+                                       m->s[0]);
+    if (st == TOYINFER_OK && launch_set_u32(m->pos, 0, m->s[0]) != hipSuccess) st = TOYINFER_ERR_HIP;
+    if (st == TOYINFER_OK && hipStreamSynchronize(m->s[0]) != hipSuccess) st = TOYINFER_ERR_HIP;
+    if (st != TOYINFER_OK) {
+        release(m);
+        return st;
+    }
+    *out = m;
+    return TOYINFER_OK;
+}
+
+void toyinfer_qwen3_destroy(toyinfer_qwen3* m) {
+    if (!m) return;
+    for (int i = 0; i < 3; ++i)
+        if (m->s[i]) (void)hipStreamSynchronize(m->s[i]);
+    release(m);
+}
+
+int toyinfer_qwen3_prefill(toyinfer_qwen3* m, const uint32_t* token_ids_d, uint32_t num_tokens) {
+    if (!m || !token_ids_d || ((uintptr_t)token_ids_d & 3) || num_tokens == 0 ||
+        num_tokens > m->cfg.max_prefill_tokens)
+        return TOYINFER_ERR_INVALID_ARGUMENT;
+    const toyinfer_qwen3_config& c = m->cfg;
+    const uint32_t T = num_tokens, H = c.hidden_size, F = c.intermediate_size, V = c.vocab_size;
+    const uint32_t hq = c.num_q_heads, hkv = c.num_kv_heads, d = c.head_dim;
+    const uint32_t qd = hq * d, kv = hkv * d, msl = c.max_seq_len;
+    const float eps = c.rms_norm_eps;
+    void* s0 = m->s[0];
+    TRYH(hipMemcpyAsync(m->tokens, token_ids_d, 4ull * T, hipMemcpyDeviceToDevice, m->s[0]));
+    TRY(toyinfer_gather_embedding_bf16(m->embed, m->tokens, m->p_hidden, T, H, V, s0));
+    for (uint32_t l = 0; l < c.num_layers; ++l) {
+        const toyinfer_qwen3_layer& L = m->layers[l];
+        uint16_t* kc = m->k_cache + (size_t)l * msl * kv;
+        uint16_t* vc = m->v_cache + (size_t)l * msl * kv;
+        TRY(toyinfer_batch_rmsnorm_bf16(m->p_hidden, L.input_layernorm, m->p_xn, nullptr, eps, T,
+                                        H, s0));
+        TRY(toyinfer_batch_gemv_proj_bf16(L.q_proj, m->p_xn, m->p_q, T, qd, H, s0));
+        TRY(toyinfer_batch_gemv_proj_bf16(L.k_proj, m->p_xn, m->p_k, T, kv, H, s0));
+        TRY(toyinfer_batch_gemv_proj_bf16(L.v_proj, m->p_xn, vc, T, kv, H, s0));
+        TRY(toyinfer_prefill_qknorm_rope_attention_bf16(m->p_q, m->p_k, vc, m->p_o, kc, L.q_norm,
+                                                        L.k_norm, m->rope, eps, hq, hkv, d, T,
+                                                        s0));
+        TRY(toyinfer_batch_gemv_proj_bf16(L.o_proj, m->p_o, m->p_tmp, T, H, qd, s0));
+        TRY(toyinfer_batch_residual_add_bf16(m->p_tmp, m->p_hidden, T, H, s0));
+        TRY(toyinfer_batch_rmsnorm_bf16(m->p_hidden, L.post_attention_layernorm, m->p_xn, nullptr,
+                                        eps, T, H, s0));
+        TRY(toyinfer_batch_gemv_proj_bf16(L.gate_proj, m->p_xn, m->p_gate, T, F, H, s0));
+        TRY(toyinfer_batch_gemv_proj_bf16(L.up_proj, m->p_xn, m->p_up, T, F, H, s0));
+        TRY(toyinfer_batch_swiglu_bf16x2(m->p_gate, m->p_up, m->p_inter, T, F, s0));
+        TRY(toyinfer_batch_gemv_proj_bf16(L.down_proj, m->p_inter, m->p_tmp, T, H, F, s0));
+        TRY(toyinfer_batch_residual_add_bf16(m->p_tmp, m->p_hidden, T, H, s0));
+    }
+    TRY(toyinfer_rmsnorm_bf16(m->p_hidden + (size_t)(T - 1) * H, m->final_norm, m->d_xn, nullptr,
+                              eps, H, s0));
+    TRY(toyinfer_gemv_proj_bf162float(m->lm_head, m->d_xn, m->logits, V, H, s0));
+    TRYH(launch_set_u32(m->pos, T - 1, m->s[0]));
+    TRYH(launch_argmax(m->logits, V, m->tokens, m->pos, msl, m->s[0]));
+    return TOYINFER_OK;
+}
+
+int toyinfer_qwen3_decode(toyinfer_qwen3* m, uint32_t steps, int use_graph) {
+    if (!m || steps >= m->cfg.max_seq_len) return TOYINFER_ERR_INVALID_ARGUMENT;
+    if (!use_graph) {
+        for (uint32_t i = 0; i < steps; ++i) TRY(decode_body(m));
+        return TOYINFER_OK;
+    }
+    if (!m->exec) {
+        TRYH(hipStreamBeginCapture(m->s[0], hipStreamCaptureModeRelaxed));
+        const int st = decode_body(m);
+        hipGraph_t g = nullptr;
+        const hipError_t e = hipStreamEndCapture(m->s[0], &g);
+        if (st != TOYINFER_OK || e != hipSuccess) {
+            if (g) (void)hipGraphDestroy(g);
+            return st != TOYINFER_OK ? st : TOYINFER_ERR_HIP;
+        }
+        if (hipGraphInstantiate(&m->exec, g, nullptr, nullptr, 0) != hipSuccess) {
+            (void)hipGraphDestroy(g);
+            m->exec = nullptr;
+            return TOYINFER_ERR_HIP;
+        }
+        m->graph = g;
+    }
+    for (uint32_t i = 0; i < steps; ++i) TRYH(hipGraphLaunch(m->exec, m->s[0]));
+    return TOYINFER_OK;
+}
+
+int toyinfer_qwen3_synchronize(toyinfer_qwen3* m) {
+    if (!m) return TOYINFER_ERR_INVALID_ARGUMENT;
+    return hipStreamSynchronize(m->s[0]) == hipSuccess ? TOYINFER_OK : TOYINFER_ERR_HIP;
+}
+
+const float* toyinfer_qwen3_logits(const toyinfer_qwen3* m) { return m ? m->logits : nullptr; }
+const uint32_t* toyinfer_qwen3_tokens(const toyinfer_qwen3* m) { return m ? m->tokens : nullptr; }
+const uint32_t* toyinfer_qwen3_position(const toyinfer_qwen3* m) { return m ? m->pos : nullptr; }
+void* toyinfer_qwen3_stream(const toyinfer_qwen3* m) { return m ? m->s[0] : nullptr; }
+
+}  // extern "C"

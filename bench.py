@@ -18,7 +18,9 @@ the north-star targets name, each with its own roofline block:
   * decode_step / decode_contract: the decode-step pre-pass and the
     reference-contract graph decode;
   * proj_gemv / proj_gemm: the projections either side of attention (lm-head
-    GEMV, HBM-bound; a 4096-token prefill projection, MFMA-bound).
+    GEMV, HBM-bound; a 4096-token prefill projection, MFMA-bound);
+  * qwen3_e2e: configs[4], random-init Qwen3-0.6B, TTFT of a 1371-token
+    prompt and greedy decode tokens/s from a captured hipGraph.
 Decode steps rotate over 4 independent KV sets (512 MiB) so every step reads
 KV that is not resident in the 256 MB Infinity Cache.
 
@@ -58,7 +60,8 @@ def traffic_bytes(workload):
     r, w = PMC_KIB[workload]
     return int(round((r * FETCH_SCALE + w * WRITE_SCALE) * 1024))
 WORKLOADS = ("all", "prefill", "prefill_fused", "decode_b8_l4096", "decode_b1_l32768",
-             "decode_step", "decode_contract", "proj_gemv", "proj_gemm", "copy_calibration")
+             "decode_step", "decode_contract", "proj_gemv", "proj_gemm", "qwen3_e2e",
+             "copy_calibration")
 
 
 def causal_flops(s, hq, d):
@@ -328,6 +331,67 @@ def bench_proj_gemm(dev, stream, steps, warmup, T=4096, M=4096, N=4096):
             "roofline": roofline("mfma", tf, PEAK_BF16_TFLOPS, "TFLOP/s")}
 
 
+def bench_qwen3_e2e(dev, prompt_len=1371, decode_steps=256, reps=3):
+    """Configuration 5: random-init Qwen3-0.6B (28 layers, hidden 1024, 16/8
+    heads, D=128, SwiGLU 3072, vocab 151936, tied embeddings; bf16 weights
+    N(0, 0.02) seeded, norms 1), prefill of `prompt_len` random token ids, then
+    `decode_steps` greedy steps replayed from one captured hipGraph.  TTFT =
+    prefill through the lm-head and the greedy pick of the first token; both
+    timed with HIP events on the model's stream (best of `reps`)."""
+    import torch
+
+    from toyinfer_amd import qwen3
+
+    cfg = dict(num_layers=28, hidden_size=1024, num_q_heads=16, num_kv_heads=8, head_dim=128,
+               intermediate_size=3072, vocab_size=151936,
+               max_seq_len=prompt_len + decode_steps + 8, max_prefill_tokens=prompt_len,
+               rms_norm_eps=1e-6, rope_theta=1e6)
+    g = torch.Generator(device=dev).manual_seed(SEED + 50)
+
+    def rnd(shape):
+        return (torch.randn(shape, generator=g, device=dev) * 0.02).to(torch.bfloat16)
+
+    shapes = qwen3.layer_shapes(qwen3.Config(**cfg))
+    w = {"layers": [{n: (torch.ones(shp, dtype=torch.bfloat16, device=dev) if len(shp) == 1
+                         else rnd(shp)) for n, shp in shapes.items()}
+                    for _ in range(cfg["num_layers"])]}
+    w["embed_tokens"] = rnd((cfg["vocab_size"], cfg["hidden_size"]))
+    w["lm_head"] = w["embed_tokens"]
+    w["norm"] = torch.ones(cfg["hidden_size"], dtype=torch.bfloat16, device=dev)
+    ids = torch.randint(0, cfg["vocab_size"], (prompt_len,), generator=g, device=dev,
+                        dtype=torch.int32)
+    m = qwen3.Qwen3(qwen3.Config(**cfg), w)
+    torch.cuda.synchronize()
+    ms_stream = torch.cuda.ExternalStream(m.stream_ptr, device=dev)
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
+    ttft, dec = [], []
+    for _ in range(reps):
+        ev[0].record(ms_stream)
+        m.prefill(ids, prompt_len)
+        ev[1].record(ms_stream)
+        m.decode(decode_steps, True)
+        ev[2].record(ms_stream)
+        m.synchronize()
+        ttft.append(ev[0].elapsed_time(ev[1]))
+        dec.append(ev[1].elapsed_time(ev[2]))
+    direct = []
+    m.prefill(ids, prompt_len)
+    ev[0].record(ms_stream)
+    m.decode(32, False)
+    ev[1].record(ms_stream)
+    m.synchronize()
+    direct.append(ev[0].elapsed_time(ev[1]) / 32)
+    m.close()
+    ms_tok = min(dec) / decode_steps
+    return {"workload": f"qwen3_0.6b_e2e_prompt{prompt_len}_decode{decode_steps}",
+            "entry": "toyinfer_qwen3_prefill / toyinfer_qwen3_decode (hipGraph)",
+            "ttft_ms": round(min(ttft), 3), "decode_ms_per_token": round(ms_tok, 4),
+            "value": round(1e3 / ms_tok, 1), "unit": "decode tokens/s",
+            "direct_launch_ms_per_token": round(direct[0], 4),
+            "note": "random-init weights N(0, 0.02) bf16 (synthetic), tied embeddings; "
+                    "TTFT includes the lm-head and the device greedy pick"}
+
+
 def bench_copy(dev, stream, steps, warmup, mib=256):
     """Device-to-device copy of `mib` MiB: a kernel with known HBM traffic (mib
     read + mib written per launch), the scale for the FETCH_SIZE / WRITE_SIZE
@@ -400,6 +464,7 @@ def main():
                                                                 args.warmup),
                "proj_gemv": lambda: bench_proj_gemv(dev, stream, args.steps, args.warmup),
                "proj_gemm": lambda: bench_proj_gemm(dev, stream, args.steps, args.warmup),
+               "qwen3_e2e": lambda: bench_qwen3_e2e(dev),
                "copy_calibration": lambda: bench_copy(dev, stream, args.steps, args.warmup)}
         print(json.dumps(one[args.workload]()), flush=True)
         return
@@ -425,6 +490,7 @@ def main():
         comps.append(bench_decode_contract(dev, stream, max(50, args.steps * 2), 2))
         comps.append(bench_proj_gemv(dev, stream, max(50, args.steps), 10))
         comps.append(bench_proj_gemm(dev, stream, max(200, args.steps), 50))
+        comps.append(bench_qwen3_e2e(dev))
         line["components"] = comps
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(host_inputs, gpu_out, args.cpu_seconds)

@@ -4,16 +4,17 @@
  * hipGraph and replayed, reading the position and the current token on the
  * device.  This re-creates the part of the reference's Transformer that the
  * attention path sits in (src/transformer.cpp:320-681): the prefill layer
- * loop (:320-470), the decode body with its three-stream fork/join
- * (:483-628) and the graph capture/replay (:630-681).  Weights are the
+ * loop (:320-470), the decode body (:483-628, whose three-stream fork/join
+ * becomes fused launches here) and the graph capture/replay (:630-681).  Weights are the
  * caller's device buffers, laid out as the reference's loader produces them
  * (projections [out][in] row-major bf16, norms [dim] bf16, tied or separate
  * lm-head [vocab][hidden]).
  *
  * The model object owns its state (KV cache [layers][max_seq_len][Hkv*D],
  * activations, rotary table, token list) in one device allocation made at
- * create time, three streams (default priority) and the graph; no call
- * after create allocates. */
+ * create time, one stream (default priority) and the graph; no call after
+ * create allocates.  hidden_size, intermediate_size and Hq*D are multiples
+ * of 64 and at most 16384. */
 #ifndef TOYINFER_QWEN3_H_
 #define TOYINFER_QWEN3_H_
 
@@ -87,7 +88,7 @@ int toyinfer_qwen3_synchronize(toyinfer_qwen3* m);
 const float* toyinfer_qwen3_logits(const toyinfer_qwen3* m);
 const uint32_t* toyinfer_qwen3_tokens(const toyinfer_qwen3* m);
 const uint32_t* toyinfer_qwen3_position(const toyinfer_qwen3* m);
-/* The hipStream_t the model enqueues on (stream 0 of its three). */
+/* The hipStream_t the model enqueues on. */
 void* toyinfer_qwen3_stream(const toyinfer_qwen3* m);
 
 #ifdef __cplusplus

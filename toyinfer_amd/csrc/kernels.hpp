@@ -126,6 +126,35 @@ hipError_t launch_batch_proj_bf16(const uint16_t* W, const uint16_t* x, uint16_t
                                   uint32_t M, uint32_t N, hipStream_t stream);
 bool proj_uses_gemm(uint32_t T, uint32_t N, const void* W, const void* x);
 
+// ------------------------------------------------- fused decode projections
+// One token: y = W * f(x) with f = RMSNorm(x; norm_w, eps) when norm_w is set,
+// over up to three stacked weight segments (rows[s] x n each), and an
+// epilogue: kDgPlain y[s][m] = bf16(acc); kDgResidual y[s][m] =
+// bf16(y[s][m] + bf16(acc)); kDgSwiglu (one segment, w[0] gate, w[1] up)
+// y[0][m] = bf16(bf16(up) * silu(bf16(gate))); kDgF32 y_f32[m] = acc.
+// n % 8 == 0, n <= kDecodeGemvMaxN, 16-byte aligned x, norm_w and weights.
+enum DecodeGemvEpi : int { kDgPlain = 0, kDgResidual = 1, kDgSwiglu = 2, kDgF32 = 3 };
+constexpr uint32_t kDecodeGemvMaxN = 16384;
+struct DecodeGemvArgs {
+    const uint16_t* x = nullptr;
+    const uint16_t* norm_w = nullptr;
+    float eps = 0.0f;
+    uint32_t n = 0;
+    int nseg = 1;
+    const uint16_t* w[3] = {nullptr, nullptr, nullptr};
+    uint16_t* y[3] = {nullptr, nullptr, nullptr};
+    uint32_t rows[3] = {0, 0, 0};
+    float* y_f32 = nullptr;
+    int epi = kDgPlain;
+};
+hipError_t launch_decode_gemv(const DecodeGemvArgs& a, hipStream_t stream);
+// Argmax over many workgroups with a last-arriving finaliser (same result and
+// out/pos_d behaviour as launch_argmax); key and ticket (device, zero before
+// the first launch) are left zero after every launch.
+hipError_t launch_argmax_wide(const float* logits, uint32_t n, uint32_t* out, uint32_t* pos_d,
+                              uint32_t out_cap, uint64_t* key, uint32_t* ticket,
+                              hipStream_t stream);
+
 // ------------------------------------------------------------ model ops
 // rows x size RMSNorm (size even); sum_out[row] = sum of squares (nullable).
 hipError_t launch_rmsnorm_rows(const uint16_t* x, const uint16_t* w, uint16_t* y, float* sum_out,

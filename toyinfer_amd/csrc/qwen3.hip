@@ -5,14 +5,19 @@
 // Reference: src/transformer.cpp:320-470 (prefill), :483-628 (decode body,
 // three-stream fork/join), :630-681 (graph capture / replay).  Differences,
 // all keeping the reference's rounding points:
+//  * one stream: the q/k/v projections the reference forks over three streams
+//    are one grid over the three weight segments, and gate/up are one grid
+//    whose epilogue applies SwiGLU;
 //  * prefill: q_norm/k_norm + RoPE are fused into the attention call, which
 //    writes the normalised, rotated K straight into the layer's cache rows;
 //    the V projection writes straight into the cache rows (no D2D copies);
 //    the residual stream stays in `hidden` (no residual copy);
-//  * decode: the six pre-attention launches are one (decode_qkv_prologue),
-//    attention is the split-K kernel with the length read on the device, and
-//    the body ends with a device argmax that appends the next token and
-//    advances the position, so consecutive graph replays need no host work;
+//  * decode: the RMSNorms are applied while each fused projection stages its
+//    input, the residual adds are projection epilogues, the six
+//    pre-attention launches are one (decode_qkv_prologue), attention is the
+//    split-K kernel with the length read on the device, and the body ends
+//    with a device argmax that appends the next token and advances the
+//    position, so consecutive graph replays need no host work;
 //  * no memset nodes (the reference's rmsnorm clears its sum with one).
 #include <hip/hip_runtime.h>
 
@@ -36,6 +41,8 @@ struct toyinfer_qwen3 {
     uint32_t* tokens = nullptr;
     uint32_t* pos = nullptr;
     uint32_t* seq_len = nullptr;
+    uint64_t* am_key = nullptr;     // argmax key and ticket, zero between launches
+    uint32_t* am_ticket = nullptr;
     float* inv_freq = nullptr;
     float* rope = nullptr;
     float* logits = nullptr;
@@ -49,8 +56,7 @@ struct toyinfer_qwen3 {
     size_t attn_ws_bytes = 0;
     uint32_t splits = 0;
 
-    hipStream_t s[3] = {nullptr, nullptr, nullptr};
-    hipEvent_t ev[3] = {nullptr, nullptr, nullptr};
+    hipStream_t s[1] = {nullptr};
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
 };
@@ -80,7 +86,7 @@ size_t carve(const toyinfer_qwen3_config& c, uint32_t splits, toyinfer_qwen3* m)
     const size_t kv = (size_t)c.num_kv_heads * c.head_dim, qd = (size_t)c.num_q_heads * c.head_dim;
     const size_t P = c.max_prefill_tokens, H = c.hidden_size, F = c.intermediate_size;
     const size_t o_tokens = take(4ull * c.max_seq_len);
-    const size_t o_pos = take(4), o_len = take(4);
+    const size_t o_pos = take(4), o_len = take(4), o_key = take(8), o_ticket = take(4);
     const size_t o_inv = take(4ull * c.head_dim / 2);
     const size_t o_rope = take(4ull * c.max_seq_len * c.head_dim);
     const size_t o_logits = take(4ull * c.vocab_size);
@@ -98,6 +104,8 @@ size_t carve(const toyinfer_qwen3_config& c, uint32_t splits, toyinfer_qwen3* m)
         m->tokens = reinterpret_cast<uint32_t*>(b + o_tokens);
         m->pos = reinterpret_cast<uint32_t*>(b + o_pos);
         m->seq_len = reinterpret_cast<uint32_t*>(b + o_len);
+        m->am_key = reinterpret_cast<uint64_t*>(b + o_key);
+        m->am_ticket = reinterpret_cast<uint32_t*>(b + o_ticket);
         m->inv_freq = reinterpret_cast<float*>(b + o_inv);
         m->rope = reinterpret_cast<float*>(b + o_rope);
         m->logits = reinterpret_cast<float*>(b + o_logits);
@@ -125,67 +133,97 @@ int check_config(const toyinfer_qwen3_config* c) {
         c->hidden_size == 0 || c->hidden_size % 64 != 0 || c->intermediate_size == 0 ||
         c->intermediate_size % 64 != 0 || c->vocab_size == 0 || c->max_seq_len < 2 ||
         c->max_prefill_tokens == 0 || c->max_prefill_tokens >= c->max_seq_len ||
-        c->max_prefill_tokens > 65535u || c->hidden_size > (1u << 22) ||
-        c->intermediate_size > (1u << 22) || !(c->rms_norm_eps > 0.0f) ||
+        c->max_prefill_tokens > 65535u || c->hidden_size > kDecodeGemvMaxN ||
+        c->intermediate_size > kDecodeGemvMaxN ||
+        c->num_q_heads * c->head_dim > kDecodeGemvMaxN || !(c->rms_norm_eps > 0.0f) ||
         !(c->rope_theta > 0.0f))
         return TOYINFER_ERR_INVALID_ARGUMENT;
     return TOYINFER_OK;
 }
 
-hipStream_t S(const toyinfer_qwen3* m, int i) { return m->s[i]; }
-
 // One decode step for the token at tokens[*pos]; ends with tokens[*pos + 1]
-// and *pos += 1.  Only kernel launches and event record/wait: capturable.
+// and *pos += 1.  Seven launches per layer, one stream, kernel launches only
+// (capturable):
+//   RMSNorm + q/k/v projections (one grid over the three weight segments,
+//     where the reference forks them over three streams, :513-533);
+//   q/k norm + RoPE + cache write; split-K attention + combine;
+//   o projection + residual add; RMSNorm + gate/up + SwiGLU;
+//   down projection + residual add.
 int decode_body(toyinfer_qwen3* m) {
     const toyinfer_qwen3_config& c = m->cfg;
     const uint32_t H = c.hidden_size, F = c.intermediate_size, V = c.vocab_size;
     const uint32_t hq = c.num_q_heads, hkv = c.num_kv_heads, d = c.head_dim;
     const uint32_t qd = hq * d, kv = hkv * d, msl = c.max_seq_len;
     const float eps = c.rms_norm_eps;
-    void* s0 = S(m, 0);
-    void* s1 = S(m, 1);
-    void* s2 = S(m, 2);
-    TRYH(launch_decode_step_setup(static_cast<const uint16_t*>(m->embed), m->tokens, m->pos,
-                                  m->d_hidden, m->seq_len, H, V, msl, S(m, 0)));
+    hipStream_t st = m->s[0];
+    void* s0 = st;
+    auto u16 = [](const void* p) { return static_cast<const uint16_t*>(p); };
+    TRYH(launch_decode_step_setup(u16(m->embed), m->tokens, m->pos, m->d_hidden, m->seq_len, H, V,
+                                  msl, st));
     for (uint32_t l = 0; l < c.num_layers; ++l) {
         const toyinfer_qwen3_layer& L = m->layers[l];
         uint16_t* kc = m->k_cache + (size_t)l * msl * kv;
         uint16_t* vc = m->v_cache + (size_t)l * msl * kv;
-        TRY(toyinfer_rmsnorm_bf16(m->d_hidden, L.input_layernorm, m->d_xn, nullptr, eps, H, s0));
-        // q on stream 0, k and v on streams 1 and 2 (src/transformer.cpp:513-533).
-        TRYH(hipEventRecord(m->ev[0], S(m, 0)));
-        TRYH(hipStreamWaitEvent(S(m, 1), m->ev[0], 0));
-        TRYH(hipStreamWaitEvent(S(m, 2), m->ev[0], 0));
-        TRY(toyinfer_gemv_proj_bf16(L.q_proj, m->d_xn, m->d_q, qd, H, s0));
-        TRY(toyinfer_gemv_proj_bf16(L.k_proj, m->d_xn, m->d_k, kv, H, s1));
-        TRY(toyinfer_gemv_proj_bf16(L.v_proj, m->d_xn, m->d_v, kv, H, s2));
-        TRYH(hipEventRecord(m->ev[1], S(m, 1)));
-        TRYH(hipEventRecord(m->ev[2], S(m, 2)));
-        TRYH(hipStreamWaitEvent(S(m, 0), m->ev[1], 0));
-        TRYH(hipStreamWaitEvent(S(m, 0), m->ev[2], 0));
+        DecodeGemvArgs qkv;
+        qkv.x = m->d_hidden;
+        qkv.norm_w = u16(L.input_layernorm);
+        qkv.eps = eps;
+        qkv.n = H;
+        qkv.nseg = 3;
+        qkv.w[0] = u16(L.q_proj);
+        qkv.w[1] = u16(L.k_proj);
+        qkv.w[2] = u16(L.v_proj);
+        qkv.y[0] = m->d_q;
+        qkv.y[1] = m->d_k;
+        qkv.y[2] = m->d_v;
+        qkv.rows[0] = qd;
+        qkv.rows[1] = kv;
+        qkv.rows[2] = kv;
+        TRYH(launch_decode_gemv(qkv, st));
         TRY(toyinfer_decode_qkv_prologue_bf16(m->d_q, m->d_k, m->d_v, L.q_norm, L.k_norm,
                                               m->inv_freq, m->pos, msl, eps, m->d_q, kc, vc, hq,
                                               hkv, d, s0));
         TRY(toyinfer_decode_attention_bf16(m->d_q, kc, vc, m->d_o, 1, hq, hkv, d, m->seq_len, msl,
                                            0, m->splits, m->attn_ws, m->attn_ws_bytes, s0));
-        TRY(toyinfer_gemv_proj_bf16(L.o_proj, m->d_o, m->d_tmp, H, qd, s0));
-        TRY(toyinfer_residual_add_bf16(m->d_tmp, m->d_hidden, H, s0));
-        TRY(toyinfer_rmsnorm_bf16(m->d_hidden, L.post_attention_layernorm, m->d_xn, nullptr, eps,
-                                  H, s0));
-        // gate on stream 0, up on stream 1 (src/transformer.cpp:595-610).
-        TRYH(hipEventRecord(m->ev[0], S(m, 0)));
-        TRYH(hipStreamWaitEvent(S(m, 1), m->ev[0], 0));
-        TRY(toyinfer_gemv_proj_bf16(L.gate_proj, m->d_xn, m->d_gate, F, H, s0));
-        TRY(toyinfer_gemv_proj_bf16(L.up_proj, m->d_xn, m->d_up, F, H, s1));
-        TRYH(hipEventRecord(m->ev[1], S(m, 1)));
-        TRYH(hipStreamWaitEvent(S(m, 0), m->ev[1], 0));
-        TRY(toyinfer_swiglu_bf16x2(m->d_gate, m->d_up, m->d_inter, F, s0));
-        TRY(toyinfer_gemv_proj_bf16(L.down_proj, m->d_inter, m->d_tmp, H, F, s0));
-        TRY(toyinfer_residual_add_bf16(m->d_tmp, m->d_hidden, H, s0));
+        DecodeGemvArgs o;
+        o.x = m->d_o;
+        o.n = qd;
+        o.w[0] = u16(L.o_proj);
+        o.y[0] = m->d_hidden;
+        o.rows[0] = H;
+        o.epi = kDgResidual;
+        TRYH(launch_decode_gemv(o, st));
+        DecodeGemvArgs gu;
+        gu.x = m->d_hidden;
+        gu.norm_w = u16(L.post_attention_layernorm);
+        gu.eps = eps;
+        gu.n = H;
+        gu.w[0] = u16(L.gate_proj);
+        gu.w[1] = u16(L.up_proj);
+        gu.y[0] = m->d_inter;
+        gu.rows[0] = F;
+        gu.epi = kDgSwiglu;
+        TRYH(launch_decode_gemv(gu, st));
+        DecodeGemvArgs dn;
+        dn.x = m->d_inter;
+        dn.n = F;
+        dn.w[0] = u16(L.down_proj);
+        dn.y[0] = m->d_hidden;
+        dn.rows[0] = H;
+        dn.epi = kDgResidual;
+        TRYH(launch_decode_gemv(dn, st));
     }
-    TRY(toyinfer_rmsnorm_bf16(m->d_hidden, m->final_norm, m->d_xn, nullptr, eps, H, s0));
-    TRY(toyinfer_gemv_proj_bf162float(m->lm_head, m->d_xn, m->logits, V, H, s0));
-    TRYH(launch_argmax(m->logits, V, m->tokens, m->pos, msl, S(m, 0)));
+    DecodeGemvArgs head;
+    head.x = m->d_hidden;
+    head.norm_w = u16(m->final_norm);
+    head.eps = eps;
+    head.n = H;
+    head.w[0] = u16(m->lm_head);
+    head.rows[0] = V;
+    head.y_f32 = m->logits;
+    head.epi = kDgF32;
+    TRYH(launch_decode_gemv(head, st));
+    TRYH(launch_argmax_wide(m->logits, V, m->tokens, m->pos, msl, m->am_key, m->am_ticket, st));
     return TOYINFER_OK;
 }
 
@@ -193,10 +231,7 @@ void release(toyinfer_qwen3* m) {
     if (!m) return;
     if (m->exec) (void)hipGraphExecDestroy(m->exec);
     if (m->graph) (void)hipGraphDestroy(m->graph);
-    for (int i = 0; i < 3; ++i) {
-        if (m->ev[i]) (void)hipEventDestroy(m->ev[i]);
-        if (m->s[i]) (void)hipStreamDestroy(m->s[i]);
-    }
+    if (m->s[0]) (void)hipStreamDestroy(m->s[0]);
     if (m->mem) (void)hipFree(m->mem);
     delete m;
 }
@@ -238,10 +273,8 @@ int toyinfer_qwen3_create(const toyinfer_qwen3_config* cfg, const void* embed_to
     m->splits = toyinfer_decode_default_splits(1, cfg->num_q_heads, cfg->num_kv_heads,
                                                cfg->head_dim, cfg->max_seq_len);
     const size_t bytes = carve(*cfg, m->splits, nullptr);
-    bool ok = hipMalloc(&m->mem, bytes) == hipSuccess;
-    for (int i = 0; ok && i < 3; ++i)
-        ok = hipStreamCreateWithFlags(&m->s[i], hipStreamNonBlocking) == hipSuccess &&
-             hipEventCreateWithFlags(&m->ev[i], hipEventDisableTiming) == hipSuccess;
+    const bool ok = hipMalloc(&m->mem, bytes) == hipSuccess &&
+                    hipStreamCreateWithFlags(&m->s[0], hipStreamNonBlocking) == hipSuccess;
     if (!ok) {
         release(m);
         return TOYINFER_ERR_HIP;
@@ -251,7 +284,10 @@ int toyinfer_qwen3_create(const toyinfer_qwen3_config* cfg, const void* embed_to
     if (st == TOYINFER_OK)
         st = toyinfer_rope_cos_sin_f32(m->rope, m->inv_freq, cfg->max_seq_len, cfg->head_dim,
                                        m->s[0]);
-    if (st == TOYINFER_OK && launch_set_u32(m->pos, 0, m->s[0]) != hipSuccess) st = TOYINFER_ERR_HIP;
+    uint32_t* zeros[4] = {m->pos, m->am_ticket, reinterpret_cast<uint32_t*>(m->am_key),
+                          reinterpret_cast<uint32_t*>(m->am_key) + 1};
+    for (uint32_t* z : zeros)
+        if (st == TOYINFER_OK && launch_set_u32(z, 0, m->s[0]) != hipSuccess) st = TOYINFER_ERR_HIP;
     if (st == TOYINFER_OK && hipStreamSynchronize(m->s[0]) != hipSuccess) st = TOYINFER_ERR_HIP;
     if (st != TOYINFER_OK) {
         release(m);
@@ -263,8 +299,7 @@ int toyinfer_qwen3_create(const toyinfer_qwen3_config* cfg, const void* embed_to
 
 void toyinfer_qwen3_destroy(toyinfer_qwen3* m) {
     if (!m) return;
-    for (int i = 0; i < 3; ++i)
-        if (m->s[i]) (void)hipStreamSynchronize(m->s[i]);
+    if (m->s[0]) (void)hipStreamSynchronize(m->s[0]);
     release(m);
 }
 

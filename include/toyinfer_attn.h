@@ -216,6 +216,15 @@ int toyinfer_gemv_proj_bf162float(const void* W, const void* hidden_states, floa
  * src/prefill.cu:124-174). */
 int toyinfer_batch_gemv_proj_bf16(const void* W, const void* hidden_states, void* y,
                                   uint32_t num_tokens, uint32_t M, uint32_t N, void* stream);
+/* Extension: up to three projections of the same hidden_states in one MFMA
+ * GEMM launch (the stacked q/k/v or gate/up of a layer): y[s] [num_tokens]
+ * [rows[s]] = hidden_states * W[s]^T; with residual != 0, y[s] = bf16(y[s] +
+ * bf16(product)) (a projection followed by the residual add).  Needs
+ * num_tokens > 4, N % 64 == 0 and 16-byte aligned hidden_states and W[s];
+ * each element equals what toyinfer_batch_gemv_proj_bf16 gives for it. */
+int toyinfer_gemm_segments_bf16(const void* hidden_states, uint32_t num_tokens, uint32_t N,
+                                uint32_t num_segments, const void* const* W, void* const* y,
+                                const uint32_t* rows, int residual, void* stream);
 
 /* ---- The rest of a Qwen3 decoder layer (for the model harness) ----
  * bf16 tensors need 4-byte alignment (16 bytes and sizes % 8 == 0 take the

@@ -211,3 +211,41 @@ def test_batch_proj_graph_replay(dev):
         attn.batch_gemv_proj_bf16(wd, xd, ref, T, M, N)
         H.sync()
         assert torch.equal(y.view(torch.int16), ref.view(torch.int16)), f"replay {k}"
+
+
+@pytest.mark.parametrize("T,hid,rows", [(1371, 1024, (2048, 1024, 1024)), (4096, 1024, (2048, 1024, 1024)),
+                                      (300, 512, (3072, 3072)), (17, 256, (200, 64, 130))])
+def test_gemm_segments_equal_separate_projections(dev, T, hid, rows):
+    """Stacked segments in one launch (whichever tile size the stacked grid
+    picks) give each element bit for bit what the separate projection gives:
+    every tile size sums k in the same MFMA order."""
+    print(f"[step] gemm segments T={T} hid={hid} rows={rows}", flush=True)
+    g = torch.Generator(device=dev).manual_seed(37)
+    x = torch.randn((T, hid), generator=g, device=dev).to(torch.bfloat16)
+    ws = [(torch.randn((r, hid), generator=g, device=dev) * 0.05).to(torch.bfloat16) for r in rows]
+    ys = [torch.empty((T, r), dtype=torch.bfloat16, device=dev) for r in rows]
+    attn.gemm_segments_bf16(x, T, hid, ws, ys, rows)
+    for w, y, r in zip(ws, ys, rows):
+        ref = torch.empty_like(y)
+        attn.batch_gemv_proj_bf16(w, x, ref, T, r, hid)
+        torch.cuda.synchronize()
+        assert torch.equal(y.view(torch.int16), ref.view(torch.int16)), f"rows {r}"
+
+
+def test_gemm_residual_epilogue_equals_projection_then_add(dev):
+    """residual != 0: y = bf16(y + bf16(x W^T)), bit for bit the projection
+    followed by residual_add_bf16."""
+    T, H, M = 700, 2048, 1024
+    g = torch.Generator(device=dev).manual_seed(38)
+    x = torch.randn((T, H), generator=g, device=dev).to(torch.bfloat16)
+    w = (torch.randn((M, H), generator=g, device=dev) * 0.05).to(torch.bfloat16)
+    hid = torch.randn((T, M), generator=g, device=dev).to(torch.bfloat16)
+    fused = hid.clone()
+    attn.gemm_segments_bf16(x, T, H, [w], [fused], [M], residual=True)
+    proj = torch.empty((T, M), dtype=torch.bfloat16, device=dev)
+    attn.batch_gemv_proj_bf16(w, x, proj, T, M, H)
+    ref = hid.clone()
+    attn.batch_residual_add_bf16(proj, ref, T, M)
+    torch.cuda.synchronize()
+    assert torch.equal(fused.view(torch.int16), ref.view(torch.int16))
+

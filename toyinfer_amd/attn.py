@@ -57,6 +57,7 @@ SIGNATURES = {
     "toyinfer_gemv_proj_bf16": (_i32, [_vp, _vp, _vp, _u32, _u32, _vp]),
     "toyinfer_gemv_proj_bf162float": (_i32, [_vp, _vp, _vp, _u32, _u32, _vp]),
     "toyinfer_batch_gemv_proj_bf16": (_i32, [_vp, _vp, _vp, _u32, _u32, _u32, _vp]),
+    "toyinfer_gemm_segments_bf16": (_i32, [_vp, _u32, _u32, _u32, _vp, _vp, _vp, _i32, _vp]),
     "toyinfer_rmsnorm_bf16": (_i32, [_vp, _vp, _vp, _vp, _f32, _u32, _vp]),
     "toyinfer_batch_rmsnorm_bf16": (_i32, [_vp, _vp, _vp, _vp, _f32, _u32, _u32, _vp]),
     "toyinfer_residual_add_bf16": (_i32, [_vp, _vp, _u32, _vp]),
@@ -315,6 +316,18 @@ def batch_gemv_proj_bf16(W, hidden_states, y, num_tokens: int, M: int, N: int,
     _check("batch_gemv_proj_bf16",
            LIB.toyinfer_batch_gemv_proj_bf16(_ptr(W), _ptr(hidden_states), _ptr(y),
                                              num_tokens, M, N, _stream(stream)))
+
+
+def gemm_segments_bf16(hidden_states, num_tokens: int, N: int, Ws, ys, rows, residual=False,
+                       stream=None) -> None:
+    """Stacked projections of one input (extension): ys[s] = x * Ws[s]^T [+ ys[s]]."""
+    n = len(Ws)
+    w_arr = (ctypes.c_void_p * n)(*[_ptr(w) for w in Ws])
+    y_arr = (ctypes.c_void_p * n)(*[_ptr(y) for y in ys])
+    r_arr = (ctypes.c_uint32 * n)(*rows)
+    _check("gemm_segments_bf16",
+           LIB.toyinfer_gemm_segments_bf16(_ptr(hidden_states), num_tokens, N, n, w_arr, y_arr,
+                                           r_arr, int(bool(residual)), _stream(stream)))
 
 
 # ------------------------------------------------- rest of a decoder layer

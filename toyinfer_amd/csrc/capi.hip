@@ -478,6 +478,28 @@ int toyinfer_batch_gemv_proj_bf16(const void* W, const void* hidden_states, void
                                            as_stream(stream)));
 }
 
+int toyinfer_gemm_segments_bf16(const void* hidden_states, uint32_t num_tokens, uint32_t N,
+                                uint32_t num_segments, const void* const* W, void* const* y,
+                                const uint32_t* rows, int residual, void* stream) {
+    if (!W || !y || !rows || num_segments == 0 || num_segments > 3 || N > kProjMaxN)
+        return TOYINFER_ERR_INVALID_ARGUMENT;
+    GemmArgs g;
+    g.x = static_cast<const uint16_t*>(hidden_states);
+    g.T = num_tokens;
+    g.N = N;
+    g.nseg = (int)num_segments;
+    g.residual = residual != 0;
+    for (uint32_t s = 0; s < num_segments; ++s) {
+        const int st = proj_args(W[s], hidden_states, y[s], 2, num_tokens, rows[s], N);
+        if (st != TOYINFER_OK) return st;
+        if (!proj_uses_gemm(num_tokens, N, W[s], hidden_states)) return TOYINFER_ERR_UNSUPPORTED;
+        g.w[s] = static_cast<const uint16_t*>(W[s]);
+        g.y[s] = static_cast<uint16_t*>(y[s]);
+        g.rows[s] = rows[s];
+    }
+    return from_hip(launch_gemm(g, as_stream(stream)));
+}
+
 static bool bf16_ok(const void* p) { return p && aligned(p, 4); }
 
 int toyinfer_rmsnorm_bf16(const void* input, const void* weight, void* output, float* sum,

@@ -125,6 +125,20 @@ hipError_t launch_gemv_f32(const uint16_t* W, const uint16_t* x, float* y, uint3
 hipError_t launch_batch_proj_bf16(const uint16_t* W, const uint16_t* x, uint16_t* y, uint32_t T,
                                   uint32_t M, uint32_t N, hipStream_t stream);
 bool proj_uses_gemm(uint32_t T, uint32_t N, const void* W, const void* x);
+// MFMA GEMM over up to three weight segments sharing the input x [T][N]:
+// y[s][t][m] = sum_n w[s][m][n] x[t][n], y[s] being [T][rows[s]]; with
+// `residual`, y[s][t][m] = bf16(y[s][t][m] + bf16(sum)).  Requires T > 0,
+// N % 64 == 0 and 16-byte aligned x and weights (proj_uses_gemm).
+struct GemmArgs {
+    const uint16_t* x = nullptr;
+    uint32_t T = 0, N = 0;
+    int nseg = 1;
+    const uint16_t* w[3] = {nullptr, nullptr, nullptr};
+    uint16_t* y[3] = {nullptr, nullptr, nullptr};
+    uint32_t rows[3] = {0, 0, 0};
+    bool residual = false;
+};
+hipError_t launch_gemm(const GemmArgs& g, hipStream_t stream);
 
 // ------------------------------------------------- fused decode projections
 // One token: y = W * f(x) with f = RMSNorm(x; norm_w, eps) when norm_w is set,

@@ -173,6 +173,7 @@ struct GmCfg {
     static constexpr int A_DMA = BM / 8 / WAVES, B_DMA = BN / 8 / WAVES;  // per wave
     static_assert(A_DMA * 8 * WAVES == BM && B_DMA * 8 * WAVES == BN, "DMA split");
 };
+using GmMini = GmCfg<64, 64, 2, 2, 4>;     // 4 waves of 32 x 32
 using GmSmall = GmCfg<128, 128, 2, 2, 2>;  // 4 waves of 64 x 64, 2 workgroups per CU
 using GmLarge = GmCfg<256, 256, 2, 4, 1>;  // 8 waves of 128 x 64
 
@@ -212,21 +213,32 @@ __device__ __forceinline__ GmTile gm_tile(uint32_t b, uint32_t n_tt, uint32_t n_
 }
 
 template <typename C>
-__global__ __launch_bounds__(C::THREADS, C::MINB) void gemm_kernel(const uint16_t* __restrict__ W,
-                                                          const uint16_t* __restrict__ x,
-                                                          uint16_t* __restrict__ y, uint32_t T,
-                                                          uint32_t M, uint32_t N) {
+__global__ __launch_bounds__(C::THREADS, C::MINB) void gemm_kernel(GemmArgs g) {
     constexpr int IM = C::IM, JN = C::JN;
+    const uint32_t T = g.T, N = g.N;
+    const uint16_t* __restrict__ x = g.x;
     // One array per stage (A rows, then B rows), so that the compiler can
     // tell the stage being read from the one the DMA is filling.
     __shared__ __align__(1024) uint16_t s_0[C::A_ELEMS + C::B_ELEMS];
     __shared__ __align__(1024) uint16_t s_1[C::A_ELEMS + C::B_ELEMS];
-    const uint32_t n_tt = (T + C::BM - 1) / C::BM, n_tm = (M + C::BN - 1) / C::BN;
+    // Output tiles run over the segments' rows stacked, each segment
+    // starting on a tile boundary.
+    uint32_t n_tm = 0;
+    for (int sg = 0; sg < g.nseg; ++sg) n_tm += (g.rows[sg] + C::BN - 1) / C::BN;
+    const uint32_t n_tt = (T + C::BM - 1) / C::BM;
     const GmTile tile = gm_tile(blockIdx.x, n_tt, n_tm);
-    const uint32_t t0 = tile.tt * C::BM, m0 = tile.tm * C::BN;
+    uint32_t tm = tile.tm;
+    int seg = 0;
+    while (seg + 1 < g.nseg && tm >= (g.rows[seg] + C::BN - 1) / C::BN) {
+        tm -= (g.rows[seg] + C::BN - 1) / C::BN;
+        ++seg;
+    }
+    const uint32_t M = g.rows[seg];
+    uint16_t* __restrict__ y = g.y[seg];
+    const uint32_t t0 = tile.tt * C::BM, m0 = tm * C::BN;
     const uint32_t row_bytes = 2 * N;
     const auto ra = make_rsrc(x + (size_t)t0 * N, min((uint32_t)C::BM, T - t0) * row_bytes);
-    const auto rb = make_rsrc(W + (size_t)m0 * N, min((uint32_t)C::BN, M - m0) * row_bytes);
+    const auto rb = make_rsrc(g.w[seg] + (size_t)m0 * N, min((uint32_t)C::BN, M - m0) * row_bytes);
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int wr = wave / C::WGN, wc = wave % C::WGN;
 
@@ -307,16 +319,27 @@ __global__ __launch_bounds__(C::THREADS, C::MINB) void gemm_kernel(const uint16_
 #pragma unroll
             for (int v = 0; v < 16; ++v) {
                 const uint32_t t = t0 + 32 * (IM * wr + i) + 8 * (v / 4) + 4 * (lane >> 5) + (v % 4);
-                if (t < T && m < M) y[(size_t)t * M + m] = f32_to_bf16(acc[i][j][v]);
+                if (t < T && m < M) {
+                    uint16_t* p = y + (size_t)t * M + m;
+                    if (g.residual)
+                        *p = f32_to_bf16(bf16_to_f32(*p) + bf16_to_f32(f32_to_bf16(acc[i][j][v])));
+                    else
+                        *p = f32_to_bf16(acc[i][j][v]);
+                }
             }
         }
 }
 
 template <typename C>
-hipError_t gemm_launch(const uint16_t* W, const uint16_t* x, uint16_t* y, uint32_t T, uint32_t M,
-                       uint32_t N, hipStream_t stream) {
-    const uint32_t tiles = ((T + C::BM - 1) / C::BM) * ((M + C::BN - 1) / C::BN);
-    gemm_kernel<C><<<tiles, C::THREADS, 0, stream>>>(W, x, y, T, M, N);
+uint32_t gemm_tiles(const GemmArgs& g) {
+    uint32_t n_tm = 0;
+    for (int sg = 0; sg < g.nseg; ++sg) n_tm += (g.rows[sg] + C::BN - 1) / C::BN;
+    return ((g.T + C::BM - 1) / C::BM) * n_tm;
+}
+
+template <typename C>
+hipError_t gemm_launch(const GemmArgs& g, hipStream_t stream) {
+    gemm_kernel<C><<<gemm_tiles<C>(g), C::THREADS, 0, stream>>>(g);
     return hipGetLastError();
 }
 
@@ -351,10 +374,22 @@ hipError_t launch_batch_proj_bf16(const uint16_t* W, const uint16_t* x, uint16_t
                                   uint32_t M, uint32_t N, hipStream_t stream) {
     if (T == 1) return gemv_any<1>(W, x, y, T, M, N, stream);
     if (!proj_uses_gemm(T, N, W, x)) return gemv_any<4>(W, x, y, T, M, N, stream);
-    // 256 x 256 tiles when they alone fill every CU once, else 128 x 128.
-    const uint32_t large = ((T + 255) / 256) * ((M + 255) / 256);
-    if (large >= (uint32_t)gemm_cus()) return gemm_launch<GmLarge>(W, x, y, T, M, N, stream);
-    return gemm_launch<GmSmall>(W, x, y, T, M, N, stream);
+    GemmArgs g;
+    g.x = x;
+    g.T = T;
+    g.N = N;
+    g.w[0] = W;
+    g.y[0] = y;
+    g.rows[0] = M;
+    return launch_gemm(g, stream);
+}
+
+hipError_t launch_gemm(const GemmArgs& g, hipStream_t stream) {
+    // The largest tile whose tiles alone fill every CU once; 64 x 64 below that.
+    const uint32_t cus = (uint32_t)gemm_cus();
+    if (gemm_tiles<GmLarge>(g) >= cus) return gemm_launch<GmLarge>(g, stream);
+    if (gemm_tiles<GmSmall>(g) >= cus) return gemm_launch<GmSmall>(g, stream);
+    return gemm_launch<GmMini>(g, stream);
 }
 
 }  // namespace tiattn

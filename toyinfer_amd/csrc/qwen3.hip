@@ -315,33 +315,106 @@ int toyinfer_qwen3_prefill(toyinfer_qwen3* m, const uint32_t* token_ids_d, uint3
     void* s0 = m->s[0];
     TRYH(hipMemcpyAsync(m->tokens, token_ids_d, 4ull * T, hipMemcpyDeviceToDevice, m->s[0]));
     TRY(toyinfer_gather_embedding_bf16(m->embed, m->tokens, m->p_hidden, T, H, V, s0));
+    hipStream_t st = m->s[0];
+    auto u16 = [](const void* p) { return static_cast<const uint16_t*>(p); };
+    // Projections of more than a few tokens run as stacked-segment GEMMs
+    // (q/k/v in one launch, gate/up in one) with the residual adds in the
+    // o and down epilogues; short prompts take the separate GEMV calls.
+    const bool gemm = proj_uses_gemm(T, H, m->layers[0].q_proj, m->p_xn) &&
+                      proj_uses_gemm(T, qd, m->layers[0].o_proj, m->p_o) &&
+                      proj_uses_gemm(T, F, m->layers[0].down_proj, m->p_inter);
     for (uint32_t l = 0; l < c.num_layers; ++l) {
         const toyinfer_qwen3_layer& L = m->layers[l];
         uint16_t* kc = m->k_cache + (size_t)l * msl * kv;
         uint16_t* vc = m->v_cache + (size_t)l * msl * kv;
         TRY(toyinfer_batch_rmsnorm_bf16(m->p_hidden, L.input_layernorm, m->p_xn, nullptr, eps, T,
                                         H, s0));
-        TRY(toyinfer_batch_gemv_proj_bf16(L.q_proj, m->p_xn, m->p_q, T, qd, H, s0));
-        TRY(toyinfer_batch_gemv_proj_bf16(L.k_proj, m->p_xn, m->p_k, T, kv, H, s0));
-        TRY(toyinfer_batch_gemv_proj_bf16(L.v_proj, m->p_xn, vc, T, kv, H, s0));
+        if (gemm) {
+            GemmArgs g;
+            g.x = m->p_xn;
+            g.T = T;
+            g.N = H;
+            g.nseg = 3;
+            g.w[0] = u16(L.q_proj);
+            g.w[1] = u16(L.k_proj);
+            g.w[2] = u16(L.v_proj);
+            g.y[0] = m->p_q;
+            g.y[1] = m->p_k;
+            g.y[2] = vc;
+            g.rows[0] = qd;
+            g.rows[1] = kv;
+            g.rows[2] = kv;
+            TRYH(launch_gemm(g, st));
+        } else {
+            TRY(toyinfer_batch_gemv_proj_bf16(L.q_proj, m->p_xn, m->p_q, T, qd, H, s0));
+            TRY(toyinfer_batch_gemv_proj_bf16(L.k_proj, m->p_xn, m->p_k, T, kv, H, s0));
+            TRY(toyinfer_batch_gemv_proj_bf16(L.v_proj, m->p_xn, vc, T, kv, H, s0));
+        }
         TRY(toyinfer_prefill_qknorm_rope_attention_bf16(m->p_q, m->p_k, vc, m->p_o, kc, L.q_norm,
                                                         L.k_norm, m->rope, eps, hq, hkv, d, T,
                                                         s0));
-        TRY(toyinfer_batch_gemv_proj_bf16(L.o_proj, m->p_o, m->p_tmp, T, H, qd, s0));
-        TRY(toyinfer_batch_residual_add_bf16(m->p_tmp, m->p_hidden, T, H, s0));
+        if (gemm) {
+            GemmArgs g;
+            g.x = m->p_o;
+            g.T = T;
+            g.N = qd;
+            g.w[0] = u16(L.o_proj);
+            g.y[0] = m->p_hidden;
+            g.rows[0] = H;
+            g.residual = true;
+            TRYH(launch_gemm(g, st));
+        } else {
+            TRY(toyinfer_batch_gemv_proj_bf16(L.o_proj, m->p_o, m->p_tmp, T, H, qd, s0));
+            TRY(toyinfer_batch_residual_add_bf16(m->p_tmp, m->p_hidden, T, H, s0));
+        }
         TRY(toyinfer_batch_rmsnorm_bf16(m->p_hidden, L.post_attention_layernorm, m->p_xn, nullptr,
                                         eps, T, H, s0));
-        TRY(toyinfer_batch_gemv_proj_bf16(L.gate_proj, m->p_xn, m->p_gate, T, F, H, s0));
-        TRY(toyinfer_batch_gemv_proj_bf16(L.up_proj, m->p_xn, m->p_up, T, F, H, s0));
+        if (gemm) {
+            GemmArgs g;
+            g.x = m->p_xn;
+            g.T = T;
+            g.N = H;
+            g.nseg = 2;
+            g.w[0] = u16(L.gate_proj);
+            g.w[1] = u16(L.up_proj);
+            g.y[0] = m->p_gate;
+            g.y[1] = m->p_up;
+            g.rows[0] = F;
+            g.rows[1] = F;
+            TRYH(launch_gemm(g, st));
+        } else {
+            TRY(toyinfer_batch_gemv_proj_bf16(L.gate_proj, m->p_xn, m->p_gate, T, F, H, s0));
+            TRY(toyinfer_batch_gemv_proj_bf16(L.up_proj, m->p_xn, m->p_up, T, F, H, s0));
+        }
         TRY(toyinfer_batch_swiglu_bf16x2(m->p_gate, m->p_up, m->p_inter, T, F, s0));
-        TRY(toyinfer_batch_gemv_proj_bf16(L.down_proj, m->p_inter, m->p_tmp, T, H, F, s0));
-        TRY(toyinfer_batch_residual_add_bf16(m->p_tmp, m->p_hidden, T, H, s0));
+        if (gemm) {
+            GemmArgs g;
+            g.x = m->p_inter;
+            g.T = T;
+            g.N = F;
+            g.w[0] = u16(L.down_proj);
+            g.y[0] = m->p_hidden;
+            g.rows[0] = H;
+            g.residual = true;
+            TRYH(launch_gemm(g, st));
+        } else {
+            TRY(toyinfer_batch_gemv_proj_bf16(L.down_proj, m->p_inter, m->p_tmp, T, H, F, s0));
+            TRY(toyinfer_batch_residual_add_bf16(m->p_tmp, m->p_hidden, T, H, s0));
+        }
     }
-    TRY(toyinfer_rmsnorm_bf16(m->p_hidden + (size_t)(T - 1) * H, m->final_norm, m->d_xn, nullptr,
-                              eps, H, s0));
-    TRY(toyinfer_gemv_proj_bf162float(m->lm_head, m->d_xn, m->logits, V, H, s0));
-    TRYH(launch_set_u32(m->pos, T - 1, m->s[0]));
-    TRYH(launch_argmax(m->logits, V, m->tokens, m->pos, msl, m->s[0]));
+    // Final norm of the last token fused into the lm-head, then the greedy pick.
+    DecodeGemvArgs head;
+    head.x = m->p_hidden + (size_t)(T - 1) * H;
+    head.norm_w = u16(m->final_norm);
+    head.eps = eps;
+    head.n = H;
+    head.w[0] = u16(m->lm_head);
+    head.rows[0] = V;
+    head.y_f32 = m->logits;
+    head.epi = kDgF32;
+    TRYH(launch_decode_gemv(head, st));
+    TRYH(launch_set_u32(m->pos, T - 1, st));
+    TRYH(launch_argmax_wide(m->logits, V, m->tokens, m->pos, msl, m->am_key, m->am_ticket, st));
     return TOYINFER_OK;
 }
 

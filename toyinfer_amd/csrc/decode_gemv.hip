@@ -4,7 +4,6 @@
 //   o projection -> residual add        (epilogue)
 //   RMSNorm -> gate/up -> SwiGLU        (one launch, paired rows)
 //   down projection -> residual add     (epilogue)
-//   final RMSNorm -> lm-head (fp32)
 // Rounding points are the unfused sequence's: the normalised input is
 // rounded to bf16 before the products, every projection output is rounded to
 // bf16 before the residual add or SwiGLU, which round again.
@@ -47,7 +46,7 @@ __device__ __forceinline__ float bf16_round(float v) { return bf16_to_f32(f32_to
 template <int RB, bool NORM, int EPI>
 __global__ __launch_bounds__(kDgThreads) void decode_gemv_kernel(DecodeGemvArgs a) {
     constexpr int NR = EPI == kDgSwiglu ? 2 * RB : RB;
-    __shared__ __align__(16) uint16_t s_x[kDecodeGemvMaxN];
+    extern __shared__ __align__(16) uint16_t s_x[];  // n values (dynamic: 2 n bytes)
     __shared__ float s_red[kDgThreads / 64];
     __shared__ float s_acc[kDgThreads / 64][NR];
     const uint32_t N = a.n, nchunk = N / 8;
@@ -62,6 +61,24 @@ __global__ __launch_bounds__(kDgThreads) void decode_gemv_kernel(DecodeGemvArgs 
     }
     const uint32_t nrows = min((uint32_t)RB, a.rows[seg] - r0);
     const uint32_t row_bytes = 2 * N;
+
+    // The weight rows do not depend on the input: the first trip's chunks
+    // are requested before the input is staged (and normalised).
+    __amdgpu_buffer_rsrc_t rw[EPI == kDgSwiglu ? 2 : 1];
+    rw[0] = make_rsrc(a.w[seg] + (size_t)r0 * N, nrows * row_bytes);
+    if constexpr (EPI == kDgSwiglu) rw[1] = make_rsrc(a.w[1] + (size_t)r0 * N, nrows * row_bytes);
+    uint4 wv[2][NR];
+    auto load_trip = [&](uint32_t off0, uint32_t off1) __attribute__((always_inline)) {
+#pragma unroll
+        for (int r = 0; r < NR; ++r) {
+            wv[0][r] = buf_load16(rw[r / RB], (r % RB) * row_bytes + off0);
+            wv[1][r] = buf_load16(rw[r / RB], (r % RB) * row_bytes + off1);
+        }
+    };
+    {
+        const uint32_t c = threadIdx.x, c2 = c + kDgThreads;
+        load_trip(c < nchunk ? c * 16 : kDgOob, c2 < nchunk ? c2 * 16 : kDgOob);
+    }
 
     // Stage the input (normalised if asked) in LDS.
     if constexpr (NORM) {
@@ -93,26 +110,18 @@ __global__ __launch_bounds__(kDgThreads) void decode_gemv_kernel(DecodeGemvArgs 
     }
     __syncthreads();
 
-    __amdgpu_buffer_rsrc_t rw[EPI == kDgSwiglu ? 2 : 1];
-    rw[0] = make_rsrc(a.w[seg] + (size_t)r0 * N, nrows * row_bytes);
-    if constexpr (EPI == kDgSwiglu) rw[1] = make_rsrc(a.w[1] + (size_t)r0 * N, nrows * row_bytes);
-
     float acc[NR];
 #pragma unroll
     for (int r = 0; r < NR; ++r) acc[r] = 0.0f;
     for (uint32_t c = threadIdx.x; c < nchunk; c += 2 * kDgThreads) {
         const uint32_t c2 = c + kDgThreads;
-        const uint32_t off[2] = {c * 16, c2 < nchunk ? c2 * 16 : kDgOob};
-        uint4 wv[2][NR];
-#pragma unroll
-        for (int u = 0; u < 2; ++u)
-#pragma unroll
-            for (int r = 0; r < NR; ++r)
-                wv[u][r] = buf_load16(rw[r / RB], (r % RB) * row_bytes + off[u]);
         const uint4 x0 = *reinterpret_cast<const uint4*>(s_x + 8 * c);
         const uint4 x1 = c2 < nchunk ? *reinterpret_cast<const uint4*>(s_x + 8 * c2) : uint4{0, 0, 0, 0};
 #pragma unroll
         for (int r = 0; r < NR; ++r) acc[r] = dot8(wv[1][r], x1, dot8(wv[0][r], x0, acc[r]));
+        // The next trip's rows.
+        const uint32_t n0 = c + 2 * kDgThreads, n1 = n0 + kDgThreads;
+        if (n0 < nchunk) load_trip(n0 * 16, n1 < nchunk ? n1 * 16 : kDgOob);
     }
 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -132,21 +141,19 @@ __global__ __launch_bounds__(kDgThreads) void decode_gemv_kernel(DecodeGemvArgs 
             a.y[seg][m] = f32_to_bf16(v);
         } else if constexpr (EPI == kDgResidual) {
             a.y[seg][m] = f32_to_bf16(bf16_to_f32(a.y[seg][m]) + bf16_round(v));
-        } else if constexpr (EPI == kDgSwiglu) {
+        } else {
             float u = 0.0f;
 #pragma unroll
             for (int w = 0; w < kDgThreads / 64; ++w) u += s_acc[w][RB + r];
             const float g = bf16_round(v), up = bf16_round(u);
             a.y[0][m] = f32_to_bf16(up * (g * (1.0f / (1.0f + expf(-g)))));
-        } else {
-            a.y_f32[m] = v;
         }
     }
 }
 
 template <int RB, bool NORM, int EPI>
 hipError_t dg_launch(const DecodeGemvArgs& a, uint32_t total_groups, hipStream_t stream) {
-    decode_gemv_kernel<RB, NORM, EPI><<<total_groups, kDgThreads, 0, stream>>>(a);
+    decode_gemv_kernel<RB, NORM, EPI><<<total_groups, kDgThreads, 2 * a.n, stream>>>(a);
     return hipGetLastError();
 }
 
@@ -231,8 +238,7 @@ hipError_t launch_decode_gemv(const DecodeGemvArgs& a, hipStream_t stream) {
         case kDgPlain: return norm ? dg_rows<true, kDgPlain>(a, stream) : dg_rows<false, kDgPlain>(a, stream);
         case kDgResidual:
             return norm ? dg_rows<true, kDgResidual>(a, stream) : dg_rows<false, kDgResidual>(a, stream);
-        case kDgSwiglu: return norm ? dg_rows<true, kDgSwiglu>(a, stream) : dg_rows<false, kDgSwiglu>(a, stream);
-        default: return norm ? dg_rows<true, kDgF32>(a, stream) : dg_rows<false, kDgF32>(a, stream);
+        default: return norm ? dg_rows<true, kDgSwiglu>(a, stream) : dg_rows<false, kDgSwiglu>(a, stream);
     }
 }
 

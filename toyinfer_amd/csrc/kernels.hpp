@@ -145,9 +145,9 @@ hipError_t launch_gemm(const GemmArgs& g, hipStream_t stream);
 // over up to three stacked weight segments (rows[s] x n each), and an
 // epilogue: kDgPlain y[s][m] = bf16(acc); kDgResidual y[s][m] =
 // bf16(y[s][m] + bf16(acc)); kDgSwiglu (one segment, w[0] gate, w[1] up)
-// y[0][m] = bf16(bf16(up) * silu(bf16(gate))); kDgF32 y_f32[m] = acc.
+// y[0][m] = bf16(bf16(up) * silu(bf16(gate))).
 // n % 8 == 0, n <= kDecodeGemvMaxN, 16-byte aligned x, norm_w and weights.
-enum DecodeGemvEpi : int { kDgPlain = 0, kDgResidual = 1, kDgSwiglu = 2, kDgF32 = 3 };
+enum DecodeGemvEpi : int { kDgPlain = 0, kDgResidual = 1, kDgSwiglu = 2 };
 constexpr uint32_t kDecodeGemvMaxN = 16384;
 struct DecodeGemvArgs {
     const uint16_t* x = nullptr;
@@ -158,7 +158,6 @@ struct DecodeGemvArgs {
     const uint16_t* w[3] = {nullptr, nullptr, nullptr};
     uint16_t* y[3] = {nullptr, nullptr, nullptr};
     uint32_t rows[3] = {0, 0, 0};
-    float* y_f32 = nullptr;
     int epi = kDgPlain;
 };
 hipError_t launch_decode_gemv(const DecodeGemvArgs& a, hipStream_t stream);

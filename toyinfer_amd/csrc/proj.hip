@@ -316,15 +316,23 @@ __global__ __launch_bounds__(C::THREADS, C::MINB) void gemm_kernel(GemmArgs g) {
 #pragma unroll
         for (int j = 0; j < JN; ++j) {
             const uint32_t m = m0 + 32 * (JN * wc + j) + (lane & 31);
+            // With a residual, all 16 old values of the block are loaded
+            // before any store, so their latencies overlap.
+            uint16_t old[16];
+            if (g.residual) {
+#pragma unroll
+                for (int v = 0; v < 16; ++v) {
+                    const uint32_t t = t0 + 32 * (IM * wr + i) + 8 * (v / 4) + 4 * (lane >> 5) + (v % 4);
+                    old[v] = (t < T && m < M) ? y[(size_t)t * M + m] : (uint16_t)0;
+                }
+            }
 #pragma unroll
             for (int v = 0; v < 16; ++v) {
                 const uint32_t t = t0 + 32 * (IM * wr + i) + 8 * (v / 4) + 4 * (lane >> 5) + (v % 4);
                 if (t < T && m < M) {
-                    uint16_t* p = y + (size_t)t * M + m;
-                    if (g.residual)
-                        *p = f32_to_bf16(bf16_to_f32(*p) + bf16_to_f32(f32_to_bf16(acc[i][j][v])));
-                    else
-                        *p = f32_to_bf16(acc[i][j][v]);
+                    const float r = g.residual ? bf16_to_f32(old[v]) + bf16_to_f32(f32_to_bf16(acc[i][j][v]))
+                                               : acc[i][j][v];
+                    y[(size_t)t * M + m] = f32_to_bf16(r);
                 }
             }
         }

@@ -148,7 +148,8 @@ int check_config(const toyinfer_qwen3_config* c) {
 //     where the reference forks them over three streams, :513-533);
 //   q/k norm + RoPE + cache write; split-K attention + combine;
 //   o projection + residual add; RMSNorm + gate/up + SwiGLU;
-//   down projection + residual add.
+//   down projection + residual add;
+// then the final norm, the lm-head and the argmax.
 int decode_body(toyinfer_qwen3* m) {
     const toyinfer_qwen3_config& c = m->cfg;
     const uint32_t H = c.hidden_size, F = c.intermediate_size, V = c.vocab_size;
@@ -213,16 +214,10 @@ int decode_body(toyinfer_qwen3* m) {
         dn.epi = kDgResidual;
         TRYH(launch_decode_gemv(dn, st));
     }
-    DecodeGemvArgs head;
-    head.x = m->d_hidden;
-    head.norm_w = u16(m->final_norm);
-    head.eps = eps;
-    head.n = H;
-    head.w[0] = u16(m->lm_head);
-    head.rows[0] = V;
-    head.y_f32 = m->logits;
-    head.epi = kDgF32;
-    TRYH(launch_decode_gemv(head, st));
+    // The lm-head streams the largest matrix: the plain GEMV (more waves in
+    // flight) after a separate norm beats the fused form here.
+    TRY(toyinfer_rmsnorm_bf16(m->d_hidden, m->final_norm, m->d_xn, nullptr, eps, H, s0));
+    TRY(toyinfer_gemv_proj_bf162float(m->lm_head, m->d_xn, m->logits, V, H, s0));
     TRYH(launch_argmax_wide(m->logits, V, m->tokens, m->pos, msl, m->am_key, m->am_ticket, st));
     return TOYINFER_OK;
 }
@@ -402,17 +397,10 @@ int toyinfer_qwen3_prefill(toyinfer_qwen3* m, const uint32_t* token_ids_d, uint3
             TRY(toyinfer_batch_residual_add_bf16(m->p_tmp, m->p_hidden, T, H, s0));
         }
     }
-    // Final norm of the last token fused into the lm-head, then the greedy pick.
-    DecodeGemvArgs head;
-    head.x = m->p_hidden + (size_t)(T - 1) * H;
-    head.norm_w = u16(m->final_norm);
-    head.eps = eps;
-    head.n = H;
-    head.w[0] = u16(m->lm_head);
-    head.rows[0] = V;
-    head.y_f32 = m->logits;
-    head.epi = kDgF32;
-    TRYH(launch_decode_gemv(head, st));
+    // Final norm of the last token, the lm-head, then the greedy pick.
+    TRY(toyinfer_rmsnorm_bf16(m->p_hidden + (size_t)(T - 1) * H, m->final_norm, m->d_xn, nullptr,
+                              eps, H, s0));
+    TRY(toyinfer_gemv_proj_bf162float(m->lm_head, m->d_xn, m->logits, V, H, s0));
     TRYH(launch_set_u32(m->pos, T - 1, st));
     TRYH(launch_argmax_wide(m->logits, V, m->tokens, m->pos, msl, m->am_key, m->am_ticket, st));
     return TOYINFER_OK;

@@ -200,6 +200,75 @@ void gemv_proj_bf162float(const bf16* __restrict__ W, const bf16* __restrict__ h
                    "gemv_proj_bf162float");
 }
 
+// include/kernel_warpper.h:12-15 and :17-21: hidden_state += residual (bf16).
+template <const uint32_t NUM_THREADS>
+void residual_add_bf16(const bf16* __restrict__ residual, bf16* __restrict__ hidden_state,
+                       const uint32_t size, hipStream_t stream_d = nullptr) {
+    static_assert(NUM_THREADS > 0 && NUM_THREADS <= 1024, "illegal launch shape");
+    TOYINFER_CHECK(toyinfer_residual_add_bf16(residual, hidden_state, size, stream_d),
+                   "residual_add_bf16");
+}
+template <const uint32_t NUM_THREADS>
+void batch_residual_add_bf16(const bf16* __restrict__ residual, bf16* __restrict__ hidden_state,
+                             const uint32_t num_tokens, const uint32_t size,
+                             hipStream_t stream_d = nullptr) {
+    static_assert(NUM_THREADS > 0 && NUM_THREADS <= 1024, "illegal launch shape");
+    TOYINFER_CHECK(toyinfer_batch_residual_add_bf16(residual, hidden_state, num_tokens, size,
+                                                    stream_d),
+                   "batch_residual_add_bf16");
+}
+
+// include/kernel_warpper.h:25-29 and :31-36: full-row RMSNorm; *sum (per
+// row) receives the sum of squares, as in the reference.
+template <const uint32_t NUM_THREADS>
+void rmsnorm_bf16(const bf16* __restrict__ input, const bf16* __restrict__ weight, bf16* output,
+                  float* sum, const float rms_norm_eps, const uint32_t size,
+                  hipStream_t stream_d = nullptr) {
+    static_assert(NUM_THREADS > 0 && NUM_THREADS <= 1024, "illegal launch shape");
+    TOYINFER_CHECK(toyinfer_rmsnorm_bf16(input, weight, output, sum, rms_norm_eps, size, stream_d),
+                   "rmsnorm_bf16");
+}
+template <const uint32_t NUM_THREADS>
+void batch_rmsnorm_bf16(const bf16* __restrict__ input, const bf16* __restrict__ weight,
+                        bf16* output, float* sum, const float rms_norm_eps,
+                        const uint32_t num_tokens, const uint32_t size,
+                        hipStream_t stream_d = nullptr) {
+    static_assert(NUM_THREADS > 0 && NUM_THREADS <= 1024, "illegal launch shape");
+    TOYINFER_CHECK(toyinfer_batch_rmsnorm_bf16(input, weight, output, sum, rms_norm_eps,
+                                               num_tokens, size, stream_d),
+                   "batch_rmsnorm_bf16");
+}
+
+// include/kernel_warpper.h:71-77: rows of the table by device token ids
+// (ids are not range-checked, as in the reference).
+template <const uint32_t NUM_THREADS>
+void gather_embedding_bf16(const bf16* __restrict__ embedding_table,
+                           const uint32_t* __restrict__ token_ids,
+                           bf16* __restrict__ hidden_states, const uint32_t num_tokens,
+                           const uint32_t hidden_size, hipStream_t stream_d = nullptr) {
+    static_assert(NUM_THREADS > 0 && NUM_THREADS <= 1024, "illegal launch shape");
+    TOYINFER_CHECK(toyinfer_gather_embedding_bf16(embedding_table, token_ids, hidden_states,
+                                                  num_tokens, hidden_size, 0xffffffffu, stream_d),
+                   "gather_embedding_bf16");
+}
+
+// include/kernel_warpper.h:116-126: intermedia = bf16(up * silu(gate)).
+template <const uint32_t NUM_THREADS>
+void swiglu_bf16x2(const bf16* __restrict__ gate, const bf16* __restrict__ up,
+                   bf16* __restrict__ intermedia, const uint32_t size,
+                   hipStream_t stream_d = nullptr) {
+    static_assert(NUM_THREADS > 0 && NUM_THREADS <= 1024, "illegal launch shape");
+    TOYINFER_CHECK(toyinfer_swiglu_bf16x2(gate, up, intermedia, size, stream_d), "swiglu_bf16x2");
+}
+template <const uint32_t NUM_THREADS>
+void batch_swiglu_bf16x2(const bf16* __restrict__ gate, const bf16* __restrict__ up,
+                         bf16* __restrict__ intermedia, const uint32_t num_tokens,
+                         const uint32_t size, hipStream_t stream_d = nullptr) {
+    static_assert(NUM_THREADS > 0 && NUM_THREADS <= 1024, "illegal launch shape");
+    TOYINFER_CHECK(toyinfer_batch_swiglu_bf16x2(gate, up, intermedia, num_tokens, size, stream_d),
+                   "batch_swiglu_bf16x2");
+}
+
 // ------------------------------------------------------------- extensions
 // Entry points with no counterpart in the reference: batched split-K decode,
 // the prefill with QK-RMSNorm + RoPE fused in front, and the decode step's

@@ -475,6 +475,69 @@ void projection_cases() {
     hip_ok(hipStreamDestroy(stream), "stream destroy");
 }
 
+// The decoder-layer ops as src/transformer.cpp calls them around attention
+// (:500-628 decode, :355-470 prefill), against the oracle at the reference
+// tests' 2e-2 bar; the rmsnorm sum against the float sum of squares.
+void layer_op_cases() {
+    hipStream_t stream;
+    hip_ok(hipStreamCreate(&stream), "stream");
+    const uint32_t T = 3, H = 1024, F = 3072, V = 64;
+    std::vector<float> h((size_t)T * H), w(H), g((size_t)T * F), u((size_t)T * F), e((size_t)V * H);
+    for (size_t i = 0; i < h.size(); ++i) h[i] = std::sin(0.013f * (float)i) * 1.3f;
+    for (uint32_t i = 0; i < H; ++i) w[i] = 0.8f + 0.4f * (float)((i * 7) % 13) / 12.0f;
+    for (size_t i = 0; i < g.size(); ++i) {
+        g[i] = std::cos(0.007f * (float)i) * 2.5f;
+        u[i] = std::sin(0.011f * (float)i + 0.3f);
+    }
+    for (size_t i = 0; i < e.size(); ++i) e[i] = std::cos(0.003f * (float)i);
+    const auto hb = to_bits(h), wb = to_bits(w), gb = to_bits(g), ub = to_bits(u), eb = to_bits(e);
+    Dev<bf16> dh(hb.size()), dw(wb.size()), dy(hb.size()), dg(gb.size()), du(ub.size()),
+        di(gb.size()), de(eb.size()), dx((size_t)T * H);
+    Dev<float> dsum(T);
+    put_bits(dh, hb);
+    put_bits(dw, wb);
+    put_bits(dg, gb);
+    put_bits(du, ub);
+    put_bits(de, eb);
+    toyinfer::batch_rmsnorm_bf16<256>(dh.p, dw.p, dy.p, dsum.p, 1e-6f, T, H, stream);
+    toyinfer::batch_swiglu_bf16x2<256>(dg.p, du.p, di.p, T, F, stream);
+    hip_ok(hipStreamSynchronize(stream), "sync");
+    std::vector<float> exp(hb.size());
+    or_multi_rmsnorm(from_bits(hb).data(), from_bits(wb).data(), exp.data(), T, H, 1e-6f);
+    check_close(from_bits(get_bits(dy)), exp, 2e-2f, 2e-2f, "batch_rmsnorm_bf16");
+    const auto sums = dsum.get();
+    const auto hf = from_bits(hb);
+    bool sum_ok = true;
+    for (uint32_t t = 0; t < T; ++t) {
+        double ss = 0;
+        for (uint32_t i = 0; i < H; ++i) ss += (double)hf[(size_t)t * H + i] * hf[(size_t)t * H + i];
+        sum_ok = sum_ok && std::fabs(sums[t] - ss) <= 5e-2 + 5e-3 * ss;
+    }
+    report(sum_ok, "batch_rmsnorm_bf16 sum", "");
+    std::vector<float> sw(gb.size());
+    const auto gf = from_bits(gb), uf = from_bits(ub);
+    for (size_t i = 0; i < sw.size(); ++i)
+        sw[i] = or_bf16_to_f32(or_f32_to_bf16(uf[i] * (gf[i] * (1.0f / (1.0f + std::exp(-gf[i]))))));
+    check_close(from_bits(get_bits(di)), sw, 2e-2f, 2e-2f, "batch_swiglu_bf16x2");
+    // residual add (in place) and the single-row forms
+    toyinfer::residual_add_bf16<256>(dy.p, dh.p, H, stream);
+    toyinfer::rmsnorm_bf16<256>(dh.p, dw.p, dx.p, dsum.p, 1e-6f, H, stream);
+    toyinfer::swiglu_bf16x2<256>(dg.p, du.p, di.p, F, stream);
+    Dev<uint32_t> ids(T);
+    ids.put({5, 63, 0});
+    toyinfer::gather_embedding_bf16<256>(de.p, ids.p, dy.p, T, H, stream);
+    hip_ok(hipStreamSynchronize(stream), "sync");
+    const auto yb = get_bits(dy);
+    bool gather_ok = true;
+    const uint32_t want[3] = {5, 63, 0};
+    for (uint32_t t = 0; t < T; ++t)
+        gather_ok = gather_ok && std::equal(eb.begin() + (size_t)want[t] * H,
+                                            eb.begin() + (size_t)(want[t] + 1) * H,
+                                            yb.begin() + (size_t)t * H);
+    report(gather_ok, "gather_embedding_bf16", "rows copied bit for bit");
+    hip_ok(hipStreamDestroy(stream), "stream destroy");
+}
+
 }  // namespace
 
 int main() {
@@ -488,6 +551,7 @@ int main() {
     prologue_cases();
     decode_step_cases();
     projection_cases();
+    layer_op_cases();
     std::printf("%s: %d failure(s)\n", g_failures ? "FAILED" : "ALL PASS", g_failures);
     return g_failures ? 1 : 0;
 }

@@ -50,9 +50,11 @@ SEED = 2026
 # 256 MiB device-to-device copy (reads x2.0, writes x1.0); the summaries are
 # under profiles/.  (read KiB, write KiB) as the counters report them.
 PMC_KIB = {"prefill": (5533.6, 5484.0),            # prefill_splitkv_kernel<128,false>
-           "prefill_fused": (92307.0, 65537.2),    # prefill_kernel<128,true>
-           "decode_b8_l4096": (65854.7, 1633.5),   # decode_split_kernel<128>
-           "decode_b1_l32768": (65615.3, 1632.4)}  # decode_split_kernel<128>
+           "prefill_fused": (92244.4, 65536.5),    # prefill_kernel<128,true>
+           "decode_b8_l4096": (65860.5, 1633.2),   # decode_split_kernel<128>
+           "decode_b1_l32768": (65617.8, 1632.3),  # decode_split_kernel<128>
+           "proj_gemv": (607796.7, 593.5),         # gemv_kernel<8,8,1,float>
+           "proj_gemm": (98486.5, 32768.0)}        # gemm_kernel<GmCfg<256,256,2,4,1>>
 FETCH_SCALE, WRITE_SCALE = 2.0, 1.0
 
 
@@ -306,7 +308,7 @@ def bench_proj_gemv(dev, stream, steps, warmup, M=151936, N=4096):
     return {"workload": f"proj_gemv_lmhead_m{M}_n{N}", "entry": "toyinfer_gemv_proj_bf162float",
             "steps": steps, "ms_per_step": round(ms, 5), "value": round(gbs, 1), "unit": "GB/s",
             "note": "weights + x read, fp32 y written, per call / call time",
-            "roofline": roofline("hbm", gbs, PEAK_HBM_GBS, "GB/s")}
+            "roofline": roofline("hbm", gbs, PEAK_HBM_GBS, "GB/s", traffic_bytes("proj_gemv"))}
 
 
 def bench_proj_gemm(dev, stream, steps, warmup, T=4096, M=4096, N=4096):
@@ -328,7 +330,7 @@ def bench_proj_gemm(dev, stream, steps, warmup, T=4096, M=4096, N=4096):
     return {"workload": f"proj_gemm_t{T}_m{M}_n{N}", "entry": "toyinfer_batch_gemv_proj_bf16",
             "steps": steps, "ms_per_step": round(ms, 5), "value": round(tf, 1),
             "unit": "TFLOP/s", "torch_matmul_tflops": round(2.0 * T * M * N / (ms_lib * 1e-3) / 1e12, 1),
-            "roofline": roofline("mfma", tf, PEAK_BF16_TFLOPS, "TFLOP/s")}
+            "roofline": roofline("mfma", tf, PEAK_BF16_TFLOPS, "TFLOP/s", traffic_bytes("proj_gemm"))}
 
 
 def bench_qwen3_e2e(dev, prompt_len=1371, decode_steps=256, reps=3):

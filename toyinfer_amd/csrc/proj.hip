@@ -159,37 +159,44 @@ hipError_t gemv_any(const uint16_t* W, const uint16_t* x, OutT* y, uint32_t T, u
 
 // ------------------------------------------------------------------ GEMM
 
-constexpr int kGmBK = 64;
+constexpr int kGmBK = 64;    // K granularity every GEMM configuration handles
 constexpr int kGmGroup = 8;  // tile groups of 8 x 8
 
 // Block tile BM (tokens) x BN (outputs) on a WGM x WGN grid of waves; each
-// wave owns IM x JN blocks of 32 x 32.
-template <int BM_, int BN_, int WGM_, int WGN_, int MINB_>
+// wave owns IM x JN blocks of 32 x 32.  K advances in slices of BK (64 or
+// 128): KS k-steps of 16 per slice.
+template <int BM_, int BN_, int WGM_, int WGN_, int MINB_, int BK_ = 64>
 struct GmCfg {
-    static constexpr int BM = BM_, BN = BN_, WGM = WGM_, WGN = WGN_, MINB = MINB_;
+    static constexpr int BM = BM_, BN = BN_, WGM = WGM_, WGN = WGN_, MINB = MINB_, BK = BK_;
     static constexpr int WAVES = WGM * WGN, THREADS = 64 * WAVES;
     static constexpr int IM = BM / WGM / 32, JN = BN / WGN / 32;
-    static constexpr int A_ELEMS = BM * kGmBK, B_ELEMS = BN * kGmBK;
-    static constexpr int A_DMA = BM / 8 / WAVES, B_DMA = BN / 8 / WAVES;  // per wave
-    static_assert(A_DMA * 8 * WAVES == BM && B_DMA * 8 * WAVES == BN, "DMA split");
+    static constexpr int KS = BK / 16, CPR = BK / 8, RPB = 64 / CPR;  // chunks per row, rows per DMA
+    static constexpr int A_ELEMS = BM * BK, B_ELEMS = BN * BK;
+    static constexpr int A_DMA = BM / RPB / WAVES, B_DMA = BN / RPB / WAVES;  // per wave
+    static_assert(A_DMA * RPB * WAVES == BM && B_DMA * RPB * WAVES == BN, "DMA split");
+    static_assert(BK == 64 || BK == 128, "slice width");
 };
-using GmMini = GmCfg<64, 64, 2, 2, 4>;     // 4 waves of 32 x 32
+// 64 x 64 tiles serve grids too small to fill the CUs with larger tiles; with
+// few MFMAs per slice they are latency-bound, so they take 128-wide slices.
+using GmMini = GmCfg<64, 64, 2, 2, 4, 128>;  // 4 waves of 32 x 32
+using GmMini64 = GmCfg<64, 64, 2, 2, 4, 64>;
 using GmSmall = GmCfg<128, 128, 2, 2, 2>;  // 4 waves of 64 x 64, 2 workgroups per CU
 using GmLarge = GmCfg<256, 256, 2, 4, 1>;  // 8 waves of 128 x 64
 
-// LDS rows of 64 bf16 (128 bytes = 8 chunks); chunk c of row r sits at
+// LDS rows of BK bf16 (CPR 16-byte chunks); chunk c of row r sits at
 // c ^ (r & 7), which makes the MFMA operand reads (8 rows x 16 bytes per
-// cycle) bank-conflict free.  One DMA instruction fills 8 rows: lane l
-// loads row l / 8, physical chunk l % 8, i.e. logical chunk (l % 8) ^ (l / 8).
-template <int WAVES, int BLOCKS>
+// cycle) bank-conflict free.  One DMA instruction fills 64 / CPR rows: lane
+// l loads row l / CPR, physical chunk l % CPR, i.e. logical chunk
+// (l % CPR) ^ (row & 7).
+template <int WAVES, int BLOCKS, int CPR>
 __device__ __forceinline__ void gm_dma(__amdgpu_buffer_rsrc_t r, uint32_t row_bytes, uint32_t k_off,
                                        uint16_t* lds) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const uint32_t logical = (lane & 7) ^ (lane >> 3);
 #pragma unroll
     for (int j = 0; j < BLOCKS; ++j) {
         const int blk = wave + WAVES * j;
-        const uint32_t row = 8 * blk + (lane >> 3);
+        const uint32_t row = (64 / CPR) * blk + lane / CPR;
+        const uint32_t logical = (lane % CPR) ^ (row & 7);
         dma16(r, lds + 512 * blk, row * row_bytes + k_off + 16 * logical);
     }
 }
@@ -244,12 +251,13 @@ __global__ __launch_bounds__(C::THREADS, C::MINB) void gemm_kernel(GemmArgs g) {
 
     // Operand read offsets (elements) inside a stage for block 0, per
     // k-step; block i adds 32 i rows.
-    int a_off[4], b_off[4];
+    constexpr int BK = C::BK, KS = C::KS;
+    int a_off[KS], b_off[KS];
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
+    for (int s = 0; s < KS; ++s) {
         const int chunk = (2 * s + (lane >> 5)) ^ (lane & 7);
-        a_off[s] = (32 * IM * wr + (lane & 31)) * kGmBK + 8 * chunk;
-        b_off[s] = C::A_ELEMS + (32 * JN * wc + (lane & 31)) * kGmBK + 8 * chunk;
+        a_off[s] = (32 * IM * wr + (lane & 31)) * BK + 8 * chunk;
+        b_off[s] = C::A_ELEMS + (32 * JN * wc + (lane & 31)) * BK + 8 * chunk;
     }
 
     f32x16_t acc[IM][JN];
@@ -260,13 +268,13 @@ __global__ __launch_bounds__(C::THREADS, C::MINB) void gemm_kernel(GemmArgs g) {
 #pragma unroll
             for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
 
-    const uint32_t nk = N / kGmBK;
+    const uint32_t nk = N / BK;
     auto dma_slice = [&](uint32_t kt, uint16_t* st) __attribute__((always_inline)) {
-        gm_dma<C::WAVES, C::A_DMA>(ra, row_bytes, kt * kGmBK * 2, st);
-        gm_dma<C::WAVES, C::B_DMA>(rb, row_bytes, kt * kGmBK * 2, st + C::A_ELEMS);
+        gm_dma<C::WAVES, C::A_DMA, C::CPR>(ra, row_bytes, kt * BK * 2, st);
+        gm_dma<C::WAVES, C::B_DMA, C::CPR>(rb, row_bytes, kt * BK * 2, st + C::A_ELEMS);
     };
     // Step kt: wait for slice kt, barrier, start slice kt + 1 into the stage
-    // step kt - 1 read, then four k-steps of MFMAs from stage kt % 2.
+    // step kt - 1 read, then KS k-steps of MFMAs from stage kt % 2.
     auto step = [&](uint32_t kt, const uint16_t* cur, uint16_t* nxt) __attribute__((always_inline)) {
         __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
         // The reads of step kt - 1 have all been consumed by its MFMAs; the
@@ -279,15 +287,15 @@ __global__ __launch_bounds__(C::THREADS, C::MINB) void gemm_kernel(GemmArgs g) {
         auto read = [&](int s) __attribute__((always_inline)) {
 #pragma unroll
             for (int i = 0; i < IM; ++i)
-                a[s & 1][i] = as_bf16x8(*reinterpret_cast<const uint4*>(cur + a_off[s] + 32 * kGmBK * i));
+                a[s & 1][i] = as_bf16x8(*reinterpret_cast<const uint4*>(cur + a_off[s] + 32 * BK * i));
 #pragma unroll
             for (int j = 0; j < JN; ++j)
-                b[s & 1][j] = as_bf16x8(*reinterpret_cast<const uint4*>(cur + b_off[s] + 32 * kGmBK * j));
+                b[s & 1][j] = as_bf16x8(*reinterpret_cast<const uint4*>(cur + b_off[s] + 32 * BK * j));
         };
         read(0);
 #pragma unroll
-        for (int s = 0; s < 4; ++s) {
-            if (s < 3) read(s + 1);
+        for (int s = 0; s < KS; ++s) {
+            if (s < KS - 1) read(s + 1);
 #pragma unroll
             for (int i = 0; i < IM; ++i)
 #pragma unroll
@@ -298,9 +306,9 @@ __global__ __launch_bounds__(C::THREADS, C::MINB) void gemm_kernel(GemmArgs g) {
         // followed by the reads of the k-step after the next.
         __builtin_amdgcn_sched_group_barrier(0x100, 2 * (IM + JN), 0);
 #pragma unroll
-        for (int s = 0; s < 4; ++s) {
+        for (int s = 0; s < KS; ++s) {
             __builtin_amdgcn_sched_group_barrier(0x008, IM * JN, 0);
-            if (s < 2) __builtin_amdgcn_sched_group_barrier(0x100, IM + JN, 0);
+            if (s < KS - 2) __builtin_amdgcn_sched_group_barrier(0x100, IM + JN, 0);
         }
     };
     dma_slice(0, s_0);
@@ -397,7 +405,8 @@ hipError_t launch_gemm(const GemmArgs& g, hipStream_t stream) {
     const uint32_t cus = (uint32_t)gemm_cus();
     if (gemm_tiles<GmLarge>(g) >= cus) return gemm_launch<GmLarge>(g, stream);
     if (gemm_tiles<GmSmall>(g) >= cus) return gemm_launch<GmSmall>(g, stream);
-    return gemm_launch<GmMini>(g, stream);
+    if (g.N % GmMini::BK == 0) return gemm_launch<GmMini>(g, stream);
+    return gemm_launch<GmMini64>(g, stream);
 }
 
 }  // namespace tiattn

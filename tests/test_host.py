@@ -38,6 +38,35 @@ def test_every_declared_function_is_exported_and_bound():
     assert set(names) == set(attn.SIGNATURES), set(names) ^ set(attn.SIGNATURES)
 
 
+def test_layer_op_validation():
+    """Decoder-layer ops reject bad arguments before any launch."""
+    assert L.toyinfer_rmsnorm_bf16(P, P, P, None, 1e-6, 7, None) == INVALID     # odd size
+    assert L.toyinfer_rmsnorm_bf16(P + 2, P, P, None, 1e-6, 8, None) == INVALID  # 4-byte alignment
+    assert L.toyinfer_batch_rmsnorm_bf16(P, P, P, P + 2, 1e-6, 2, 8, None) == INVALID
+    assert L.toyinfer_batch_rmsnorm_bf16(P, P, P, None, 1e-6, 0, 8, None) == INVALID
+    assert L.toyinfer_residual_add_bf16(P, None, 8, None) == INVALID
+    assert L.toyinfer_batch_residual_add_bf16(P, P, 3, 5, None) == INVALID    # odd total
+    assert L.toyinfer_swiglu_bf16x2(P, P, P, 0, None) == INVALID
+    assert L.toyinfer_batch_swiglu_bf16x2(P, P, P + 2, 2, 8, None) == INVALID
+    g = L.toyinfer_gather_embedding_bf16
+    assert g(P, P, P, 0, 8, 10, None) == INVALID
+    assert g(P, P, P, 70000, 8, 10, None) == INVALID                          # > 65535 tokens
+    assert g(P, P + 2, P, 1, 8, 10, None) == INVALID                          # ids 4-byte aligned
+    assert g(P, P, P, 1, 8, 0, None) == INVALID                               # empty vocabulary
+    assert L.toyinfer_argmax_f32(P, 0, P, None) == INVALID
+    assert L.toyinfer_argmax_f32(P, 10, None, None) == INVALID
+    import ctypes
+    seg = L.toyinfer_gemm_segments_bf16
+    W = (ctypes.c_void_p * 3)(P, P, P)
+    Y = (ctypes.c_void_p * 3)(P, P, P)
+    R = (ctypes.c_uint32 * 3)(64, 64, 64)
+    assert seg(P, 100, 256, 4, W, Y, R, 0, None) == INVALID                   # at most 3 segments
+    assert seg(P, 100, 256, 0, W, Y, R, 0, None) == INVALID
+    assert seg(P, 4, 256, 3, W, Y, R, 0, None) == UNSUPPORTED                 # GEMV-sized batch
+    assert seg(P, 100, 96, 3, W, Y, R, 0, None) == UNSUPPORTED                # N % 64 != 0
+    assert seg(P + 2, 100, 256, 3, W, Y, R, 0, None) == UNSUPPORTED           # unaligned input
+
+
 def test_model_header_functions_exported_and_bound():
     """include/toyinfer_qwen3.h: every function exported and bound by
     toyinfer_amd/qwen3.py (importing it binds them; no GPU call)."""

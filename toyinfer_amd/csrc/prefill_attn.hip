@@ -406,6 +406,8 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(PrefillProblem p
 constexpr int kSkBM = 32;
 constexpr int kSkBN = 32;
 
+constexpr uint32_t kSkOob = 0xF0000000u;  // a byte offset past any K/V buffer range here
+
 template <int D>
 struct SkShape {
     static constexpr int CPR = D / 8;
@@ -477,16 +479,21 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_splitkv_kernel(PrefillP
     __amdgpu_buffer_rsrc_t rv = make_rsrc(p.v + (int64_t)it.kvh * D, kv_bytes);
 
     uint4 kreg[P::LOADS], vreg[P::LOADS];
-    auto load_k = [&](uint32_t t) {
+    // Tile t of the item's keys; `base` overrides the tile's byte offset (a
+    // value past every buffer range makes the loads return zeros without
+    // touching memory).
+    auto load_k_at = [&](uint32_t base) {
 #pragma unroll
         for (int i = 0; i < P::LOADS; ++i)
-            kreg[i] = buf_load16(rk, t * kSkBN * row_bytes + voff + i * P::ROWS_PER_LOAD * row_bytes);
+            kreg[i] = buf_load16(rk, base + voff + i * P::ROWS_PER_LOAD * row_bytes);
     };
-    auto load_v = [&](uint32_t t) {
+    auto load_v_at = [&](uint32_t base) {
 #pragma unroll
         for (int i = 0; i < P::LOADS; ++i)
-            vreg[i] = buf_load16(rv, t * kSkBN * row_bytes + voff + i * P::ROWS_PER_LOAD * row_bytes);
+            vreg[i] = buf_load16(rv, base + voff + i * P::ROWS_PER_LOAD * row_bytes);
     };
+    auto load_k = [&](uint32_t t) { load_k_at(t * kSkBN * row_bytes); };
+    auto load_v = [&](uint32_t t) { load_v_at(t * kSkBN * row_bytes); };
     auto load = [&](uint32_t t) {
         load_k(t);
         load_v(t);
@@ -520,7 +527,16 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_splitkv_kernel(PrefillP
 #pragma unroll
             for (int i = 0; i < P::LOADS; ++i)
                 *reinterpret_cast<uint4*>(sk + (st_row + i * P::ROWS_PER_LOAD) * P::PK + 8 * st_c) = kreg[i];
-            if (t + 4 < n_tiles) load_k(t + 4);
+            // The next tile's loads are unconditional (out of range past the
+            // item's last tile), so that the compiler's wait before the next
+            // iteration's K stores counts exactly the K loads and leaves the
+            // V loads in flight.
+            const uint32_t next = t + 4 < n_tiles ? (t + 4) * kSkBN * row_bytes : kSkOob;
+            load_k_at(next);
+            // Keep the K requests here and the V stores after the QK
+            // products: the scheduler would otherwise hoist the V stores
+            // (and their wait for V) above both.
+            __builtin_amdgcn_sched_barrier(0);
             const uint32_t n0 = t * kSkBN;
             f32x16_t st;
 #pragma unroll
@@ -529,10 +545,11 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_splitkv_kernel(PrefillP
 #pragma unroll
             for (int ks = 0; ks < P::KSTEPS; ++ks)
                 st = mfma32x32x16(as_bf16x8(*reinterpret_cast<const uint4*>(ka + 16 * ks)), qf[ks], st);
+            __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int i = 0; i < P::LOADS; ++i)
                 *reinterpret_cast<uint4*>(sv + (st_row + i * P::ROWS_PER_LOAD) * P::PV + 8 * st_c) = vreg[i];
-            if (t + 4 < n_tiles) load_v(t + 4);
+            load_v_at(next);
             if (n0 + kSkBN - 1 > q0) {
 #pragma unroll
                 for (int i = 0; i < 16; ++i) {

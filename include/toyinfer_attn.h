@@ -272,6 +272,32 @@ int toyinfer_gather_embedding_bf16(const void* embedding_table, const uint32_t* 
  * reference's greedy sampler does this on the host (src/sampler.cpp:71-82). */
 int toyinfer_argmax_f32(const float* logits, uint32_t n, uint32_t* out_index, void* stream);
 
+/* Device-side top-k / top-p sampling.  Replaces toyinfer::Sampler::sample
+ * (include/sampler.h:10-16; src/sampler.cpp:18-67), which the reference runs
+ * on the host over logits copied back each step (src/engine.cpp:183-190):
+ * here logits[0..vocab) stay in device memory and *out_token is written on
+ * the device.  Same rules: |temperature| < 1e-3 or top_k == 1 gives the first
+ * index of the maximum (as toyinfer_argmax_f32); otherwise x = logit /
+ * temperature, the top min(top_k, vocab) values of x, p = exp((x - max) /
+ * temperature) normalised, sorted descending, cut after the first running
+ * sum above top_p, and the first kept token whose running sum exceeds
+ * *coin times the kept sum.  *coin (device memory, in [0, 1)) is the
+ * uniform draw the reference takes from its time-seeded mt19937.  Ties at
+ * the k-th value keep the lowest indices.  The workspace
+ * (toyinfer_sample_workspace_bytes(), 256-byte aligned) must be zero before
+ * its first use; every call leaves it so.  Calls sharing a workspace must be
+ * stream-ordered.  Limits: vocab <= TOYINFER_SAMPLE_MAX_VOCAB, top_k <=
+ * TOYINFER_SAMPLE_MAX_K unless greedy (TOYINFER_ERR_UNSUPPORTED beyond);
+ * top_k == 0 (an assertion in the reference) and a negative or NaN
+ * temperature give TOYINFER_ERR_INVALID_ARGUMENT. */
+#define TOYINFER_SAMPLE_MAX_K 256u
+#define TOYINFER_SAMPLE_MAX_VOCAB 262144u
+size_t toyinfer_sample_workspace_bytes(void);
+int toyinfer_sample_topk_topp_f32(const float* logits, uint32_t vocab, float temperature,
+                                  uint32_t top_k, float top_p, const float* coin,
+                                  uint32_t* out_token, void* workspace, size_t workspace_bytes,
+                                  void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,6 +1,6 @@
 /* Minimal Qwen3 forward on one MI355X for the end-to-end configuration:
- * prefill of a prompt, then greedy decode steps whose body (all layers, the
- * lm-head, argmax and the position advance) can be captured once in a
+ * prefill of a prompt, then decode steps (greedy or sampled) whose body (all layers, the
+ * lm-head, the token pick and the position advance) can be captured once in a
  * hipGraph and replayed, reading the position and the current token on the
  * device.  This re-creates the part of the reference's Transformer that the
  * attention path sits in (src/transformer.cpp:320-681): the prefill layer
@@ -79,6 +79,16 @@ int toyinfer_qwen3_prefill(toyinfer_qwen3* m, const uint32_t* token_ids_d, uint3
  * replayed (one graph launch per step); without it the same kernels are
  * launched directly.  pos + steps must stay below max_seq_len. */
 int toyinfer_qwen3_decode(toyinfer_qwen3* m, uint32_t steps, int use_graph);
+
+/* The pick after the lm-head in prefill and decode, as the reference's
+ * sampler options (--temperature, --top_k, --top_p; src/options.cpp:32-34,
+ * src/sampler.cpp:18-67; see toyinfer_sample_topk_topp_f32): greedy (the
+ * default after create) when |temperature| < 1e-3 or top_k == 1.  Each draw's
+ * uniform number is a SplitMix64 hash of (seed, device position), so graph
+ * replays sample without host work and a seed reproduces a generation.  A
+ * captured decode graph is dropped and captured again on the next decode. */
+int toyinfer_qwen3_set_sampling(toyinfer_qwen3* m, float temperature, uint32_t top_k,
+                                float top_p, uint64_t seed);
 
 /* Waits for the model's stream. */
 int toyinfer_qwen3_synchronize(toyinfer_qwen3* m);

@@ -24,6 +24,7 @@ _LIB_PATH = os.path.join(_HERE, "liboracle.so")
 _f32p = np.ctypeslib.ndpointer(dtype=np.float32, flags="C_CONTIGUOUS")
 _u16p = np.ctypeslib.ndpointer(dtype=np.uint16, flags="C_CONTIGUOUS")
 _u32 = ctypes.c_uint32
+_u32p = np.ctypeslib.ndpointer(dtype=np.uint32, flags="C_CONTIGUOUS")
 _f32 = ctypes.c_float
 _vp = ctypes.c_void_p
 
@@ -77,6 +78,9 @@ def _load() -> ctypes.CDLL:
         "or_residual_add": (None, [_f32p, _f32p, _f32p, ctypes.c_int64]),
         "or_swiglu": (None, [_f32p, _f32p, _f32p, ctypes.c_int64]),
         "or_argmax": (_u32, [_f32p, _u32]),
+        "or_sample_topk_topp": (_u32, [_f32p, _u32, _f32, _u32, _f32, _f32, _u32p, _f32p,
+                                       _u32p]),
+        "or_sample_coin": (_f32, [ctypes.c_uint64, _u32]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -378,6 +382,25 @@ def swiglu(gate, up):
 def argmax(logits):
     x = _c32(logits).reshape(-1)
     return int(lib().or_argmax(x, x.size))
+
+
+def sample_topk_topp(logits, temperature, top_k, top_p, u):
+    """src/sampler.cpp:18-67 with the uniform draw u given: (token, order,
+    probs, kept) where order/probs are the sorted top-k ids and probabilities
+    (empty on the greedy path) and kept is the top-p prefix length."""
+    x = _c32(logits).reshape(-1)
+    greedy = abs(temperature) < 1e-3 or top_k == 1
+    k = 0 if greedy else min(top_k, x.size)
+    order = np.zeros(max(k, 1), np.uint32)
+    probs = np.zeros(max(k, 1), np.float32)
+    kept = np.zeros(1, np.uint32)
+    tok = lib().or_sample_topk_topp(x, x.size, temperature, top_k, top_p, u, order, probs, kept)
+    return int(tok), order[:k], probs[:k], int(kept[0])
+
+
+def sample_coin(seed, pos):
+    """The harness's per-position uniform draw (SplitMix64 output function)."""
+    return float(lib().or_sample_coin(seed, pos))
 
 
 # ------------------------------------------------------------ Qwen3 forward

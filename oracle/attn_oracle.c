@@ -28,6 +28,7 @@
  *   row RMSNorm, residual  tests/rmsnorm_test_common.h, tests/add_test_common.h,
  *   add, SwiGLU, argmax .. tests/swiglu_test_common.h, the batch tests, and
  *                          src/sampler.cpp:71-82
+ *   top-k/top-p sampling . src/sampler.cpp:18-67 (the draw u is an input)
  *
  * Arithmetic follows the reference's host code operation by operation
  * (float vs double, accumulation order, where bf16 rounding happens).
@@ -628,3 +629,90 @@ uint32_t or_argmax(const float* logits, uint32_t n) {
     return idx;
 }
 
+
+/* ------------------------------------------------------------ sampling */
+
+typedef struct {
+    float x;
+    uint32_t i;
+} or_scored;
+
+/* Larger value first; equal values by smaller index. */
+static int or_scored_cmp(const void* a, const void* b) {
+    const or_scored* p = (const or_scored*)a;
+    const or_scored* q = (const or_scored*)b;
+    if (p->x != q->x) return p->x > q->x ? -1 : 1;
+    return p->i < q->i ? -1 : (p->i > q->i);
+}
+
+/* src/sampler.cpp:18-67 with the uniform draw u in [0, 1) given (the
+ * reference takes it from a time-seeded mt19937, :58-60):
+ *   greedy (or_argmax) when |T - 0| < 1e-3 or top_k == 1 (:20-22);
+ *   x_i = logit_i / T (:24-27); the top k = min(top_k, n) of x (:29-32; a
+ *   full sort here, larger first, equal values by index, where the reference
+ *   quick-selects and keeps its own order among ties);
+ *   p_i = expf((x_i - max) / T), summed in that order, divided by the sum
+ *   (:33-44); sorted descending (:45-49, already so);
+ *   kept = 1 + the first index whose running sum exceeds top_p (:50-57), or
+ *   all k when none does (the reference then reads one entry past its top k);
+ *   coin = u * the kept sum; the first kept index whose running sum exceeds
+ *   the coin, else the last kept one (:58-67).
+ * Optional outputs: order[k] (token ids, sorted), probs[k], kept. */
+uint32_t or_sample_topk_topp(const float* logits, uint32_t n, float temperature, uint32_t top_k,
+                             float top_p, float u, uint32_t* order, float* probs,
+                             uint32_t* kept_out) {
+    if (fabsf(temperature - 0.0f) < 1e-3f || top_k == 1) {
+        if (kept_out) *kept_out = 1;
+        return or_argmax(logits, n);
+    }
+    const uint32_t k = top_k < n ? top_k : n;
+    or_scored* t = (or_scored*)malloc(sizeof(or_scored) * n);
+    float* p = (float*)malloc(sizeof(float) * k);
+    for (uint32_t i = 0; i < n; ++i) {
+        t[i].x = logits[i] / temperature;
+        t[i].i = i;
+    }
+    qsort(t, n, sizeof(or_scored), or_scored_cmp);
+    const float max_x = t[0].x;
+    float sum = 0.0f;
+    for (uint32_t i = 0; i < k; ++i) {
+        p[i] = expf((t[i].x - max_x) / temperature);
+        sum += p[i];
+    }
+    for (uint32_t i = 0; i < k; ++i) p[i] /= sum;
+    float acc = 0.0f;
+    uint32_t j = 0;
+    for (; j < k; ++j) {
+        acc += p[j];
+        if (acc > top_p) break;
+    }
+    const uint32_t kept = j < k ? j + 1 : k;
+    const float coin = u * acc;
+    uint32_t pick = t[kept - 1].i;
+    float run = 0.0f;
+    for (uint32_t i = 0; i < kept; ++i) {
+        run += p[i];
+        if (run > coin) {
+            pick = t[i].i;
+            break;
+        }
+    }
+    if (order)
+        for (uint32_t i = 0; i < k; ++i) order[i] = t[i].i;
+    if (probs) memcpy(probs, p, sizeof(float) * k);
+    if (kept_out) *kept_out = kept;
+    free(t);
+    free(p);
+    return pick;
+}
+
+/* The draw the model harness uses for position pos: the SplitMix64 output
+ * function (Steele, Lea, Flood 2014) of seed + (pos + 1) * 0x9E3779B97F4A7C15,
+ * top 24 bits scaled to [0, 1). */
+float or_sample_coin(uint64_t seed, uint32_t pos) {
+    uint64_t z = seed + (uint64_t)(pos + 1) * 0x9E3779B97F4A7C15ull;
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    z ^= z >> 31;
+    return (float)(uint32_t)(z >> 40) * 0x1p-24f;
+}

@@ -56,6 +56,18 @@ def test_layer_op_validation():
     assert L.toyinfer_argmax_f32(P, 0, P, None) == INVALID
     assert L.toyinfer_argmax_f32(P, 10, None, None) == INVALID
     import ctypes
+    ws = attn.sample_workspace_bytes()
+    assert ws >= 256 + 2 * 32 * 256 * 4
+    smp = L.toyinfer_sample_topk_topp_f32
+    assert smp(P, 1000, 0.6, 0, 0.95, P, P, P, ws, None) == INVALID   # top_k 0 (asserted in the reference)
+    assert smp(P, 1000, -0.5, 20, 0.95, P, P, P, ws, None) == INVALID  # negative temperature
+    assert smp(P, 1000, float("nan"), 20, 0.95, P, P, P, ws, None) == INVALID
+    assert smp(P, 0, 0.6, 20, 0.95, P, P, P, ws, None) == INVALID
+    assert smp(P, 1000, 0.6, 20, 0.95, None, P, P, ws, None) == INVALID  # coin required
+    assert smp(P, 1000, 0.6, 20, 0.95, P, P, P + 64, ws, None) == INVALID  # workspace alignment
+    assert smp(P, 1000, 0.6, 257, 0.95, P, P, P, ws, None) == UNSUPPORTED  # k above the maximum
+    assert smp(P, 262145, 0.6, 20, 0.95, P, P, P, ws, None) == UNSUPPORTED
+    assert smp(P, 1000, 0.6, 20, 0.95, P, P, P, ws - 4, None) == WORKSPACE
     seg = L.toyinfer_gemm_segments_bf16
     W = (ctypes.c_void_p * 3)(P, P, P)
     Y = (ctypes.c_void_p * 3)(P, P, P)
@@ -74,7 +86,7 @@ def test_model_header_functions_exported_and_bound():
     text = re.sub(r"/\*.*?\*/", "", open(os.path.join(ROOT, "include", "toyinfer_qwen3.h")).read(),
                   flags=re.S)
     names = set(re.findall(r"\b(toyinfer_\w+)\s*\(", text))
-    assert len(names) == 10
+    assert len(names) == 11
     out = subprocess.run(["nm", "-D", "--defined-only", attn.LIB_PATH], capture_output=True,
                          text=True, check=True).stdout
     assert names <= set(re.findall(r"\bT (toyinfer_\w+)", out))
@@ -108,6 +120,7 @@ def test_model_config_validation():
     assert create(ctypes.byref(c), P, P, P, layers, ctypes.byref(h)) == UNSUPPORTED
     assert L.toyinfer_qwen3_prefill(None, P, 4) == INVALID
     assert L.toyinfer_qwen3_decode(None, 1, 1) == INVALID
+    assert L.toyinfer_qwen3_set_sampling(None, 0.6, 20, 0.95, 1) == INVALID
 
 
 def test_abi_version_and_status_strings():

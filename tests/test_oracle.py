@@ -441,3 +441,89 @@ def test_argmax_first_maximum_and_nan():
     assert oracle.argmax(x) == 3
     assert oracle.argmax(np.array([-np.inf, np.nan], np.float32)) == 0xFFFFFFFF
 
+
+
+# ------------------------------------------------------------ sampling
+# oracle.sample_topk_topp restates src/sampler.cpp:18-67 with the draw u given.
+
+def test_sample_known_answers():
+    """Hand-computed: logits [2, 1, 0, -1], T = 1, top_k = 3 gives
+    p = e^(2,1,0) / (e^2 + e + 1) = (0.6652, 0.2447, 0.0900); cumulative
+    0.6652, 0.9100, 1."""
+    lg = np.array([2, 1, 0, -1], np.float32)
+    e = np.exp(np.array([2.0, 1.0, 0.0]))
+    tok, order, probs, kept = oracle.sample_topk_topp(lg, 1.0, 3, 0.8, 0.5)
+    assert list(order) == [0, 1, 2] and kept == 2 and tok == 0
+    np.testing.assert_allclose(probs, e / e.sum(), rtol=1e-6)
+    assert oracle.sample_topk_topp(lg, 1.0, 3, 0.8, 0.9)[0] == 1    # coin 0.819 > 0.665
+    for u in (0.0, 0.5, 0.99):                                          # top_p 0.5 keeps one
+        assert oracle.sample_topk_topp(lg, 1.0, 3, 0.5, u)[:4:3] == (0, 1)
+    assert oracle.sample_topk_topp(lg, 1.0, 3, 1.0, 0.95)[0] == 2       # coin 0.95 > 0.910
+    assert oracle.sample_topk_topp(lg, 1.0, 3, 0.0, 0.99)[0] == 0       # top_p 0: first only
+
+
+def test_sample_greedy_paths():
+    """|T| < 1e-3 or top_k == 1: the reference's argmax (first maximum,
+    strict '>' from -FLT_MAX; none for all -inf)."""
+    lg = np.array([1, 3, 3, 2], np.float32)
+    for T, k in ((0.0, 20), (5e-4, 20), (1.0, 1), (0.7, 1)):
+        assert oracle.sample_topk_topp(lg, T, k, 0.95, 0.7)[0] == 1
+    assert oracle.sample_topk_topp(np.full(5, -np.inf, np.float32), 0.0, 5, 0.9, 0.5)[0] == 0xFFFFFFFF
+
+
+@pytest.mark.parametrize("T", [0.5, 0.7, 1.3])
+def test_sample_probabilities_closed_form(T):
+    """The reference divides by T twice (x = logit / T, then exp((x - max) / T)):
+    the kept probabilities are softmax(logit / T^2) over the top k in float64.
+    One division instead of two would fail this for T != 1."""
+    rng = np.random.default_rng(int(T * 10))
+    lg = (rng.standard_normal(500) * 2).astype(np.float32)
+    k = 40
+    tok, order, probs, kept = oracle.sample_topk_topp(lg, T, k, 0.95, 0.3)
+    x = lg.astype(np.float32) / np.float32(T)
+    exp_order = np.lexsort((np.arange(lg.size), -x))[:k]           # larger first, ties by index
+    assert np.array_equal(order, exp_order)
+    z = lg[order].astype(np.float64) / (T * T)
+    ref = np.exp(z - z.max())
+    ref /= ref.sum()
+    np.testing.assert_allclose(probs, ref, rtol=2e-5, atol=1e-9)
+    cum = np.cumsum(ref)
+    assert np.min(np.abs(cum - 0.95)) > 1e-5                        # the cut is not a near tie
+    assert kept == int(np.argmax(cum > 0.95)) + 1
+
+
+def test_sample_coin_walk_brute_force():
+    """A draw at the middle of kept interval j picks order[j]; u = 0 picks the
+    first; a draw just below 1 picks the last kept."""
+    rng = np.random.default_rng(9)
+    lg = (rng.standard_normal(300) * 1.5).astype(np.float32)
+    tok, order, probs, kept = oracle.sample_topk_topp(lg, 1.0, 30, 0.9, 0.0)
+    assert tok == order[0]
+    cum = np.cumsum(probs.astype(np.float64))[:kept]
+    lo = np.concatenate([[0.0], cum[:-1]])
+    for j in range(kept):
+        u = (lo[j] + cum[j]) / 2 / cum[-1]
+        assert oracle.sample_topk_topp(lg, 1.0, 30, 0.9, u)[0] == order[j], j
+    assert oracle.sample_topk_topp(lg, 1.0, 30, 0.9, 1 - 2 ** -24)[0] == order[kept - 1]
+
+
+def test_sample_ties_keep_lowest_indices():
+    lg = np.array([5, 3, 3, 3, 1], np.float32)
+    tok, order, probs, kept = oracle.sample_topk_topp(lg, 1.0, 2, 1.0, 0.99)
+    assert list(order) == [0, 1] and tok == 1
+    lg = np.array([0, 2, 2, 1, 2], np.float32)
+    assert list(oracle.sample_topk_topp(lg, 1.0, 3, 1.0, 0.5)[1]) == [1, 2, 4]
+
+
+def test_sample_coin_is_splitmix64():
+    """The first two SplitMix64 outputs of seed 0 are the published
+    0xE220A8397B1DCDAF and 0x6E789E6AA1B965F4 (Vigna's splitmix64.c); the
+    draw is their top 24 bits over 2^24.  Draws over many positions are
+    uniform to within sampling error."""
+    assert oracle.sample_coin(0, 0) == 0xE220A8 / 2 ** 24
+    assert oracle.sample_coin(0, 1) == 0x6E789E / 2 ** 24
+    u = np.array([oracle.sample_coin(12345, p) for p in range(20000)])
+    assert u.min() >= 0 and u.max() < 1
+    assert abs(u.mean() - 0.5) < 0.01
+    hist = np.histogram(u, bins=10, range=(0, 1))[0]
+    assert hist.min() > 1800 and hist.max() < 2200

@@ -150,3 +150,79 @@ def test_create_rejects_bad_config(dev):
                 dict(hidden_size=100)):
         with pytest.raises(Exception):
             qwen3.Qwen3(qwen3.Config(**dict(TINY, **bad)), dw)
+
+
+def coin_clear(logits, T, k, p, u, margin=1e-4):
+    """True when the draw u lands at least `margin` (in probability) away
+    from every boundary of the oracle's kept intervals, so that the device's
+    differently ordered float sums cannot pick a neighbour."""
+    _, _, probs, kept = oracle.sample_topk_topp(logits, T, k, p, u)
+    cum = np.cumsum(probs.astype(np.float64))
+    coin = u * cum[kept - 1]
+    return np.min(np.abs(cum[:kept] - coin)) > margin and np.min(np.abs(cum[:-1] - p)) > margin
+
+
+@pytest.mark.parametrize("graph", [False, True])
+def test_sampled_decode_vs_oracle(dev, graph):
+    """set_sampling(T, top_k, top_p, seed): every pick (prefill and each decode
+    step) equals the oracle's sampler on the device logits with the draw
+    sample_coin(seed, position before the step)."""
+    print(f"[step] qwen3 sampled decode graph={graph}", flush=True)
+    cfg = TINY
+    _, dw = make_weights(cfg, dev, seed=54)
+    T, steps, seed = 10, 8, 2024
+    temp, top_k, top_p = 0.7, 20, 0.9
+    ids = prompt(T, cfg["vocab_size"], seed=55)
+    m = qwen3.Qwen3(qwen3.Config(**cfg), dw)
+    m.set_sampling(temp, top_k, top_p, seed)
+    H.sync()
+    m.prefill(ids_dev(ids, dev), T)
+    checked = 0
+    for s in range(steps + 1):
+        if s:
+            m.decode(1, graph)
+        got = m.logits_host()
+        pos = T - 1 + s
+        tok = m.tokens_host(pos + 2)[pos + 1]
+        u = oracle.sample_coin(seed, pos)
+        if coin_clear(got, temp, top_k, top_p, u):
+            assert tok == oracle.sample_topk_topp(got, temp, top_k, top_p, u)[0], f"step {s}"
+            checked += 1
+    assert checked >= steps - 1
+    assert m.position_host() == T + steps
+    m.close()
+
+
+def test_sampled_graph_equals_direct_and_reseeding(dev):
+    """Sampled generation: graph replays and direct launches give the same
+    tokens; the same seed reproduces them after re-prefill; set_sampling
+    between replays re-captures (greedy again = argmax of the logits)."""
+    cfg = dict(TINY, num_layers=3)
+    _, dw = make_weights(cfg, dev, seed=56, tied=True)
+    T = 7
+    ids = prompt(T, cfg["vocab_size"], seed=57)
+    a = qwen3.Qwen3(qwen3.Config(**cfg), dw)
+    b = qwen3.Qwen3(qwen3.Config(**cfg), dw)
+    for m in (a, b):
+        m.set_sampling(1.0, 50, 0.95, 99)
+    H.sync()
+    for m in (a, b):
+        m.prefill(ids_dev(ids, dev), T)
+    a.decode(10, False)
+    b.decode(4, True)
+    b.decode(6, True)
+    ta, tb = a.tokens_host(T + 11), b.tokens_host(T + 11)
+    assert np.array_equal(ta, tb)
+    a.prefill(ids_dev(ids, dev), T)
+    a.decode(10, True)
+    assert np.array_equal(a.tokens_host(T + 11), ta)
+    b.set_sampling(0.0, 20, 0.95, 99)
+    b.decode(1, True)
+    toks = b.tokens_host(T + 12)
+    assert toks[T + 11] == oracle.argmax(b.logits_host())
+    with pytest.raises(Exception):
+        b.set_sampling(0.7, 0, 0.9, 1)
+    with pytest.raises(Exception):
+        b.set_sampling(0.7, 300, 0.9, 1)
+    a.close()
+    b.close()

@@ -66,6 +66,9 @@ SIGNATURES = {
     "toyinfer_batch_swiglu_bf16x2": (_i32, [_vp, _vp, _vp, _u32, _u32, _vp]),
     "toyinfer_gather_embedding_bf16": (_i32, [_vp, _vp, _vp, _u32, _u32, _u32, _vp]),
     "toyinfer_argmax_f32": (_i32, [_vp, _u32, _vp, _vp]),
+    "toyinfer_sample_workspace_bytes": (_sz, []),
+    "toyinfer_sample_topk_topp_f32": (_i32, [_vp, _u32, _f32, _u32, _f32, _vp, _vp, _vp, _sz,
+                                             _vp]),
     "toyinfer_decode_qkv_prologue_bf16": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _u32, _f32,
                                                  _vp, _vp, _vp, _u32, _u32, _u32, _vp]),
 }
@@ -381,4 +384,19 @@ def gather_embedding_bf16(table, token_ids, hidden_states, num_tokens: int, hidd
 def argmax_f32(logits, n: int, out_index, stream=None) -> None:
     _check("argmax_f32", LIB.toyinfer_argmax_f32(_ptr(logits), n, _ptr(out_index),
                                                  _stream(stream)))
+
+
+def sample_workspace_bytes() -> int:
+    return int(LIB.toyinfer_sample_workspace_bytes())
+
+
+def sample_topk_topp_f32(logits, vocab: int, temperature: float, top_k: int, top_p: float,
+                         coin, out_token, workspace, stream=None) -> None:
+    """Device top-k/top-p pick (src/sampler.cpp:18-67); coin is a device
+    float in [0, 1); workspace zero-filled before its first use."""
+    _check("sample_topk_topp_f32",
+           LIB.toyinfer_sample_topk_topp_f32(_ptr(logits), vocab, temperature, top_k, top_p,
+                                             _ptr(coin), _ptr(out_token), _ptr(workspace),
+                                             workspace.numel() * workspace.element_size(),
+                                             _stream(stream)))
 

@@ -567,4 +567,24 @@ int toyinfer_argmax_f32(const float* logits, uint32_t n, uint32_t* out_index, vo
     return from_hip(launch_argmax(logits, n, out_index, nullptr, 1, as_stream(stream)));
 }
 
+size_t toyinfer_sample_workspace_bytes(void) { return sample_workspace_bytes(); }
+
+int toyinfer_sample_topk_topp_f32(const float* logits, uint32_t vocab, float temperature,
+                                  uint32_t top_k, float top_p, const float* coin,
+                                  uint32_t* out_token, void* workspace, size_t workspace_bytes,
+                                  void* stream) {
+    if (!logits || !aligned(logits, 4) || !out_token || !aligned(out_token, 4) || !coin ||
+        !aligned(coin, 4) || !workspace || !aligned(workspace, 256))
+        return TOYINFER_ERR_INVALID_ARGUMENT;
+    SampleArgs a;
+    const int st = sample_config(vocab, temperature, top_k, top_p, a);
+    if (st != TOYINFER_OK) return st;
+    if (workspace_bytes < sample_workspace_bytes()) return TOYINFER_ERR_WORKSPACE;
+    a.logits = logits;
+    a.coin = coin;
+    a.out = out_token;
+    a.workspace = workspace;
+    return from_hip(launch_sample(a, as_stream(stream)));
+}
+
 }  // extern "C"

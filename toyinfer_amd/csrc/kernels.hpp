@@ -168,6 +168,31 @@ hipError_t launch_argmax_wide(const float* logits, uint32_t n, uint32_t* out, ui
                               uint32_t out_cap, uint64_t* key, uint32_t* ticket,
                               hipStream_t stream);
 
+// Top-k / top-p sampling (sampler.hip).  `workspace` holds
+// sample_workspace_bytes(), zero before the first launch (each launch leaves
+// it so).  coin: device pointer to u in [0, 1), or null to hash (seed, *pos).
+// pos: null writes out[0]; else out[*pos + 1] (if below out_cap), *pos += 1.
+constexpr uint32_t kSampleMaxK = 256, kSampleMaxVocab = 262144;
+struct SampleArgs {
+    const float* logits = nullptr;
+    uint32_t n = 0;
+    float temperature = 0.0f;
+    uint32_t k = 1;
+    float top_p = 1.0f;
+    bool greedy = true;  // |temperature| < 1e-3 or top_k == 1: first index of the maximum
+    const float* coin = nullptr;
+    uint64_t seed = 0;
+    uint32_t* out = nullptr;
+    uint32_t* pos = nullptr;
+    uint32_t out_cap = 0;
+    void* workspace = nullptr;
+};
+size_t sample_workspace_bytes();
+// Checks the parameters as the reference's sampler reads them and fills n, k,
+// temperature, top_p and greedy; returns a TOYINFER_* status.
+int sample_config(uint32_t vocab, float temperature, uint32_t top_k, float top_p, SampleArgs& a);
+hipError_t launch_sample(const SampleArgs& a, hipStream_t stream);
+
 // ------------------------------------------------------------ model ops
 // rows x size RMSNorm (size even); sum_out[row] = sum of squares (nullable).
 hipError_t launch_rmsnorm_rows(const uint16_t* x, const uint16_t* w, uint16_t* y, float* sum_out,

@@ -16,8 +16,9 @@
 //    input, the residual adds are projection epilogues, the six
 //    pre-attention launches are one (decode_qkv_prologue), attention is the
 //    split-K kernel with the length read on the device, and the body ends
-//    with a device argmax that appends the next token and advances the
-//    position, so consecutive graph replays need no host work;
+//    with a device pick (argmax, or top-k/top-p sampling) that appends the
+//    next token and advances the position, so consecutive graph replays need
+//    no host work;
 //  * no memset nodes (the reference's rmsnorm clears its sum with one).
 #include <hip/hip_runtime.h>
 
@@ -41,8 +42,8 @@ struct toyinfer_qwen3 {
     uint32_t* tokens = nullptr;
     uint32_t* pos = nullptr;
     uint32_t* seq_len = nullptr;
-    uint64_t* am_key = nullptr;     // argmax key and ticket, zero between launches
-    uint32_t* am_ticket = nullptr;
+    void* sample_ws = nullptr;  // sampler / argmax workspace, zero between launches
+    SampleArgs sample;          // the pick after the lm-head (greedy by default)
     float* inv_freq = nullptr;
     float* rope = nullptr;
     float* logits = nullptr;
@@ -86,7 +87,7 @@ size_t carve(const toyinfer_qwen3_config& c, uint32_t splits, toyinfer_qwen3* m)
     const size_t kv = (size_t)c.num_kv_heads * c.head_dim, qd = (size_t)c.num_q_heads * c.head_dim;
     const size_t P = c.max_prefill_tokens, H = c.hidden_size, F = c.intermediate_size;
     const size_t o_tokens = take(4ull * c.max_seq_len);
-    const size_t o_pos = take(4), o_len = take(4), o_key = take(8), o_ticket = take(4);
+    const size_t o_pos = take(4), o_len = take(4), o_sws = take(sample_workspace_bytes());
     const size_t o_inv = take(4ull * c.head_dim / 2);
     const size_t o_rope = take(4ull * c.max_seq_len * c.head_dim);
     const size_t o_logits = take(4ull * c.vocab_size);
@@ -104,8 +105,7 @@ size_t carve(const toyinfer_qwen3_config& c, uint32_t splits, toyinfer_qwen3* m)
         m->tokens = reinterpret_cast<uint32_t*>(b + o_tokens);
         m->pos = reinterpret_cast<uint32_t*>(b + o_pos);
         m->seq_len = reinterpret_cast<uint32_t*>(b + o_len);
-        m->am_key = reinterpret_cast<uint64_t*>(b + o_key);
-        m->am_ticket = reinterpret_cast<uint32_t*>(b + o_ticket);
+        m->sample_ws = b + o_sws;
         m->inv_freq = reinterpret_cast<float*>(b + o_inv);
         m->rope = reinterpret_cast<float*>(b + o_rope);
         m->logits = reinterpret_cast<float*>(b + o_logits);
@@ -141,6 +141,17 @@ int check_config(const toyinfer_qwen3_config* c) {
     return TOYINFER_OK;
 }
 
+// The token pick after the lm-head: tokens[*pos + 1] and *pos += 1.
+hipError_t launch_pick(toyinfer_qwen3* m) {
+    SampleArgs a = m->sample;
+    a.logits = m->logits;
+    a.out = m->tokens;
+    a.pos = m->pos;
+    a.out_cap = m->cfg.max_seq_len;
+    a.workspace = m->sample_ws;
+    return launch_sample(a, m->s[0]);
+}
+
 // One decode step for the token at tokens[*pos]; ends with tokens[*pos + 1]
 // and *pos += 1.  Seven launches per layer, one stream, kernel launches only
 // (capturable):
@@ -149,7 +160,7 @@ int check_config(const toyinfer_qwen3_config* c) {
 //   q/k norm + RoPE + cache write; split-K attention + combine;
 //   o projection + residual add; RMSNorm + gate/up + SwiGLU;
 //   down projection + residual add;
-// then the final norm, the lm-head and the argmax.
+// then the final norm, the lm-head and the token pick.
 int decode_body(toyinfer_qwen3* m) {
     const toyinfer_qwen3_config& c = m->cfg;
     const uint32_t H = c.hidden_size, F = c.intermediate_size, V = c.vocab_size;
@@ -218,7 +229,7 @@ int decode_body(toyinfer_qwen3* m) {
     // flight) after a separate norm beats the fused form here.
     TRY(toyinfer_rmsnorm_bf16(m->d_hidden, m->final_norm, m->d_xn, nullptr, eps, H, s0));
     TRY(toyinfer_gemv_proj_bf162float(m->lm_head, m->d_xn, m->logits, V, H, s0));
-    TRYH(launch_argmax_wide(m->logits, V, m->tokens, m->pos, msl, m->am_key, m->am_ticket, st));
+    TRYH(launch_pick(m));
     return TOYINFER_OK;
 }
 
@@ -265,6 +276,7 @@ int toyinfer_qwen3_create(const toyinfer_qwen3_config* cfg, const void* embed_to
     m->final_norm = final_norm;
     m->lm_head = lm_head;
     m->layers.assign(layers, layers + cfg->num_layers);
+    (void)sample_config(cfg->vocab_size, 0.0f, 1, 1.0f, m->sample);
     m->splits = toyinfer_decode_default_splits(1, cfg->num_q_heads, cfg->num_kv_heads,
                                                cfg->head_dim, cfg->max_seq_len);
     const size_t bytes = carve(*cfg, m->splits, nullptr);
@@ -279,8 +291,8 @@ int toyinfer_qwen3_create(const toyinfer_qwen3_config* cfg, const void* embed_to
     if (st == TOYINFER_OK)
         st = toyinfer_rope_cos_sin_f32(m->rope, m->inv_freq, cfg->max_seq_len, cfg->head_dim,
                                        m->s[0]);
-    uint32_t* zeros[4] = {m->pos, m->am_ticket, reinterpret_cast<uint32_t*>(m->am_key),
-                          reinterpret_cast<uint32_t*>(m->am_key) + 1};
+    uint32_t* sw = static_cast<uint32_t*>(m->sample_ws);
+    uint32_t* zeros[5] = {m->pos, sw, sw + 1, sw + 2, sw + 3};
     for (uint32_t* z : zeros)
         if (st == TOYINFER_OK && launch_set_u32(z, 0, m->s[0]) != hipSuccess) st = TOYINFER_ERR_HIP;
     if (st == TOYINFER_OK && hipStreamSynchronize(m->s[0]) != hipSuccess) st = TOYINFER_ERR_HIP;
@@ -402,7 +414,7 @@ int toyinfer_qwen3_prefill(toyinfer_qwen3* m, const uint32_t* token_ids_d, uint3
                               eps, H, s0));
     TRY(toyinfer_gemv_proj_bf162float(m->lm_head, m->d_xn, m->logits, V, H, s0));
     TRYH(launch_set_u32(m->pos, T - 1, st));
-    TRYH(launch_argmax_wide(m->logits, V, m->tokens, m->pos, msl, m->am_key, m->am_ticket, st));
+    TRYH(launch_pick(m));
     return TOYINFER_OK;
 }
 
@@ -429,6 +441,26 @@ int toyinfer_qwen3_decode(toyinfer_qwen3* m, uint32_t steps, int use_graph) {
         m->graph = g;
     }
     for (uint32_t i = 0; i < steps; ++i) TRYH(hipGraphLaunch(m->exec, m->s[0]));
+    return TOYINFER_OK;
+}
+
+int toyinfer_qwen3_set_sampling(toyinfer_qwen3* m, float temperature, uint32_t top_k, float top_p,
+                                uint64_t seed) {
+    if (!m) return TOYINFER_ERR_INVALID_ARGUMENT;
+    SampleArgs a;
+    TRY(sample_config(m->cfg.vocab_size, temperature, top_k, top_p, a));
+    a.seed = seed;
+    m->sample = a;
+    // The captured step holds the old parameters: capture again on next use.
+    if (m->exec) {
+        TRYH(hipStreamSynchronize(m->s[0]));
+        (void)hipGraphExecDestroy(m->exec);
+        m->exec = nullptr;
+    }
+    if (m->graph) {
+        (void)hipGraphDestroy(m->graph);
+        m->graph = nullptr;
+    }
     return TOYINFER_OK;
 }
 

@@ -39,6 +39,8 @@ _SIGS = {
     "toyinfer_qwen3_destroy": (None, [_vp]),
     "toyinfer_qwen3_prefill": (_i32, [_vp, _vp, _u32]),
     "toyinfer_qwen3_decode": (_i32, [_vp, _u32, _i32]),
+    "toyinfer_qwen3_set_sampling": (_i32, [_vp, ctypes.c_float, _u32, ctypes.c_float,
+                                           ctypes.c_uint64]),
     "toyinfer_qwen3_synchronize": (_i32, [_vp]),
     "toyinfer_qwen3_logits": (_vp, [_vp]),
     "toyinfer_qwen3_tokens": (_vp, [_vp]),
@@ -105,6 +107,10 @@ class Qwen3:
 
     def decode(self, steps: int, graph: bool) -> None:
         attn._check("qwen3_decode", attn.LIB.toyinfer_qwen3_decode(self.h, steps, int(graph)))
+
+    def set_sampling(self, temperature: float, top_k: int, top_p: float, seed: int) -> None:
+        attn._check("qwen3_set_sampling",
+                    attn.LIB.toyinfer_qwen3_set_sampling(self.h, temperature, top_k, top_p, seed))
 
     def synchronize(self) -> None:
         attn._check("qwen3_synchronize", attn.LIB.toyinfer_qwen3_synchronize(self.h))

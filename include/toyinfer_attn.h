@@ -29,6 +29,7 @@ extern "C" {
 #define TOYINFER_ERR_UNSUPPORTED 2      /* valid in principle, not implemented (e.g. head_dim) */
 #define TOYINFER_ERR_WORKSPACE 3        /* caller workspace too small */
 #define TOYINFER_ERR_HIP 4              /* a HIP call failed; see toyinfer_last_hip_error() */
+#define TOYINFER_ERR_IO 5               /* a model file is missing, unreadable or malformed */
 
 const char* toyinfer_status_string(int status);
 /* hipError_t of the most recent TOYINFER_ERR_HIP returned on this thread. */

@@ -126,7 +126,7 @@ def test_model_config_validation():
 def test_abi_version_and_status_strings():
     assert L.toyinfer_abi_version() == 1
     assert attn.status_string(0) == "ok"
-    for st in (INVALID, UNSUPPORTED, WORKSPACE, attn.ERR_HIP):
+    for st in (INVALID, UNSUPPORTED, WORKSPACE, attn.ERR_HIP, attn.ERR_IO):
         assert attn.status_string(st) not in ("ok", "unknown status")
 
 

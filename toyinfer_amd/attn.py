@@ -24,6 +24,7 @@ ERR_INVALID_ARGUMENT = 1
 ERR_UNSUPPORTED = 2
 ERR_WORKSPACE = 3
 ERR_HIP = 4
+ERR_IO = 5
 
 # Every entry point of include/toyinfer_attn.h, with its ctypes signature.
 _vp, _u32, _u64, _f32, _i32, _sz = (ctypes.c_void_p, ctypes.c_uint32, ctypes.c_uint64,

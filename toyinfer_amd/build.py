@@ -1,7 +1,7 @@
 """Build the gfx950 attention library in-tree.
 
 ``python -m toyinfer_amd.build`` (or ``__graft_entry__.build()``) compiles
-every HIP source under ``toyinfer_amd/csrc`` with hipcc into
+every HIP and host C++ source under ``toyinfer_amd/csrc`` with hipcc into
 ``toyinfer_amd/lib/libtoyinfer_attn.so``.  Packed-FP32 VALU forms are
 disabled on purpose: some of their encodings have produced silently wrong
 results on the target machines, and the kernels do not depend on them.
@@ -41,7 +41,8 @@ def hipcc() -> str:
 
 
 def sources() -> list:
-    return sorted(glob.glob(os.path.join(CSRC, "*.hip")))
+    """HIP kernels and launchers (*.hip) plus host-only C++ (*.cpp)."""
+    return sorted(glob.glob(os.path.join(CSRC, "*.hip")) + glob.glob(os.path.join(CSRC, "*.cpp")))
 
 
 def build_synth(verbose: bool = False) -> str:

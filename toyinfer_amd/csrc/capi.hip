@@ -82,6 +82,7 @@ const char* toyinfer_status_string(int status) {
         case TOYINFER_ERR_UNSUPPORTED: return "unsupported configuration";
         case TOYINFER_ERR_WORKSPACE: return "workspace too small";
         case TOYINFER_ERR_HIP: return "HIP error";
+        case TOYINFER_ERR_IO: return "model file missing or malformed";
         default: return "unknown status";
     }
 }

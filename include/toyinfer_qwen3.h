@@ -55,6 +55,62 @@ typedef struct toyinfer_qwen3_layer {
 
 typedef struct toyinfer_qwen3 toyinfer_qwen3;
 
+/* ------------------------------------------------ checkpoint files (host)
+ * The reference reads config.json into LLMConfig (src/config.cpp:10-40) and
+ * copies the data sections of model-0000i-of-00003.safetensors into one
+ * device allocation, finding each tensor through an offset table that
+ * export.py generates for Qwen3-4B (src/qwen.cpp:17-416, 431-518).  Here the
+ * loader reads the safetensors headers themselves, so any layer count and
+ * any shard split works: the shards are the files named by
+ * model.safetensors.index.json when present, else every *.safetensors in
+ * the directory (sorted by name, as export.py:254-300 orders them). */
+
+typedef struct toyinfer_qwen3_model_info {
+    uint32_t bos_token_id;
+    uint32_t eos_token_id;
+    uint32_t max_position_embeddings;
+    int32_t tie_word_embeddings; /* 1 when config.json says so (lm_head = embed_tokens) */
+} toyinfer_qwen3_model_info;
+
+/* Fills cfg from model_dir/config.json (num_hidden_layers, hidden_size,
+ * num_attention_heads, num_key_value_heads, head_dim, intermediate_size,
+ * vocab_size, rms_norm_eps, rope_theta) with the caller's max_seq_len (0:
+ * max_position_embeddings) and max_prefill_tokens; info (may be NULL) gets
+ * the remaining fields.  TOYINFER_ERR_IO for a missing file, malformed JSON
+ * or a missing or non-numeric field. */
+int toyinfer_qwen3_read_config(const char* model_dir, uint32_t max_seq_len,
+                               uint32_t max_prefill_tokens, toyinfer_qwen3_config* cfg,
+                               toyinfer_qwen3_model_info* info);
+
+/* Weights on the device: every tensor the model reads, each at a 256-byte
+ * aligned offset of one allocation. */
+typedef struct toyinfer_qwen3_weights {
+    void* device;
+    size_t device_bytes;
+    const void* embed_tokens;
+    const void* final_norm;
+    const void* lm_head; /* lm_head.weight, or embed_tokens when tied or absent */
+    toyinfer_qwen3_layer* layers; /* num_layers entries (host memory, owned) */
+    uint32_t num_layers;
+} toyinfer_qwen3_weights;
+
+/* Host-only check of the checkpoint against cfg: every tensor present
+ * (model.embed_tokens.weight, model.norm.weight, optional lm_head.weight,
+ * and per layer model.layers.L.{input_layernorm, post_attention_layernorm,
+ * self_attn.{q,k,v,o}_proj, self_attn.{q,k}_norm, mlp.{gate,up,down}_proj}
+ * .weight), of dtype BF16, with the shape cfg implies and its bytes inside
+ * its file.  *device_bytes receives what the load allocates.  No HIP call. */
+int toyinfer_qwen3_check_weights(const char* model_dir, const toyinfer_qwen3_config* cfg,
+                                 int tie_word_embeddings, size_t* device_bytes);
+
+/* The check above, then one device allocation and the tensors streamed into
+ * it through two pinned staging buffers (up to 64 MiB each) on `stream`
+ * (waited for before returning).  On failure nothing stays allocated. */
+int toyinfer_qwen3_load_weights(const char* model_dir, const toyinfer_qwen3_config* cfg,
+                                int tie_word_embeddings, void* stream,
+                                toyinfer_qwen3_weights* out);
+void toyinfer_qwen3_free_weights(toyinfer_qwen3_weights* w);
+
 /* Device bytes create() allocates for this configuration. */
 size_t toyinfer_qwen3_state_bytes(const toyinfer_qwen3_config* cfg);
 

@@ -86,7 +86,7 @@ def test_model_header_functions_exported_and_bound():
     text = re.sub(r"/\*.*?\*/", "", open(os.path.join(ROOT, "include", "toyinfer_qwen3.h")).read(),
                   flags=re.S)
     names = set(re.findall(r"\b(toyinfer_\w+)\s*\(", text))
-    assert len(names) == 11
+    assert len(names) == 15
     out = subprocess.run(["nm", "-D", "--defined-only", attn.LIB_PATH], capture_output=True,
                          text=True, check=True).stdout
     assert names <= set(re.findall(r"\bT (toyinfer_\w+)", out))

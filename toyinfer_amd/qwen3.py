@@ -32,7 +32,25 @@ class Layer(ctypes.Structure):
     _fields_ = [(n, _vp) for n in LAYER_FIELDS]
 
 
+class ModelInfo(ctypes.Structure):
+    _fields_ = [("bos_token_id", _u32), ("eos_token_id", _u32),
+                ("max_position_embeddings", _u32), ("tie_word_embeddings", ctypes.c_int32)]
+
+
+class Weights(ctypes.Structure):
+    _fields_ = [("device", _vp), ("device_bytes", _sz), ("embed_tokens", _vp),
+                ("final_norm", _vp), ("lm_head", _vp), ("layers", ctypes.POINTER(Layer)),
+                ("num_layers", _u32)]
+
+
 _SIGS = {
+    "toyinfer_qwen3_read_config": (_i32, [ctypes.c_char_p, _u32, _u32, ctypes.POINTER(Config),
+                                          ctypes.POINTER(ModelInfo)]),
+    "toyinfer_qwen3_check_weights": (_i32, [ctypes.c_char_p, ctypes.POINTER(Config), _i32,
+                                            ctypes.POINTER(_sz)]),
+    "toyinfer_qwen3_load_weights": (_i32, [ctypes.c_char_p, ctypes.POINTER(Config), _i32, _vp,
+                                           ctypes.POINTER(Weights)]),
+    "toyinfer_qwen3_free_weights": (None, [ctypes.POINTER(Weights)]),
     "toyinfer_qwen3_state_bytes": (_sz, [ctypes.POINTER(Config)]),
     "toyinfer_qwen3_create": (_i32, [ctypes.POINTER(Config), _vp, _vp, _vp, ctypes.POINTER(Layer),
                                      ctypes.POINTER(_vp)]),
@@ -69,6 +87,59 @@ def make_config(**kw) -> Config:
     return Config(**kw)
 
 
+def read_config(model_dir: str, max_seq_len: int = 0, max_prefill_tokens: int = 4096):
+    """(Config, ModelInfo) from model_dir/config.json (src/config.cpp:10-40)."""
+    cfg, info = Config(), ModelInfo()
+    attn._check("qwen3_read_config", attn.LIB.toyinfer_qwen3_read_config(
+        model_dir.encode(), max_seq_len, max_prefill_tokens, ctypes.byref(cfg), ctypes.byref(info)))
+    return cfg, info
+
+
+def check_weights(model_dir: str, cfg: Config, tie: bool) -> int:
+    """Device bytes the load needs; raises if the checkpoint does not match cfg."""
+    n = _sz()
+    attn._check("qwen3_check_weights", attn.LIB.toyinfer_qwen3_check_weights(
+        model_dir.encode(), ctypes.byref(cfg), int(tie), ctypes.byref(n)))
+    return n.value
+
+
+class _Addr:
+    """A device address standing in for a tensor (data_ptr only)."""
+
+    def __init__(self, p: int):
+        self.p = int(p)
+
+    def data_ptr(self) -> int:
+        return self.p
+
+
+class LoadedWeights:
+    """Checkpoint weights uploaded by toyinfer_qwen3_load_weights; the dict
+    form (`as_dict`) is what Qwen3 takes."""
+
+    def __init__(self, model_dir: str, cfg: Config, tie: bool, stream=None):
+        self.w = Weights()
+        attn._check("qwen3_load_weights", attn.LIB.toyinfer_qwen3_load_weights(
+            model_dir.encode(), ctypes.byref(cfg), int(tie), stream, ctypes.byref(self.w)))
+
+    def as_dict(self) -> Dict:
+        w = self.w
+        layers = [{n: _Addr(getattr(w.layers[i], n)) for n in LAYER_FIELDS}
+                  for i in range(w.num_layers)]
+        return {"embed_tokens": _Addr(w.embed_tokens), "norm": _Addr(w.final_norm),
+                "lm_head": _Addr(w.lm_head), "layers": layers, "_owner": self}
+
+    def close(self) -> None:
+        if self.w.device:
+            attn.LIB.toyinfer_qwen3_free_weights(ctypes.byref(self.w))
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
 class Qwen3:
     """weights: dict with embed_tokens, norm, lm_head (may be embed_tokens) and
     layers: a list of dicts keyed by LAYER_FIELDS; all bf16 CUDA tensors."""
@@ -86,6 +157,17 @@ class Qwen3:
             ctypes.byref(cfg), weights["embed_tokens"].data_ptr(), weights["norm"].data_ptr(),
             weights["lm_head"].data_ptr(), layers, ctypes.byref(handle)))
         self.h = handle
+
+    @classmethod
+    def from_pretrained(cls, model_dir: str, max_seq_len: int = 0,
+                        max_prefill_tokens: int = 4096) -> "Qwen3":
+        """config.json + safetensors shards of model_dir (the reference's
+        LLMConfig and Qwen3::load_weights, src/config.cpp, src/qwen.cpp)."""
+        cfg, info = read_config(model_dir, max_seq_len, max_prefill_tokens)
+        weights = LoadedWeights(model_dir, cfg, bool(info.tie_word_embeddings))
+        m = cls(cfg, weights.as_dict())
+        m.info = info
+        return m
 
     def close(self):
         if self.h:

@@ -19,8 +19,10 @@ the north-star targets name, each with its own roofline block:
     reference-contract graph decode;
   * proj_gemv / proj_gemm: the projections either side of attention (lm-head
     GEMV, HBM-bound; a 4096-token prefill projection, MFMA-bound);
+  * sample: the device top-k/top-p pick over a 151936-entry vocabulary;
   * qwen3_e2e: configs[4], random-init Qwen3-0.6B, TTFT of a 1371-token
-    prompt and greedy decode tokens/s from a captured hipGraph.
+    prompt and greedy decode tokens/s from a captured hipGraph (and the
+    same with the reference's default sampling settings).
 Decode steps rotate over 4 independent KV sets (512 MiB) so every step reads
 KV that is not resident in the 256 MB Infinity Cache.
 
@@ -63,7 +65,7 @@ def traffic_bytes(workload):
     return int(round((r * FETCH_SCALE + w * WRITE_SCALE) * 1024))
 WORKLOADS = ("all", "prefill", "prefill_fused", "decode_b8_l4096", "decode_b1_l32768",
              "decode_step", "decode_contract", "proj_gemv", "proj_gemm", "qwen3_e2e",
-             "copy_calibration")
+             "sample", "copy_calibration")
 
 
 def causal_flops(s, hq, d):
@@ -383,6 +385,16 @@ def bench_qwen3_e2e(dev, prompt_len=1371, decode_steps=256, reps=3):
     ev[1].record(ms_stream)
     m.synchronize()
     direct.append(ev[0].elapsed_time(ev[1]) / 32)
+    # The reference's default sampler settings, sampled on the device in the graph.
+    m.set_sampling(0.6, 20, 0.95, SEED)
+    sampled = []
+    for _ in range(reps):
+        m.prefill(ids, prompt_len)
+        ev[0].record(ms_stream)
+        m.decode(decode_steps, True)
+        ev[1].record(ms_stream)
+        m.synchronize()
+        sampled.append(ev[0].elapsed_time(ev[1]) / decode_steps)
     m.close()
     ms_tok = min(dec) / decode_steps
     return {"workload": f"qwen3_0.6b_e2e_prompt{prompt_len}_decode{decode_steps}",
@@ -390,8 +402,40 @@ def bench_qwen3_e2e(dev, prompt_len=1371, decode_steps=256, reps=3):
             "ttft_ms": round(min(ttft), 3), "decode_ms_per_token": round(ms_tok, 4),
             "value": round(1e3 / ms_tok, 1), "unit": "decode tokens/s",
             "direct_launch_ms_per_token": round(direct[0], 4),
+            "sampled_decode_ms_per_token": round(min(sampled), 4),
             "note": "random-init weights N(0, 0.02) bf16 (synthetic), tied embeddings; "
                     "TTFT includes the lm-head and the device greedy pick"}
+
+
+def bench_sample(dev, stream, steps, warmup, V=151936, T=0.6, top_k=20, top_p=0.95):
+    """The token pick after the lm-head with the reference's default sampler
+    settings (src/options.cpp:32-34): top-k/top-p sampling on the device
+    (toyinfer_sample_topk_topp_f32) over fp32 logits N(0, 3^2) of Qwen3's
+    vocabulary; the greedy pick (toyinfer_argmax_f32's wide form, same entry
+    at temperature 0) timed beside it.  Launch-latency bound: the roofline
+    prices the 0.6 MB logits read."""
+    import torch
+
+    from toyinfer_amd import attn
+
+    g = torch.Generator(device=dev).manual_seed(SEED + 60)
+    logits = torch.randn((V,), generator=g, device=dev) * 3.0
+    coin = torch.full((1,), 0.37, dtype=torch.float32, device=dev)
+    out = torch.zeros(1, dtype=torch.int32, device=dev)
+    ws = torch.zeros(attn.sample_workspace_bytes(), dtype=torch.uint8, device=dev)
+    torch.cuda.synchronize()
+    ms = time_steps(lambda i: attn.sample_topk_topp_f32(logits, V, T, top_k, top_p, coin, out, ws,
+                                                        stream), steps, warmup, stream)
+    ms_greedy = time_steps(lambda i: attn.sample_topk_topp_f32(logits, V, 0.0, top_k, top_p, coin,
+                                                               out, ws, stream), steps, warmup,
+                           stream)
+    gbs = 4.0 * V / (ms * 1e-3) / 1e9
+    return {"workload": f"sample_topk{top_k}_topp{top_p}_t{T}_v{V}",
+            "entry": "toyinfer_sample_topk_topp_f32", "steps": steps,
+            "us_per_call": round(ms * 1e3, 2), "greedy_us_per_call": round(ms_greedy * 1e3, 2),
+            "value": round(gbs, 1), "unit": "GB/s",
+            "note": "logits read per call / call time; launch-latency bound at this size",
+            "roofline": roofline("hbm", gbs, PEAK_HBM_GBS, "GB/s")}
 
 
 def bench_copy(dev, stream, steps, warmup, mib=256):
@@ -467,6 +511,7 @@ def main():
                "proj_gemv": lambda: bench_proj_gemv(dev, stream, args.steps, args.warmup),
                "proj_gemm": lambda: bench_proj_gemm(dev, stream, args.steps, args.warmup),
                "qwen3_e2e": lambda: bench_qwen3_e2e(dev),
+               "sample": lambda: bench_sample(dev, stream, args.steps, args.warmup),
                "copy_calibration": lambda: bench_copy(dev, stream, args.steps, args.warmup)}
         print(json.dumps(one[args.workload]()), flush=True)
         return
@@ -492,6 +537,7 @@ def main():
         comps.append(bench_decode_contract(dev, stream, max(50, args.steps * 2), 2))
         comps.append(bench_proj_gemv(dev, stream, max(50, args.steps), 10))
         comps.append(bench_proj_gemm(dev, stream, max(200, args.steps), 50))
+        comps.append(bench_sample(dev, stream, max(200, args.steps), 50))
         comps.append(bench_qwen3_e2e(dev))
         line["components"] = comps
     if not args.no_cpu:

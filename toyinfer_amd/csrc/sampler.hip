@@ -16,13 +16,15 @@
 // draws a fresh coin per step without host work.
 //
 // Layout: 32 workgroups of 256 threads.  Workgroup b takes the contiguous
-// chunk b of the logits (at most 8192), finds its local k-th largest key by an
-// LDS radix select (four 8-bit digit passes), and writes its top k (keys and
-// indices) to the workspace in index order.  The last workgroup to finish (an
-// agent-scope ticket) runs the same select over the 32*k candidates, sorts
-// the k survivors (bitonic, in LDS), and does the softmax, the top-p cut and
-// the coin walk with block scans.  Ties at the k-th value keep the lowest
-// indices; equal values are ordered by index.
+// chunk b of the logits (at most 8192, held in registers: element j*256 + t
+// in thread t's j-th slot), finds its local k-th largest key by a radix
+// select (four 8-bit digit passes over per-wave LDS histograms), and writes
+// its top k (keys and indices) to the workspace.  The last workgroup to
+// finish (an agent-scope ticket) runs the same select over the 32*k
+// candidates, sorts the k survivors (in one wave's registers for k <= 64,
+// in LDS above), and does the softmax, the top-p cut and the coin walk with
+// lane or block scans.  Ties at the k-th value keep the lowest indices;
+// equal values are ordered by index.
 #include <hip/hip_runtime.h>
 
 #include "../../include/toyinfer_attn.h"
@@ -32,10 +34,11 @@
 namespace tiattn {
 namespace {
 
-constexpr int kSpBlocks = 32, kSpThreads = 256;
+constexpr int kSpBlocks = 32, kSpThreads = 256, kSpWaves = kSpThreads / 64;
 constexpr uint32_t kSpChunk = kSampleMaxVocab / kSpBlocks;
+constexpr int kSpPer = kSpChunk / kSpThreads;  // keys per thread, held in registers
 static_assert(kSampleMaxK <= kSpThreads, "one thread per kept candidate");
-static_assert(kSpBlocks * kSampleMaxK <= kSpChunk, "candidates reuse the chunk buffer");
+static_assert(kSpBlocks * kSampleMaxK <= kSpChunk, "candidates fit the per-thread key slots");
 
 // Workspace: [0, 8) argmax key, [8, 12) argmax ticket, [12, 16) sampler
 // ticket, then keys [32][k] and indices [32][k] from byte 256.
@@ -65,7 +68,7 @@ __device__ __forceinline__ T block_scan_excl(T v, T* s_w, T& total) {
     T base = 0;
     total = 0;
 #pragma unroll
-    for (int i = 0; i < kSpThreads / 64; ++i) {
+    for (int i = 0; i < kSpWaves; ++i) {
         if (i < w) base += s_w[i];
         total += s_w[i];
     }
@@ -73,80 +76,136 @@ __device__ __forceinline__ T block_scan_excl(T v, T* s_w, T& total) {
     return base + x - v;
 }
 
-// The k-th largest of s_key[0..m) (1 <= k <= m): its key, and how many of
-// the elements equal to it belong to the top k (the rest of the top k is
-// strictly larger).
-__device__ void radix_select(const uint32_t* s_key, uint32_t m, uint32_t k, uint32_t* s_hist,
-                             uint32_t* s_sel, uint32_t& thr, uint32_t& need) {
-    uint32_t prefix = 0, mask = 0;
-    need = k;
-    for (int shift = 24; shift >= 0; shift -= 8) {
-        s_hist[threadIdx.x] = 0;
-        __syncthreads();
-        for (uint32_t i = threadIdx.x; i < m; i += kSpThreads) {
-            const uint32_t key = s_key[i];
-            if ((key & mask) == prefix) atomicAdd(&s_hist[(key >> shift) & 255u], 1u);
-        }
-        __syncthreads();
-        if (threadIdx.x < 64) {
-            // Lane l holds digits 4l..4l+3; `above` counts the elements with a
-            // larger digit.  Exactly one digit has above < need <= above + h.
-            const int l = threadIdx.x;
-            uint32_t h[4];
-#pragma unroll
-            for (int j = 0; j < 4; ++j) h[j] = s_hist[4 * l + j];
-            const uint32_t t = h[0] + h[1] + h[2] + h[3];
-            uint32_t suf = t;
-#pragma unroll
-            for (int o = 1; o < 64; o <<= 1) {
-                const uint32_t y = __shfl_down(suf, o);
-                if (l + o < 64) suf += y;
-            }
-            uint32_t above = suf - t;
-#pragma unroll
-            for (int j = 3; j >= 0; --j) {
-                if (above < need && need <= above + h[j]) {
-                    s_sel[0] = 4 * l + j;
-                    s_sel[1] = need - above;
-                }
-                above += h[j];
-            }
-        }
-        __syncthreads();
-        prefix |= s_sel[0] << shift;
-        mask |= 255u << shift;
-        need = s_sel[1];
-        __syncthreads();
-    }
-    thr = prefix;
+// Inclusive prefix sum over the 64 lanes of a wave with DPP row shifts and
+// row broadcasts (no LDS round trips): within each row of 16 lanes by
+// shifts of 1, 2, 3, then 4 and 8 on the upper banks; then row 1 and 3 take
+// lane 15 of the row before, rows 2 and 3 lane 31.
+__device__ __forceinline__ uint32_t wave_scan_incl(uint32_t v) {
+    uint32_t s = v;
+    s += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x111, 0xf, 0xf, true);
+    s += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x112, 0xf, 0xf, true);
+    s += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x113, 0xf, 0xf, true);
+    s += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)s, 0x114, 0xf, 0xe, true);
+    s += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)s, 0x118, 0xf, 0xc, true);
+    s += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)s, 0x142, 0xa, 0xf, true);
+    s += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)s, 0x143, 0xc, 0xf, true);
+    return s;
+}
+template <int CTRL, int ROWS, int BANKS>
+__device__ __forceinline__ float dpp_f(float x) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, ROWS, BANKS, true));
+}
+__device__ __forceinline__ float wave_scan_incl(float v) {
+    float s = v + dpp_f<0x111, 0xf, 0xf>(v);
+    s += dpp_f<0x112, 0xf, 0xf>(v);
+    s += dpp_f<0x113, 0xf, 0xf>(v);
+    s += dpp_f<0x114, 0xf, 0xe>(s);
+    s += dpp_f<0x118, 0xf, 0xc>(s);
+    s += dpp_f<0x142, 0xa, 0xf>(s);
+    s += dpp_f<0x143, 0xc, 0xf>(s);
+    return s;
+}
+// The value of lane l - 1 (0 for lane 0): DPP wave_shr:1.
+__device__ __forceinline__ float lane_before(float x) { return dpp_f<0x138, 0xf, 0xf>(x); }
+__device__ __forceinline__ uint32_t read_lane(uint32_t x, int l) {
+    return (uint32_t)__builtin_amdgcn_readlane((int)x, l);
 }
 
-// Calls emit(slot, i) for the top k of s_key[0..m) given the select's result:
-// slots [0, k-need) take the larger keys in index order, slots [k-need, k)
-// the first `need` keys equal to thr in index order.
-template <typename F>
-__device__ void compact_top(const uint32_t* s_key, uint32_t m, uint32_t k, uint32_t thr,
-                            uint32_t need, uint32_t* s_w, F&& emit) {
-    const uint32_t per = (m + kSpThreads - 1) / kSpThreads;
-    const uint32_t b = min(m, threadIdx.x * per), e = min(m, b + per);
-    uint32_t ngt = 0, neq = 0;
-    for (uint32_t i = b; i < e; ++i) {
-        const uint32_t key = s_key[i];
-        ngt += key > thr;
-        neq += key == thr;
-    }
-    uint32_t tot;
-    uint32_t gt = block_scan_excl(ngt, s_w, tot);
-    uint32_t eq = block_scan_excl(neq, s_w, tot);
-    for (uint32_t i = b; i < e; ++i) {
-        const uint32_t key = s_key[i];
-        if (key > thr) {
-            emit(gt++, i);
-        } else if (key == thr) {
-            if (eq < need) emit(k - need + eq, i);
-            ++eq;
+struct Sel {
+    uint32_t thr;   // the k-th largest key
+    uint32_t need;  // how many keys equal to thr belong to the top k
+    uint32_t eq;    // how many keys equal thr
+};
+
+// The k-th largest of the valid keys of the workgroup (1 <= k <= their
+// number): thread t holds element j*256 + t in key[j], valid where bit j of
+// `valid` is set.  Four 8-bit digit passes; each wave counts into its own
+// histogram (two sets, alternating by pass, so one barrier per pass
+// suffices), and every wave then finds the digit itself from the four
+// histograms with a lane scan, so no result needs broadcasting.
+__device__ __forceinline__ Sel select_kth(const uint32_t (&key)[kSpPer], uint32_t valid, uint32_t k,
+                          uint32_t* s_hist) {
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    uint32_t prefix = 0, mask = 0, need = k, eq = 0;
+#pragma unroll
+    for (int pass = 0; pass < 4; ++pass) {
+        const int shift = 24 - 8 * pass;
+        uint32_t* set = s_hist + (pass & 1) * kSpWaves * 256;
+        uint32_t* own = set + w * 256;
+        *reinterpret_cast<uint4*>(own + 4 * lane) = make_uint4(0u, 0u, 0u, 0u);
+#pragma unroll
+        for (int j = 0; j < kSpPer; ++j)
+            if ((valid >> j & 1u) && (key[j] & mask) == prefix)
+                atomicAdd(&own[(key[j] >> shift) & 255u], 1u);
+        __syncthreads();
+        // Lane l: digits 255-4l down to 252-4l, so that the larger digits sit
+        // in the lower lanes.  `above` counts larger digits; exactly one digit
+        // has above < need <= above + count.
+        uint32_t h[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+        for (int ww = 0; ww < kSpWaves; ++ww) {
+            const uint4 v = *reinterpret_cast<const uint4*>(set + ww * 256 + 252 - 4 * lane);
+            h[0] += v.w;
+            h[1] += v.z;
+            h[2] += v.y;
+            h[3] += v.x;
         }
+        const uint32_t t = h[0] + h[1] + h[2] + h[3];
+        uint32_t above = wave_scan_incl(t) - t;
+        int found = -1;
+        uint32_t f_need = 0, f_cnt = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            if (above < need && need <= above + h[i]) {
+                found = 255 - 4 * lane - i;
+                f_need = need - above;
+                f_cnt = h[i];
+            }
+            above += h[i];
+        }
+        const int src = __builtin_ctzll(__ballot(found >= 0));
+        prefix |= read_lane((uint32_t)found, src) << shift;
+        mask |= 255u << shift;
+        need = read_lane(f_need, src);
+        eq = read_lane(f_cnt, src);
     }
+    return {prefix, need, eq};
+}
+
+// Bit j set: element j*256 + t is one of the top k.  Keys above thr all are;
+// of the keys equal to thr, the `need` with the smallest indices (a second
+// select over the complemented indices when there are more).
+__device__ __forceinline__ uint32_t top_mask(const uint32_t (&key)[kSpPer], const uint32_t (&idx)[kSpPer],
+                             uint32_t valid, const Sel& s, uint32_t* s_hist) {
+    uint32_t take = 0, tie = 0;
+    uint32_t nidx[kSpPer];
+#pragma unroll
+    for (int j = 0; j < kSpPer; ++j) {
+        const bool v = valid >> j & 1u;
+        take |= (uint32_t)(v && key[j] > s.thr) << j;
+        tie |= (uint32_t)(v && key[j] == s.thr) << j;
+        nidx[j] = ~idx[j];
+    }
+    if (s.eq == s.need) return take | tie;  // uniform over the workgroup
+    const Sel t = select_kth(nidx, tie, s.need, s_hist);
+#pragma unroll
+    for (int j = 0; j < kSpPer; ++j) take |= (uint32_t)((tie >> j & 1u) && nidx[j] >= t.thr) << j;
+    return take;
+}
+
+// Slots 0..k-1 for the set bits of `take` across the workgroup (any order):
+// a wave scan of the per-thread counts and one LDS atomic per wave.
+template <typename F>
+__device__ __forceinline__ void emit_top(uint32_t take, uint32_t k, uint32_t* s_cnt, F&& emit) {
+    const int lane = threadIdx.x & 63;
+    const uint32_t n = __popc(take);
+    const uint32_t incl = wave_scan_incl(n);
+    uint32_t base = 0;
+    if (lane == 63) base = atomicAdd(s_cnt, incl);
+    uint32_t slot = read_lane(base, 63) + incl - n;
+#pragma unroll
+    for (int j = 0; j < kSpPer; ++j)
+        if ((take >> j & 1u) && slot < k) emit(slot++, j);  // exactly k bits are set
 }
 
 // SplitMix64 finaliser (Steele, Lea and Flood, "Fast splittable pseudorandom
@@ -160,15 +219,25 @@ __device__ __forceinline__ float sp_coin(uint64_t seed, uint32_t pos) {
     return (float)(uint32_t)(z >> 40) * 0x1p-24f;
 }
 
+// Writes the picked token (and advances the position) from thread 0.
+__device__ __forceinline__ void sp_write(const SampleArgs& a, uint32_t p_out, uint32_t idx,
+                                         uint32_t* ticket) {
+    *ticket = 0;
+    if (a.pos) {
+        if (p_out + 1 < a.out_cap) a.out[p_out + 1] = idx;
+        *a.pos = p_out + 1;
+    } else {
+        a.out[0] = idx;
+    }
+}
+
 __global__ __launch_bounds__(kSpThreads) void sample_kernel(SampleArgs a) {
-    __shared__ uint32_t s_key[kSpChunk];
-    __shared__ uint32_t s_hist[256];
-    __shared__ uint32_t s_sel[2];
-    __shared__ uint32_t s_wu[kSpThreads / 64];
-    __shared__ float s_wf[kSpThreads / 64];
+    __shared__ __align__(16) uint32_t s_hist[2 * kSpWaves * 256];
+    __shared__ uint32_t s_wu[kSpWaves];
+    __shared__ float s_wf[kSpWaves];
     __shared__ uint64_t s_top[kSampleMaxK];
     __shared__ float s_acc[kSampleMaxK];
-    __shared__ uint32_t s_res[2];
+    __shared__ uint32_t s_res[2], s_cnt;
     __shared__ bool s_last;
 
     const uint32_t k = a.k, tid = threadIdx.x;
@@ -176,50 +245,122 @@ __global__ __launch_bounds__(kSpThreads) void sample_kernel(SampleArgs a) {
     uint32_t* ticket = reinterpret_cast<uint32_t*>(ws + 12);
     uint32_t* ws_key = reinterpret_cast<uint32_t*>(ws + kSpCandOff);
     uint32_t* ws_idx = ws_key + kSpBlocks * k;
+    if (tid == 0) s_cnt = 0;
 
-    // Phase 1: this workgroup's chunk.
+    // Phase 1: this workgroup's chunk, element j*256 + t in thread t's key[j].
     const uint32_t cs = (a.n + kSpBlocks - 1) / kSpBlocks;
     const uint32_t c0 = min(a.n, blockIdx.x * cs), m = min(a.n, c0 + cs) - c0;
-    for (uint32_t i = tid; i < m; i += kSpThreads) s_key[i] = sp_key(a.logits[c0 + i] / a.temperature);
-    __syncthreads();
+    uint32_t key[kSpPer], idx[kSpPer], valid = 0;
+    {
+        // Range-checked buffer loads: no branch per slot, zeros past the chunk.
+        const __amdgpu_buffer_rsrc_t r = make_rsrc(a.logits + c0, m * 4);
+        float x[kSpPer];
+#pragma unroll
+        for (int j = 0; j < kSpPer; ++j)
+            x[j] = __uint_as_float((uint32_t)__builtin_amdgcn_raw_buffer_load_b32(
+                r, 4 * (j * kSpThreads + tid), 0, 0));
+#pragma unroll
+        for (int j = 0; j < kSpPer; ++j) {
+            const uint32_t e = j * kSpThreads + tid;
+            key[j] = sp_key(x[j] / a.temperature);
+            idx[j] = c0 + e;
+            valid |= (uint32_t)(e < m) << j;
+        }
+    }
     uint32_t* bk = ws_key + blockIdx.x * k;
     uint32_t* bi = ws_idx + blockIdx.x * k;
     if (m <= k) {
         // The whole chunk; key 0 pads (below every key of a non-NaN float).
-        for (uint32_t i = tid; i < k; i += kSpThreads) {
-            bk[i] = i < m ? s_key[i] : 0u;
-            bi[i] = i < m ? c0 + i : 0xffffffffu;
+#pragma unroll
+        for (int j = 0; j < kSpPer; ++j) {
+            const uint32_t e = j * kSpThreads + tid;
+            if (e < k) {
+                bk[e] = e < m ? key[j] : 0u;
+                bi[e] = e < m ? idx[j] : 0xffffffffu;
+            }
         }
     } else {
-        uint32_t thr, need;
-        radix_select(s_key, m, k, s_hist, s_sel, thr, need);
-        compact_top(s_key, m, k, thr, need, s_wu, [&](uint32_t slot, uint32_t i) {
-            bk[slot] = s_key[i];
-            bi[slot] = c0 + i;
+        const Sel s = select_kth(key, valid, k, s_hist);
+        const uint32_t take = top_mask(key, idx, valid, s, s_hist);
+        emit_top(take, k, &s_cnt, [&](uint32_t slot, int j) {
+            bk[slot] = key[j];
+            bi[slot] = idx[j];
         });
     }
-    __threadfence();
+    // Every wave waits for its own stores to reach the L2, the barrier joins
+    // them, and one agent-scope release (not one per wave) publishes the
+    // chunk before the ticket; the last workgroup's acquire precedes its reads
+    // of the other chunks.
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
-    if (tid == 0) s_last = atomicAdd(ticket, 1u) == kSpBlocks - 1;
+    if (tid == 0) {
+        __threadfence();
+        s_last = atomicAdd(ticket, 1u) == kSpBlocks - 1;
+        if (s_last) __threadfence();
+        s_cnt = 0;
+    }
     __syncthreads();
     if (!s_last) return;
-    __threadfence();
 
-    // Phase 2 (last workgroup): the top k of the 32*k candidates.  Within a
-    // block's slots, equal keys sit in index order and blocks ascend, so
-    // slot order is index order among equal keys.
+    // Phase 2 (last workgroup): the top k of the 32*k candidates, as
+    // (key << 32 | ~index) so that one ordering covers the ties.
     const uint32_t nc = kSpBlocks * k;
-    for (uint32_t i = tid; i < nc; i += kSpThreads) s_key[i] = ws_key[i];
-    if (tid < kSampleMaxK) s_top[tid] = 0;
-    __syncthreads();
+    valid = 0;
+#pragma unroll
+    for (int j = 0; j < kSpPer; ++j) {
+        const uint32_t e = j * kSpThreads + tid;
+        const bool v = e < nc;
+        key[j] = v ? ws_key[e] : 0u;
+        idx[j] = v ? ws_idx[e] : 0xffffffffu;
+        valid |= (uint32_t)v << j;
+    }
     {
-        uint32_t thr, need;
-        radix_select(s_key, nc, k, s_hist, s_sel, thr, need);
-        compact_top(s_key, nc, k, thr, need, s_wu, [&](uint32_t slot, uint32_t i) {
-            s_top[slot] = ((uint64_t)s_key[i] << 32) | (uint32_t)~ws_idx[i];
+        const Sel s = select_kth(key, valid, k, s_hist);
+        const uint32_t take = top_mask(key, idx, valid, s, s_hist);
+        emit_top(take, k, &s_cnt, [&](uint32_t slot, int j) {
+            s_top[slot] = ((uint64_t)key[j] << 32) | (uint32_t)~idx[j];
         });
     }
-    // Bitonic sort, descending: larger key first, then smaller index.
+    uint32_t p_out = 0;
+    if (a.pos) p_out = *a.pos;
+    const float u = a.coin ? *a.coin : sp_coin(a.seed, p_out);
+    __syncthreads();
+
+    if (k <= 64) {
+        // One wave: bitonic sort in registers (descending), then softmax,
+        // running sums, the top-p cut and the coin walk with lane scans.
+        if (tid >= 64) return;
+        const int lane = tid;
+        uint64_t v = (uint32_t)lane < k ? s_top[lane] : 0ull;
+#pragma unroll
+        for (int size = 2; size <= 64; size <<= 1) {
+#pragma unroll
+            for (int stride = size >> 1; stride > 0; stride >>= 1) {
+                const uint64_t o = __shfl_xor(v, stride);
+                const bool keep_max = ((lane & stride) == 0) == ((lane & size) == 0);
+                v = keep_max ? (v > o ? v : o) : (v < o ? v : o);
+            }
+        }
+        const bool in = (uint32_t)lane < k;
+        const float x = sp_val((uint32_t)(v >> 32));
+        const float xmax = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(x)));
+        const float p = in ? expf((x - xmax) / a.temperature) : 0.0f;
+        const float sum = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wave_scan_incl(p)), 63));
+        const float acc = wave_scan_incl(p / sum);
+        const float prev = lane_before(acc);
+        const uint64_t cut = __ballot(in && acc > a.top_p && (lane == 0 || !(prev > a.top_p)));
+        const uint32_t kept = cut ? (uint32_t)__builtin_ctzll(cut) + 1 : k;
+        const float coin = u * __int_as_float(__builtin_amdgcn_readlane(__float_as_int(acc), kept - 1));
+        const uint64_t hit = __ballot((uint32_t)lane < kept && acc > coin &&
+                                      (lane == 0 || !(prev > coin)));
+        const int pick = hit ? __builtin_ctzll(hit) : (int)kept - 1;
+        const uint64_t chosen = __shfl(v, pick);
+        if (lane == 0) sp_write(a, p_out, ~(uint32_t)chosen, ticket);
+        return;
+    }
+
+    // k > 64: bitonic sort in LDS over the workgroup, block scans.
+    if (tid >= k && tid < kSampleMaxK) s_top[tid] = 0;
     uint32_t n2 = 1;
     while (n2 < k) n2 <<= 1;
     for (uint32_t size = 2; size <= n2; size <<= 1) {
@@ -237,8 +378,6 @@ __global__ __launch_bounds__(kSpThreads) void sample_kernel(SampleArgs a) {
         }
     }
     __syncthreads();
-
-    // Softmax over the sorted top k (the first is the largest), running sums.
     const float xmax = sp_val((uint32_t)(s_top[0] >> 32));
     const float p = tid < k ? expf((sp_val((uint32_t)(s_top[tid] >> 32)) - xmax) / a.temperature) : 0.0f;
     float sum;
@@ -256,22 +395,12 @@ __global__ __launch_bounds__(kSpThreads) void sample_kernel(SampleArgs a) {
     if (tid < k && acc > a.top_p && (tid == 0 || !(s_acc[tid - 1] > a.top_p))) s_res[0] = tid + 1;
     __syncthreads();
     const uint32_t kept = s_res[0];
-    uint32_t p_out = 0;
-    if (a.pos) p_out = *a.pos;
-    const float u = a.coin ? *a.coin : sp_coin(a.seed, p_out);
     const float coin = u * s_acc[kept - 1];
     if (tid < kept && acc > coin && (tid == 0 || !(s_acc[tid - 1] > coin))) s_res[1] = tid;
     __syncthreads();
     if (tid == 0) {
         const uint32_t pick = s_res[1] != 0xffffffffu ? s_res[1] : kept - 1;
-        const uint32_t idx = ~(uint32_t)s_top[pick];
-        *ticket = 0;
-        if (a.pos) {
-            if (p_out + 1 < a.out_cap) a.out[p_out + 1] = idx;
-            *a.pos = p_out + 1;
-        } else {
-            a.out[0] = idx;
-        }
+        sp_write(a, p_out, ~(uint32_t)s_top[pick], ticket);
     }
 }
 

@@ -124,7 +124,7 @@ struct Sel {
 // suffices), and every wave then finds the digit itself from the four
 // histograms with a lane scan, so no result needs broadcasting.
 __device__ __forceinline__ Sel select_kth(const uint32_t (&key)[kSpPer], uint32_t valid, uint32_t k,
-                          uint32_t* s_hist) {
+                          uint32_t* s_hist, int slots) {
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     uint32_t prefix = 0, mask = 0, need = k, eq = 0;
 #pragma unroll
@@ -134,9 +134,11 @@ __device__ __forceinline__ Sel select_kth(const uint32_t (&key)[kSpPer], uint32_
         uint32_t* own = set + w * 256;
         *reinterpret_cast<uint4*>(own + 4 * lane) = make_uint4(0u, 0u, 0u, 0u);
 #pragma unroll
-        for (int j = 0; j < kSpPer; ++j)
+        for (int j = 0; j < kSpPer; ++j) {
+            if (j >= slots) break;  // workgroup-uniform: slots past the last key are skipped
             if ((valid >> j & 1u) && (key[j] & mask) == prefix)
                 atomicAdd(&own[(key[j] >> shift) & 255u], 1u);
+        }
         __syncthreads();
         // Lane l: digits 255-4l down to 252-4l, so that the larger digits sit
         // in the lower lanes.  `above` counts larger digits; exactly one digit
@@ -176,18 +178,20 @@ __device__ __forceinline__ Sel select_kth(const uint32_t (&key)[kSpPer], uint32_
 // of the keys equal to thr, the `need` with the smallest indices (a second
 // select over the complemented indices when there are more).
 __device__ __forceinline__ uint32_t top_mask(const uint32_t (&key)[kSpPer], const uint32_t (&idx)[kSpPer],
-                             uint32_t valid, const Sel& s, uint32_t* s_hist) {
+                             uint32_t valid, const Sel& s, uint32_t* s_hist, int slots) {
     uint32_t take = 0, tie = 0;
     uint32_t nidx[kSpPer];
 #pragma unroll
     for (int j = 0; j < kSpPer; ++j) {
+        nidx[j] = 0;
+        if (j >= slots) break;
         const bool v = valid >> j & 1u;
         take |= (uint32_t)(v && key[j] > s.thr) << j;
         tie |= (uint32_t)(v && key[j] == s.thr) << j;
         nidx[j] = ~idx[j];
     }
     if (s.eq == s.need) return take | tie;  // uniform over the workgroup
-    const Sel t = select_kth(nidx, tie, s.need, s_hist);
+    const Sel t = select_kth(nidx, tie, s.need, s_hist, slots);
 #pragma unroll
     for (int j = 0; j < kSpPer; ++j) take |= (uint32_t)((tie >> j & 1u) && nidx[j] >= t.thr) << j;
     return take;
@@ -196,7 +200,8 @@ __device__ __forceinline__ uint32_t top_mask(const uint32_t (&key)[kSpPer], cons
 // Slots 0..k-1 for the set bits of `take` across the workgroup (any order):
 // a wave scan of the per-thread counts and one LDS atomic per wave.
 template <typename F>
-__device__ __forceinline__ void emit_top(uint32_t take, uint32_t k, uint32_t* s_cnt, F&& emit) {
+__device__ __forceinline__ void emit_top(uint32_t take, uint32_t k, int slots, uint32_t* s_cnt,
+                                         F&& emit) {
     const int lane = threadIdx.x & 63;
     const uint32_t n = __popc(take);
     const uint32_t incl = wave_scan_incl(n);
@@ -205,7 +210,7 @@ __device__ __forceinline__ void emit_top(uint32_t take, uint32_t k, uint32_t* s_
     uint32_t slot = read_lane(base, 63) + incl - n;
 #pragma unroll
     for (int j = 0; j < kSpPer; ++j)
-        if ((take >> j & 1u) && slot < k) emit(slot++, j);  // exactly k bits are set
+        if (j < slots && (take >> j & 1u) && slot < k) emit(slot++, j);  // exactly k bits are set
 }
 
 // SplitMix64 finaliser (Steele, Lea and Flood, "Fast splittable pseudorandom
@@ -254,11 +259,13 @@ __global__ __launch_bounds__(kSpThreads) void sample_kernel(SampleArgs a) {
     {
         // Range-checked buffer loads: no branch per slot, zeros past the chunk.
         const __amdgpu_buffer_rsrc_t r = make_rsrc(a.logits + c0, m * 4);
+        const int slots = (int)((m + kSpThreads - 1) / kSpThreads);
         float x[kSpPer];
 #pragma unroll
         for (int j = 0; j < kSpPer; ++j)
-            x[j] = __uint_as_float((uint32_t)__builtin_amdgcn_raw_buffer_load_b32(
-                r, 4 * (j * kSpThreads + tid), 0, 0));
+            x[j] = j < slots ? __uint_as_float((uint32_t)__builtin_amdgcn_raw_buffer_load_b32(
+                                   r, 4 * (j * kSpThreads + tid), 0, 0))
+                             : 0.0f;
 #pragma unroll
         for (int j = 0; j < kSpPer; ++j) {
             const uint32_t e = j * kSpThreads + tid;
@@ -280,9 +287,10 @@ __global__ __launch_bounds__(kSpThreads) void sample_kernel(SampleArgs a) {
             }
         }
     } else {
-        const Sel s = select_kth(key, valid, k, s_hist);
-        const uint32_t take = top_mask(key, idx, valid, s, s_hist);
-        emit_top(take, k, &s_cnt, [&](uint32_t slot, int j) {
+        const int slots = (int)((m + kSpThreads - 1) / kSpThreads);
+        const Sel s = select_kth(key, valid, k, s_hist, slots);
+        const uint32_t take = top_mask(key, idx, valid, s, s_hist, slots);
+        emit_top(take, k, slots, &s_cnt, [&](uint32_t slot, int j) {
             bk[slot] = key[j];
             bi[slot] = idx[j];
         });
@@ -309,15 +317,16 @@ __global__ __launch_bounds__(kSpThreads) void sample_kernel(SampleArgs a) {
 #pragma unroll
     for (int j = 0; j < kSpPer; ++j) {
         const uint32_t e = j * kSpThreads + tid;
-        const bool v = e < nc;
+        const bool v = e < nc && j < (int)((nc + kSpThreads - 1) / kSpThreads);
         key[j] = v ? ws_key[e] : 0u;
         idx[j] = v ? ws_idx[e] : 0xffffffffu;
         valid |= (uint32_t)v << j;
     }
     {
-        const Sel s = select_kth(key, valid, k, s_hist);
-        const uint32_t take = top_mask(key, idx, valid, s, s_hist);
-        emit_top(take, k, &s_cnt, [&](uint32_t slot, int j) {
+        const int slots = (int)((nc + kSpThreads - 1) / kSpThreads);
+        const Sel s = select_kth(key, valid, k, s_hist, slots);
+        const uint32_t take = top_mask(key, idx, valid, s, s_hist, slots);
+        emit_top(take, k, slots, &s_cnt, [&](uint32_t slot, int j) {
             s_top[slot] = ((uint64_t)key[j] << 32) | (uint32_t)~idx[j];
         });
     }

@@ -15,12 +15,13 @@
 // harness, from a counter-based hash of (seed, position), so a replayed graph
 // draws a fresh coin per step without host work.
 //
-// Layout: 32 workgroups of 256 threads.  Workgroup b takes the contiguous
+// Layout: G workgroups of 256 threads (G = 64 for k <= 128, else 32).
+// Workgroup b takes the contiguous
 // chunk b of the logits (at most 8192, held in registers: element j*256 + t
 // in thread t's j-th slot), finds its local k-th largest key by a radix
 // select (four 8-bit digit passes over per-wave LDS histograms), and writes
 // its top k (keys and indices) to the workspace.  The last workgroup to
-// finish (an agent-scope ticket) runs the same select over the 32*k
+// finish (an agent-scope ticket) runs the same select over the G*k
 // candidates, sorts the k survivors (in one wave's registers for k <= 64,
 // in LDS above), and does the softmax, the top-p cut and the coin walk with
 // lane or block scans.  Ties at the k-th value keep the lowest indices;
@@ -34,11 +35,17 @@
 namespace tiattn {
 namespace {
 
-constexpr int kSpBlocks = 32, kSpThreads = 256, kSpWaves = kSpThreads / 64;
-constexpr uint32_t kSpChunk = kSampleMaxVocab / kSpBlocks;
-constexpr int kSpPer = kSpChunk / kSpThreads;  // keys per thread, held in registers
+constexpr int kSpThreads = 256, kSpWaves = kSpThreads / 64;
+constexpr int kSpPer = 32;                             // keys per thread, held in registers
+constexpr uint32_t kSpChunk = kSpPer * kSpThreads;     // logits (or candidates) per workgroup
+// 64 workgroups for k <= 128 (half the chunk per workgroup), 32 above, so
+// that the merge's blocks * k candidates always fit one workgroup's slots.
+constexpr int kSpBlocksSmallK = 64, kSpBlocksLargeK = 32, kSpSmallK = 128;
 static_assert(kSampleMaxK <= kSpThreads, "one thread per kept candidate");
-static_assert(kSpBlocks * kSampleMaxK <= kSpChunk, "candidates fit the per-thread key slots");
+static_assert(kSpBlocksSmallK * kSpSmallK <= kSpChunk && kSpBlocksLargeK * kSampleMaxK <= kSpChunk,
+              "candidates fit the per-thread key slots");
+static_assert(kSpBlocksLargeK * kSpChunk >= kSampleMaxVocab, "every chunk fits one workgroup");
+constexpr uint32_t kSpMaxCand = kSpChunk;
 
 // Workspace: [0, 8) argmax key, [8, 12) argmax ticket, [12, 16) sampler
 // ticket, then keys [32][k] and indices [32][k] from byte 256.
@@ -249,11 +256,12 @@ __global__ __launch_bounds__(kSpThreads) void sample_kernel(SampleArgs a) {
     char* ws = static_cast<char*>(a.workspace);
     uint32_t* ticket = reinterpret_cast<uint32_t*>(ws + 12);
     uint32_t* ws_key = reinterpret_cast<uint32_t*>(ws + kSpCandOff);
-    uint32_t* ws_idx = ws_key + kSpBlocks * k;
+    const uint32_t G = gridDim.x;
+    uint32_t* ws_idx = ws_key + G * k;
     if (tid == 0) s_cnt = 0;
 
     // Phase 1: this workgroup's chunk, element j*256 + t in thread t's key[j].
-    const uint32_t cs = (a.n + kSpBlocks - 1) / kSpBlocks;
+    const uint32_t cs = (a.n + G - 1) / G;
     const uint32_t c0 = min(a.n, blockIdx.x * cs), m = min(a.n, c0 + cs) - c0;
     uint32_t key[kSpPer], idx[kSpPer], valid = 0;
     {
@@ -303,16 +311,16 @@ __global__ __launch_bounds__(kSpThreads) void sample_kernel(SampleArgs a) {
     __syncthreads();
     if (tid == 0) {
         __threadfence();
-        s_last = atomicAdd(ticket, 1u) == kSpBlocks - 1;
+        s_last = atomicAdd(ticket, 1u) == G - 1;
         if (s_last) __threadfence();
         s_cnt = 0;
     }
     __syncthreads();
     if (!s_last) return;
 
-    // Phase 2 (last workgroup): the top k of the 32*k candidates, as
+    // Phase 2 (last workgroup): the top k of the G*k candidates, as
     // (key << 32 | ~index) so that one ordering covers the ties.
-    const uint32_t nc = kSpBlocks * k;
+    const uint32_t nc = G * k;
     valid = 0;
 #pragma unroll
     for (int j = 0; j < kSpPer; ++j) {
@@ -415,7 +423,7 @@ __global__ __launch_bounds__(kSpThreads) void sample_kernel(SampleArgs a) {
 
 }  // namespace
 
-size_t sample_workspace_bytes() { return kSpCandOff + 2ull * kSpBlocks * kSampleMaxK * 4; }
+size_t sample_workspace_bytes() { return kSpCandOff + 2ull * kSpMaxCand * 4; }
 
 int sample_config(uint32_t vocab, float temperature, uint32_t top_k, float top_p, SampleArgs& a) {
     if (vocab == 0 || !(temperature >= 0.0f)) return TOYINFER_ERR_INVALID_ARGUMENT;
@@ -440,7 +448,7 @@ hipError_t launch_sample(const SampleArgs& a, hipStream_t stream) {
                                   reinterpret_cast<uint64_t*>(ws), reinterpret_cast<uint32_t*>(ws + 8),
                                   stream);
     }
-    sample_kernel<<<kSpBlocks, kSpThreads, 0, stream>>>(a);
+    sample_kernel<<<a.k <= kSpSmallK ? kSpBlocksSmallK : kSpBlocksLargeK, kSpThreads, 0, stream>>>(a);
     return hipGetLastError();
 }
 

@@ -203,3 +203,33 @@ def test_load_weights_bytes_and_model(dev, tmp_path, tie):
     a.close()
     b.close()
     lw.close()
+
+
+def test_config_json_forms(tmp_path):
+    """The loader's JSON reader on valid forms real configs use (nested
+    objects, escapes, surrogate pairs, exponents, null) and on malformed ones."""
+    d = str(tmp_path)
+    good = ('{"architectures": ["Qwen3ForCausalLM"], "name": "caf\\u00e9 \\ud83d\\ude00 \\"q\\" \\\\ \\/",'
+            ' "rope_scaling": {"type": "yarn", "factor": 4.0, "deep": [[[1, 2], {"a": null}]]},'
+            ' "num_hidden_layers": 2, "hidden_size": 256, "num_attention_heads": 4,'
+            ' "num_key_value_heads": 2, "head_dim": 64, "intermediate_size": 512,'
+            ' "vocab_size": 1000, "rms_norm_eps": 1e-06, "rope_theta": 1000000.0,'
+            ' "max_position_embeddings": 40960, "bos_token_id": null, "eos_token_id": [151645, 151643],'
+            ' "tie_word_embeddings": true, "torch_dtype": "bfloat16", "use_cache": false}')
+    open(os.path.join(d, "config.json"), "w").write(good)
+    cfg, info = qwen3.read_config(d, 0, 16)
+    assert cfg.rms_norm_eps == pytest.approx(1e-6) and cfg.rope_theta == 1e6
+    assert (info.bos_token_id, info.eos_token_id, info.tie_word_embeddings) == (0, 151645, 1)
+    bad = [good[:-1],                                           # unterminated object
+           good.replace('"use_cache": false}', '"use_cache": false,}'),   # trailing comma
+           good.replace("\\u00e9", "\\u00g9"),                  # bad hex digit
+           good.replace("\\ud83d\\ude00", "\\ud83d"),           # lone high surrogate
+           good.replace("4.0", "4."),                           # digits must follow '.'
+           good.replace('"hidden_size": 256', '"hidden_size": 256.5'),   # not an integer
+           '[' * 100 + ']' * 100,                               # nesting too deep
+           good + " x"]                                         # trailing garbage
+    for b in bad:
+        open(os.path.join(d, "config.json"), "w").write(b)
+        with pytest.raises(attn.ToyInferError) as e:
+            qwen3.read_config(d, 0, 16)
+        assert e.value.status == attn.ERR_IO, b[:60]

@@ -486,7 +486,7 @@ def main():
     args = parse()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only: bench.py --gpus 1 "
-                                   "(sharding across GPUs is described in DESIGN.md, not run)"}))
+                                   "(sharding across GPUs is designed, not implemented)"}))
         sys.exit(2)
     import torch
 

@@ -57,7 +57,7 @@ def check_case(smp, lg, T, k, p, label):
         got = smp(dev_lg, T, k, p, u)
         assert got == order[j], f"{label}: u={u:.6f} expected order[{j}]={order[j]}, got {got}"
     cum = np.cumsum(probs.astype(np.float64))
-    if np.min(np.abs(cum[:-1] - p)) > CUT_MARGIN and probs[kept - 1] > MIN_P:
+    if (len(cum) == 1 or np.min(np.abs(cum[:-1] - p)) > CUT_MARGIN) and probs[kept - 1] > MIN_P:
         got = smp(dev_lg, T, k, p, 1 - 2 ** -24)
         assert got == order[kept - 1], f"{label}: last kept {order[kept - 1]}, got {got}"
 
@@ -122,3 +122,16 @@ def test_sample_frequencies(dev):
     chi2 = float(((obs - exp) ** 2 / exp).sum())
     from scipy.stats import chi2 as chi2_dist
     assert chi2 < chi2_dist.ppf(0.999, kept - 1), (obs, exp)
+
+
+@pytest.mark.parametrize("V,k", [(7, 100), (256, 256), (1000, 64), (1000, 65), (151936, 128),
+                                 (151936, 129), (262144, 256), (4097, 3), (1, 5)])
+def test_sample_boundaries(dev, V, k):
+    """k clamped to the vocabulary, every candidate kept, the one-wave sort
+    (k <= 64) against the workgroup sort, the 64/32 workgroup switch at
+    k = 128, odd vocabulary sizes, a one-entry vocabulary."""
+    print(f"[step] sample boundary V={V} k={k}", flush=True)
+    smp = Sampler(dev)
+    rng = np.random.default_rng(V * 7 + k)
+    lg = (rng.standard_normal(V) * 2).astype(np.float32)
+    check_case(smp, lg, 1.3, k, 0.97, f"boundary V={V} k={k}")

@@ -44,8 +44,10 @@ int toyinfer_tokenizer_encode(toyinfer_tokenizer* t, const char* text, uint32_t*
                               uint32_t cap, uint32_t* count);
 
 /* Tokenizer::decode (src/tokenizer.cpp:327-333): the token's bytes
- * (NUL-terminated), NULL for an id at or above vocab_size.  *len (if not
- * NULL) receives the byte length, which counts embedded NUL bytes. */
+ * (NUL-terminated, owned by the tokenizer and valid until destroy), NULL for
+ * an id at or above vocab_size.  *len (if not NULL) receives the byte length,
+ * which counts embedded NUL bytes.  A tokenizer is read-only after create:
+ * encode, decode and render_prompt may run on several threads at once. */
 const char* toyinfer_tokenizer_decode(const toyinfer_tokenizer* t, uint32_t id, uint32_t* len);
 
 /* Tokenizer::render_prompt (src/tokenizer.cpp:335-369): the system template

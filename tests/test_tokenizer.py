@@ -215,3 +215,18 @@ def test_header_functions_exported_and_bound():
                          text=True, check=True).stdout
     assert names <= set(re.findall(r"\bT (toyinfer_\w+)", out))
     assert names == set(tokenizer._SIGS)
+
+
+def test_special_token_scan_limits(tmp_path):
+    """src/tokenizer.cpp:177-197: the '>' must come within the longest token
+    length (counted from the '<'), and only the first '>' is tried."""
+    d = str(tmp_path)
+    vocab = [b"<", b">", b"a", b"b", b"<ab>", b"<a>"]          # longest token: 4 bytes
+    write_files(d, vocab, [])
+    t, o = Tokenizer(d, 8), bpe.Tokenizer(d, 8)
+    cases = {"<ab>": [4], "<a>": [5], "<a>>": [5, 1],
+             "<abb>": [0, 2, 3, 3, 1],        # '>' at offset 4: beyond the scan window
+             "<a<ab>": [0, 2, 4],             # no '>' in the first window; the second '<' starts "<ab>"
+             "<": [0], "<ab": [0, 2, 3]}
+    for s, exp in cases.items():
+        assert t.encode(s) == exp == o.encode(s.encode()), s

@@ -233,3 +233,21 @@ def test_config_json_forms(tmp_path):
         with pytest.raises(attn.ToyInferError) as e:
             qwen3.read_config(d, 0, 16)
         assert e.value.status == attn.ERR_IO, b[:60]
+
+
+def test_lm_head_choice(tmp_path):
+    """lm_head.weight is loaded only when present and the embeddings are not
+    tied; otherwise the embeddings serve as the lm-head (the reference always
+    uses them, src/qwen.cpp:482-483)."""
+    d = str(tmp_path)
+    t = random_tensors(TINY)                       # has lm_head.weight
+    write_model(d, TINY, t, 2, True)
+    cfg = qwen3.Config(**TINY)
+    head = (t["lm_head.weight"].numel() * 2 + 255) // 256 * 256
+    untied = qwen3.check_weights(d, cfg, False)
+    assert qwen3.check_weights(d, cfg, True) == untied - head
+    d2 = str(tmp_path / "nohead")
+    t2 = dict(t)
+    del t2["lm_head.weight"]
+    write_model(d2, TINY, t2, 2, True)
+    assert qwen3.check_weights(d2, cfg, False) == untied - head

@@ -1,22 +1,24 @@
 #!/usr/bin/env python3
 """Benchmark of the MI355X attention hot path (one GPU).
 
-Prints ONE JSON line.  The headline workload is BASELINE.json configs[1]:
-causal GQA prefill, batch 1, S=1371, 16 query / 8 KV heads, head_dim 128,
-bf16 ~ N(0,1) seeded; metric TFLOP/s with the causal FLOP count
-4*S^2*Hq*D/2.  A step is one prefill over that input (one
-toyinfer_flash_attention_v1_bf16 call); W untimed steps, then exactly K
-timed steps between two device synchronisations, timed with HIP events on
-the stream the kernel runs on.
+Prints ONE JSON line.  The headline workload is BASELINE.json configs[3], the
+largest single-GPU configuration and the north-star prefill: causal GQA
+prefill, batch 1, S=8192, 32 query / 8 KV heads, head_dim 128, with Qwen3's
+per-head QK-RMSNorm (eps 1e-6, gamma ~ U(0.9, 1.1)) and RoPE (theta 1e6,
+positions 0..8191) fused in front; bf16 ~ N(0,1) seeded; metric TFLOP/s with
+the causal FLOP count 4*S^2*Hq*D/2 (attention only; the K pre-pass time is
+inside the step).  A step is one toyinfer_prefill_qknorm_rope_attention_bf16
+call over that input; W untimed steps, then exactly K timed steps between two
+device synchronisations, timed with HIP events recorded on the stream the
+kernels run on.
 
-The same line carries, under "components", the other hot-path workloads
-the north-star targets name, each with its own roofline block:
-  * prefill_fused_s8192: configs[3], S=8192, 32/8, QK-RMSNorm + RoPE fused
-    in front (toyinfer_prefill_qknorm_rope_attention_bf16), MFMA-bound;
+The same line carries, under "components", the other hot-path workloads,
+each with its own roofline block:
+  * prefill_s1371: configs[1], S=1371, 16/8 (toyinfer_flash_attention_v1_bf16);
   * decode_b8_l4096: configs[2], split-K decode over 128 MiB of KV, HBM-bound;
   * decode_b1_l32768: the north-star 32k-token decode, 128 MiB of KV;
   * decode_step / decode_contract: the decode-step pre-pass and the
-    reference-contract graph decode;
+    reference-contract graph decode at the engine's cache size;
   * proj_gemv / proj_gemm: the projections either side of attention (lm-head
     GEMV, HBM-bound; a 4096-token prefill projection, MFMA-bound);
   * sample: the device top-k/top-p pick over a 151936-entry vocabulary;
@@ -27,8 +29,10 @@ Decode steps rotate over 4 independent KV sets (512 MiB) so every step reads
 KV that is not resident in the 256 MB Infinity Cache.
 
 cpu_baseline: the CPU oracle (oracle/, the restated host reference of the
-reference's tests) timed on this host's cores on a bounded sample of the
-headline workload, and used there as the checker of the GPU output.
+reference's tests) timed on this host's cores on a bounded, stated row
+subset of the headline workload (all cores, and one core on a smaller
+subset), plus the config-3 decode on the CPU; the same oracle output checks
+the GPU output of those rows.
 """
 from __future__ import annotations
 
@@ -75,10 +79,10 @@ def causal_flops(s, hq, d):
 def parse():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
-    # The headline step is ~20 us, and the MFMA clock settles over the first
-    # few milliseconds of sustained launches: defaults give it ~4 ms to settle.
-    ap.add_argument("--steps", type=int, default=500)
-    ap.add_argument("--warmup", type=int, default=200)
+    # The headline step is ~0.6 ms; the defaults give the MFMA clock ~12 ms of
+    # sustained launches to settle before the timed region.
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-components", action="store_true",
                     help="only the headline workload")
     ap.add_argument("--no-cpu", action="store_true", help="skip the cpu_baseline leg")
@@ -140,42 +144,61 @@ def prefill_inputs(s, hq, hkv, d, dev, seed=SEED):
 
 
 def bench_prefill(dev, stream, steps, warmup, s=1371, hq=16, hkv=8, d=128):
+    """causal GQA prefill through toyinfer_flash_attention_v1_bf16."""
     import torch
 
     from toyinfer_amd import attn
 
-    host, (q, k, v) = prefill_inputs(s, hq, hkv, d, dev)
+    _, (q, k, v) = prefill_inputs(s, hq, hkv, d, dev)
     o = torch.empty((s, hq, d), dtype=torch.bfloat16, device=dev)
     ms = time_steps(lambda i: attn.flash_attention_v1_bf16(q, k, v, o, hq, hkv, d, s, stream),
                     steps, warmup, stream)
     tflops = causal_flops(s, hq, d) / (ms * 1e-3) / 1e12
-    return ms, tflops, host, to_host(o)
+    return {"workload": f"prefill_causal_gqa_s{s}_hq{hq}_hkv{hkv}_d{d}",
+            "entry": "toyinfer_flash_attention_v1_bf16", "steps": steps,
+            "ms_per_step": round(ms, 5), "value": round(tflops, 2), "unit": "TFLOP/s",
+            "roofline": roofline("mfma", tflops, PEAK_BF16_TFLOPS, "TFLOP/s",
+                                 traffic_bytes("prefill"))}
 
 
-def bench_prefill_fused(dev, stream, steps, warmup, s=8192, hq=32, hkv=8, d=128):
+FUSED = dict(s=8192, hq=32, hkv=8, d=128, eps=1e-6, theta=1e6)
+
+
+def fused_inputs(dev, s, hq, hkv, d, theta):
+    """configs[3] inputs: raw Q/K/V projections, gamma_q/gamma_k ~ U(0.9, 1.1),
+    and the rotary table the model builds once (as the reference keeps
+    inv_freq): host bf16 bits and device tensors."""
     import torch
 
     from toyinfer_amd import attn, synth
 
-    _, (q, k, v) = prefill_inputs(s, hq, hkv, d, dev, seed=SEED + 4)
-    gq = to_dev(synth.uniform_bf16(SEED + 4, "gamma_q", (d,), 0.9, 1.1), dev)
-    gk = to_dev(synth.uniform_bf16(SEED + 4, "gamma_k", (d,), 0.9, 1.1), dev)
-    # Model-init state, as the reference keeps inv_freq: the rotary table.
+    host, (q, k, v) = prefill_inputs(s, hq, hkv, d, dev, seed=SEED + 4)
+    gqb = synth.uniform_bf16(SEED + 4, "gamma_q", (d,), 0.9, 1.1)
+    gkb = synth.uniform_bf16(SEED + 4, "gamma_k", (d,), 0.9, 1.1)
     f = torch.empty(d // 2, dtype=torch.float32, device=dev)
-    attn.precompute_freq_f32(f, d, 1e6, stream)
+    attn.precompute_freq_f32(f, d, theta)
     table = torch.empty((s, d // 2, 2), dtype=torch.float32, device=dev)
-    attn.rope_cos_sin_f32(table, f, s, d, stream)
+    attn.rope_cos_sin_f32(table, f, s, d)
+    torch.cuda.synchronize()
+    return host + (gqb, gkb), (q, k, v, to_dev(gqb, dev), to_dev(gkb, dev), table)
+
+
+def bench_prefill_fused(dev, stream, steps, warmup):
+    """the headline step (K norm+RoPE pre-pass, then attention
+    with Q normalised and rotated on load)."""
+    import torch
+
+    from toyinfer_amd import attn
+
+    s, hq, hkv, d = FUSED["s"], FUSED["hq"], FUSED["hkv"], FUSED["d"]
+    host, (q, k, v, gq, gk, table) = fused_inputs(dev, s, hq, hkv, d, FUSED["theta"])
     o = torch.empty((s, hq, d), dtype=torch.bfloat16, device=dev)
     k_out = torch.empty_like(k)
     ms = time_steps(lambda i: attn.prefill_qknorm_rope_attention_bf16(
-        q, k, v, o, k_out, gq, gk, table, 1e-6, hq, hkv, d, s, stream), steps, warmup, stream)
+        q, k, v, o, k_out, gq, gk, table, FUSED["eps"], hq, hkv, d, s, stream), steps, warmup,
+        stream)
     tflops = causal_flops(s, hq, d) / (ms * 1e-3) / 1e12
-    return {"workload": "prefill_fused_qknorm_rope_s8192_hq32_hkv8_d128",
-            "entry": "toyinfer_prefill_qknorm_rope_attention_bf16", "steps": steps,
-            "ms_per_step": round(ms, 5), "value": round(tflops, 2), "unit": "TFLOP/s",
-            "note": "time includes the K norm+RoPE pre-pass; FLOPs count attention only",
-            "roofline": roofline("mfma", tflops, PEAK_BF16_TFLOPS, "TFLOP/s",
-                                 traffic_bytes("prefill_fused"))}
+    return ms, tflops, host, to_host(o)
 
 
 # ------------------------------------------------------------------- decode
@@ -455,31 +478,99 @@ def bench_copy(dev, stream, steps, warmup, mib=256):
 
 # ------------------------------------------------------------- CPU baseline
 
-def cpu_baseline(host_inputs, gpu_out, budget_s, s=1371, hq=16, d=128):
-    """Oracle on this host's cores over the full headline workload, repeated
-    until ~budget_s of CPU time; its output also checks the GPU output."""
+def _subset_rows(s, stride):
+    """First and last 64 rows plus every `stride`-th row (deterministic)."""
+    return sorted(set(range(min(64, s))) | set(range(max(0, s - 64), s)) | set(range(0, s, stride)))
+
+
+def _cpu_fused_rows(host, rows, threads):
+    """The oracle's config-3 path on `rows`: K norm -> bf16 -> RoPE -> bf16 on
+    every row (each query row reads all earlier keys), the same on Q for the
+    listed rows only (their own positions), then causal attention for those
+    rows (fp64 scores and softmax, fp32 P.V).  Returns float32 [S][Hq][D]
+    with the listed rows filled."""
+    import numpy as np
+
+    import oracle
+
+    qb, kb, vb, gqb, gkb = host
+    s, hq, d = qb.shape
+    eps, theta = FUSED["eps"], FUSED["theta"]
+    inv = oracle.inv_freq(d, theta)
+    gq, gk = oracle.bf16_to_f32(gqb), oracle.bf16_to_f32(gkb)
+    kr = oracle.qk_norm_rope(oracle.bf16_to_f32(kb), gk, inv, eps)
+    qr = np.zeros((s, hq, d), np.float32)
+    qf = oracle.bf16_to_f32(qb[rows])
+    for j, r in enumerate(rows):
+        qr[r] = oracle.rope(oracle.multi_rmsnorm(qf[j], gq, d, eps), inv, 1, hq, d, pos0=r)
+    return oracle.flash_reference(qr, kr, oracle.bf16_to_f32(vb), rows=rows, nthreads=threads)
+
+
+def cpu_baseline(host, gpu_out, budget_s):
+    """The oracle on this host's cores: the headline workload on a row
+    subset, all cores (repeated to ~budget_s/2) and one core (a sparser
+    subset), plus config 3's decode; the all-core output checks the GPU's
+    rows."""
     import numpy as np
 
     import oracle
 
     threads = len(os.sched_getaffinity(0))
-    qb, kb, vb = host_inputs
+    s, hq, d = FUSED["s"], FUSED["hq"], FUSED["d"]
+
+    def flops(rows):
+        return sum(4.0 * (r + 1) * d * hq for r in rows)
+
+    rows = _subset_rows(s, 61)
     t0 = time.perf_counter()
-    ref = oracle.flash_reference(qb, kb, vb, nthreads=threads)
-    reps, elapsed = 1, time.perf_counter() - t0
-    while elapsed < budget_s and reps < 64:
-        oracle.flash_reference(qb, kb, vb, nthreads=threads)
+    ref = _cpu_fused_rows(host, rows, threads)
+    reps, el = 1, time.perf_counter() - t0
+    while el < budget_s / 2 and reps < 16:
+        _cpu_fused_rows(host, rows, threads)
         reps += 1
-        elapsed = time.perf_counter() - t0
-    tflops = causal_flops(s, hq, d) * reps / elapsed / 1e12
-    exp = oracle.round_bf16(ref)
-    got = (gpu_out.astype(np.uint32) << 16).view(np.float32)
-    diff = np.abs(got - exp)
-    return {"value": round(tflops, 6), "unit": "TFLOP/s", "cores": threads, "kind": "port",
-            "sample": f"full headline workload (S={s}, {hq}/8 heads, D={d}) x {reps} runs "
-                      f"of the oracle (fp64 scores/softmax, fp32 P.V), {elapsed:.1f} s, "
-                      f"{threads} OpenMP threads",
-            "parity_vs_gpu": {"max_abs": float(diff.max()), "mean_abs": float(diff.mean())}}
+        el = time.perf_counter() - t0
+    tf_all = flops(rows) * reps / el / 1e12
+    got = (gpu_out[rows].astype(np.uint32) << 16).view(np.float32)
+    diff = np.abs(got - oracle.round_bf16(ref[rows]))
+
+    rows1 = list(range(0, s, 122))
+    t0 = time.perf_counter()
+    _cpu_fused_rows(host, rows1, 1)
+    el1 = time.perf_counter() - t0
+    tf_one = flops(rows1) / el1 / 1e12
+
+    # configs[2] decode (B=8, L=4096, 32/8), the full workload.
+    from toyinfer_amd import synth
+
+    b, L, dhq, dhkv = 8, 4096, 32, 8
+    qb = synth.normal_bf16(SEED + 10, "q", (b, dhq, d))
+    kb = synth.normal_bf16(SEED + 10, "k", (b, L, dhkv, d))
+    vb = synth.normal_bf16(SEED + 10, "v", (b, L, dhkv, d))
+    kv_bytes = 2.0 * b * L * dhkv * d * 2
+    dec = {}
+    for n in (threads, 1):
+        t0 = time.perf_counter()
+        oracle.decode_batched(qb, kb, vb, [L] * b, nthreads=n)
+        reps_d, eld = 1, time.perf_counter() - t0
+        while eld < 1.0 and reps_d < 32:
+            oracle.decode_batched(qb, kb, vb, [L] * b, nthreads=n)
+            reps_d += 1
+            eld = time.perf_counter() - t0
+        dec[n] = kv_bytes * reps_d / eld / 1e9
+    return {"value": round(tf_all, 6), "unit": "TFLOP/s", "cores": threads, "kind": "port",
+            "sample": f"headline workload (S={s}, {hq}/8 heads, D={d}, QK-norm + RoPE) on "
+                      f"{len(rows)} query rows (first and last 64 plus every 61st) of all "
+                      f"heads, x {reps} runs, {el:.1f} s, {threads} OpenMP threads; the oracle: "
+                      "K norm/RoPE on all rows, Q's on those rows, fp64 scores and softmax, fp32 "
+                      "P.V; FLOPs = 4*(i+1)*D*Hq summed over those rows",
+            "single_core": {"value": round(tf_one, 6), "unit": "TFLOP/s", "cores": 1,
+                            "sample": f"{len(rows1)} query rows (every 122nd), {el1:.1f} s"},
+            "decode_b8_l4096": {"unit": "GB/s", "value": round(dec[threads], 2),
+                                "cores": threads, "single_core_value": round(dec[1], 2),
+                                "sample": "configs[2] full workload (KV bytes / time), fp32 "
+                                          "scores, softmax and P.V"},
+            "parity_vs_gpu": {"rows": len(rows), "max_abs": float(diff.max()),
+                              "mean_abs": float(diff.mean())}}
 
 
 def main():
@@ -495,53 +586,55 @@ def main():
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     stream = torch.cuda.Stream(device=dev)
+    comp = {
+        "prefill": lambda: bench_prefill(dev, stream, max(50, args.steps * 5), 20),
+        "decode_b8_l4096": lambda: bench_decode(dev, stream, max(50, args.steps * 2), 10,
+                                                b=8, L=4096),
+        "decode_b1_l32768": lambda: bench_decode(dev, stream, max(50, args.steps * 2), 10,
+                                                 b=1, L=32768),
+        "decode_step": lambda: bench_decode_step(dev, stream, max(50, args.steps * 2), 10),
+        "decode_contract": lambda: bench_decode_contract(dev, stream, max(50, args.steps * 2), 2),
+        "proj_gemv": lambda: bench_proj_gemv(dev, stream, max(50, args.steps), 10),
+        "proj_gemm": lambda: bench_proj_gemm(dev, stream, max(200, args.steps), 50),
+        "sample": lambda: bench_sample(dev, stream, max(200, args.steps), 50),
+        "qwen3_e2e": lambda: bench_qwen3_e2e(dev),
+        "copy_calibration": lambda: bench_copy(dev, stream, args.steps, args.warmup),
+    }
     if args.workload != "all":
-        one = {"prefill": lambda: dict(zip(("ms_per_step", "value"),
-                                           bench_prefill(dev, stream, args.steps, args.warmup)[:2]),
-                                       workload="prefill_causal_gqa_s1371_hq16_hkv8_d128",
-                                       unit="TFLOP/s"),
-               "prefill_fused": lambda: bench_prefill_fused(dev, stream, args.steps, args.warmup),
-               "decode_b8_l4096": lambda: bench_decode(dev, stream, args.steps, args.warmup,
-                                                       b=8, L=4096),
-               "decode_b1_l32768": lambda: bench_decode(dev, stream, args.steps, args.warmup,
-                                                        b=1, L=32768),
-               "decode_step": lambda: bench_decode_step(dev, stream, args.steps, args.warmup),
-               "decode_contract": lambda: bench_decode_contract(dev, stream, args.steps,
-                                                                args.warmup),
-               "proj_gemv": lambda: bench_proj_gemv(dev, stream, args.steps, args.warmup),
-               "proj_gemm": lambda: bench_proj_gemm(dev, stream, args.steps, args.warmup),
-               "qwen3_e2e": lambda: bench_qwen3_e2e(dev),
-               "sample": lambda: bench_sample(dev, stream, args.steps, args.warmup),
-               "copy_calibration": lambda: bench_copy(dev, stream, args.steps, args.warmup)}
-        print(json.dumps(one[args.workload]()), flush=True)
+        if args.workload == "prefill_fused":
+            ms, tf, _, _ = bench_prefill_fused(dev, stream, args.steps, args.warmup)
+            out = {"workload": "prefill_fused_qknorm_rope_s8192_hq32_hkv8_d128",
+                   "ms_per_step": round(ms, 5), "value": round(tf, 2), "unit": "TFLOP/s"}
+        else:
+            out = comp[args.workload]()
+        print(json.dumps(out), flush=True)
         return
 
-    ms, tflops, host_inputs, gpu_out = bench_prefill(dev, stream, args.steps, args.warmup)
+    s, hq, hkv, d = FUSED["s"], FUSED["hq"], FUSED["hkv"], FUSED["d"]
+    ms, tflops, host, gpu_out = bench_prefill_fused(dev, stream, args.steps, args.warmup)
     line = {
         "metric": METRIC, "value": round(tflops, 2), "unit": "TFLOP/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 5),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
-        "data": "synthetic: bf16 N(0,1) from seed 2026 (SplitMix64 + Box-Muller)",
-        "config": {"workload": "prefill_causal_gqa_s1371_hq16_hkv8_d128", "batch": 1,
-                   "seq_len": 1371, "num_q_heads": 16, "num_kv_heads": 8, "head_dim": 128,
-                   "flops_per_step": causal_flops(1371, 16, 128), "accumulate": "fp32",
+        "data": "synthetic: bf16 N(0,1) from seed 2030 (SplitMix64 + Box-Muller), "
+                "gamma ~ U(0.9, 1.1)",
+        "config": {"workload": "prefill_fused_qknorm_rope_s8192_hq32_hkv8_d128", "batch": 1,
+                   "seq_len": s, "num_q_heads": hq, "num_kv_heads": hkv, "head_dim": d,
+                   "qk_norm_eps": FUSED["eps"], "rope_theta": FUSED["theta"],
+                   "flops_per_step": causal_flops(s, hq, d), "accumulate": "fp32",
+                   "entry": "toyinfer_prefill_qknorm_rope_attention_bf16",
+                   "note": "step = K norm+RoPE pre-pass + attention; FLOPs count attention only",
                    "parallelism": "single GPU"},
         "roofline": roofline("mfma", tflops, PEAK_BF16_TFLOPS, "TFLOP/s",
-                             traffic_bytes("prefill")),
+                             traffic_bytes("prefill_fused")),
     }
     if not args.no_components:
-        comps = [bench_prefill_fused(dev, stream, max(10, args.steps // 4), 10)]
-        comps.append(bench_decode(dev, stream, max(50, args.steps * 2), 10, b=8, L=4096))
-        comps.append(bench_decode(dev, stream, max(50, args.steps * 2), 10, b=1, L=32768))
-        comps.append(bench_decode_step(dev, stream, max(50, args.steps * 2), 10))
-        comps.append(bench_decode_contract(dev, stream, max(50, args.steps * 2), 2))
-        comps.append(bench_proj_gemv(dev, stream, max(50, args.steps), 10))
-        comps.append(bench_proj_gemm(dev, stream, max(200, args.steps), 50))
-        comps.append(bench_sample(dev, stream, max(200, args.steps), 50))
-        comps.append(bench_qwen3_e2e(dev))
-        line["components"] = comps
+        line["components"] = [comp[n]() for n in
+                              ("prefill", "decode_b8_l4096", "decode_b1_l32768", "decode_step",
+                               "decode_contract", "proj_gemv", "proj_gemm", "sample",
+                               "qwen3_e2e")]
     if not args.no_cpu:
-        line["cpu_baseline"] = cpu_baseline(host_inputs, gpu_out, args.cpu_seconds)
+        line["cpu_baseline"] = cpu_baseline(host, gpu_out, args.cpu_seconds)
     print(json.dumps(line), flush=True)
 
 

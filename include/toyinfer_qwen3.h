@@ -124,14 +124,19 @@ void toyinfer_qwen3_destroy(toyinfer_qwen3* m);
 
 /* Runs the prompt token_ids_d[0..num_tokens) (device memory) through every
  * layer (KV cache rows 0..num_tokens-1 written), the final norm and the
- * lm-head on the last token, and the greedy pick: afterwards the logits,
- * tokens[num_tokens] and the device position (= num_tokens) are set.
- * Enqueued on the model's stream; returns without waiting. */
+ * lm-head on the last token, and the pick that toyinfer_qwen3_set_sampling
+ * selects (greedy by default): afterwards the logits, tokens[num_tokens] and
+ * the device position (= num_tokens) are set.  Enqueued on the model's
+ * stream; returns without waiting.  The ids are copied on the model's stream
+ * with no ordering against the caller's streams: token_ids_d must stay valid
+ * and unmodified until the model's stream has passed this call (for example
+ * until toyinfer_qwen3_synchronize returns). */
 int toyinfer_qwen3_prefill(toyinfer_qwen3* m, const uint32_t* token_ids_d, uint32_t num_tokens);
 
-/* `steps` greedy decode steps from the device position: each runs the token
- * at tokens[pos] through the layers (KV row pos), writes tokens[pos + 1] and
- * advances pos.  With use_graph the step body is captured on first use and
+/* `steps` decode steps from the device position: each runs the token at
+ * tokens[pos] through the layers (KV row pos), writes the pick that
+ * toyinfer_qwen3_set_sampling selects (greedy by default) to tokens[pos + 1]
+ * and advances pos.  With use_graph the step body is captured on first use and
  * replayed (one graph launch per step); without it the same kernels are
  * launched directly.  pos + steps must stay below max_seq_len. */
 int toyinfer_qwen3_decode(toyinfer_qwen3* m, uint32_t steps, int use_graph);

@@ -94,6 +94,40 @@ def test_graph_replay(dev, hq, hkv, d, msl, positions):
         check_compat(score, ob, o, q, k, v, pos, msl, f"graph pos={pos}")
 
 
+def test_reference_contract_engine_cache(dev):
+    """The engine's cache size (--max_seq_len=40960, the reference's
+    experiment scripts) at Qwen3-8B heads: direct calls at pos 0, 32767 and
+    40959, then attention_bf16_graph captured once and replayed at pos
+    32767, 0 and 40959 (the partials then sit in the score rows, ~96
+    splits).  score, O_buffer and O against the oracle, zero tail checked."""
+    hq, hkv, d, msl = 32, 8, 128, 40960
+    print(f"[decode] reference contract at msl={msl}", flush=True)
+    qf, kf, vf = oracle.make_attention_case(hq, hkv, d, msl, 0.03, 0.017)
+    qb, kb, vb = oracle.f32_to_bf16(qf), oracle.f32_to_bf16(kf), oracle.f32_to_bf16(vf)
+    q, k, v = oracle.bf16_to_f32(qb), oracle.bf16_to_f32(kb), oracle.bf16_to_f32(vb)
+    qd, kd, vd = H.to_dev_bf16(qb, dev), H.to_dev_bf16(kb, dev), H.to_dev_bf16(vb, dev)
+    for pos in (0, 32767, msl - 1):
+        score, ob, o = dirty_buffers(hq, d, msl, dev)
+        attn.attention_bf16(qd, kd, vd, score, ob, o, hq, hkv, d, pos, msl)
+        H.sync()
+        check_compat(score, ob, o, q, k, v, pos, msl, f"direct pos={pos}")
+    score, ob, o = dirty_buffers(hq, d, msl, dev)
+    pos_d = torch.zeros(1, dtype=torch.int32, device=dev)
+    stream = torch.cuda.Stream()
+    with torch.cuda.stream(stream):
+        attn.attention_bf16_graph(qd, kd, vd, score, ob, o, hq, hkv, d, pos_d, msl, stream)
+    H.sync()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        attn.attention_bf16_graph(qd, kd, vd, score, ob, o, hq, hkv, d, pos_d, msl, stream)
+    for pos in (32767, 0, msl - 1):
+        pos_d.fill_(pos)
+        H.sync()
+        graph.replay()
+        H.sync()
+        check_compat(score, ob, o, q, k, v, pos, msl, f"graph pos={pos}")
+
+
 def run_batched(qb, kb, vb, lens, dev, splits=0, seq_lens_on_device=False):
     b, hq, d = qb.shape
     cap, hkv = kb.shape[1], kb.shape[2]

@@ -527,3 +527,117 @@ def test_sample_coin_is_splitmix64():
     assert abs(u.mean() - 0.5) < 0.01
     hist = np.histogram(u, bins=10, range=(0, 1))[0]
     assert hist.min() > 1800 and hist.max() < 2200
+
+
+# ------------------------------------------------------------ Qwen3 forward
+
+def _qwen3_fixture():
+    import json
+
+    from tests import qwen3_weights as QW
+
+    g = np.load(os.path.join(GOLD, "qwen3_tiny.npz"))
+    cfg = json.loads(str(g["config"]))
+    init = json.loads(str(g["init"]))
+    bits = QW.weight_bits(cfg, int(g["seed"]), init["proj_std"], init["embed_std"],
+                          tuple(init["norm_range"]), init["tied"])
+    w = QW.to_f32(bits)
+    w["inv_freq"] = oracle.inv_freq(cfg["head_dim"], cfg["rope_theta"])
+    return cfg, w, g
+
+
+def _qwen3_oracle_logits(cfg, w, g):
+    ids, T = g["ids"], int(g["prompt"])
+    ref = oracle.Qwen3Reference(cfg, w)
+    rows = [ref.forward(ids[:T], 0)]
+    for s in range(len(ids) - T):
+        rows.append(ref.forward(ids[T + s:T + s + 1], T + s))
+    return np.stack(rows)
+
+
+# The oracle against the float64 forward with the same bf16 rounding points
+# (tests/golden/make_qwen3_golden.py, itself checked against transformers'
+# Qwen3).  The remaining differences are fp32-vs-fp64 sums flipping a bf16
+# activation by one step now and then; on logits of std ~17 they measure
+# max 0.20, mean 0.043 (the rounding points themselves move the logits by
+# mean 0.067).  Each planted slip below moves them by mean 1 or more.
+QWEN3_PIN_MAX = 0.5
+QWEN3_PIN_MEAN = 0.1
+
+
+def test_qwen3_reference_vs_float64_fixture():
+    cfg, w, g = _qwen3_fixture()
+    got = _qwen3_oracle_logits(cfg, w, g)
+    d = np.abs(got.astype(np.float64) - g["logits_rounded"])
+    assert d.max() <= QWEN3_PIN_MAX and d.mean() <= QWEN3_PIN_MEAN, (d.max(), d.mean())
+    # Same greedy pick at every step, and the exact (unrounded) forward is
+    # within the spread the rounding points themselves cause.
+    assert np.array_equal(got.argmax(1), g["logits_rounded"].argmax(1))
+    assert np.abs(got - g["logits_exact"]).max() < 1.0
+    assert float(g["transformers_max_diff"]) < 1e-5 * np.abs(g["logits_exact"]).max()
+
+
+def _interleaved_rope(qk, inv_freq, num_tokens, num_heads, d, pos0=0):
+    """RoPE over adjacent pairs (2i, 2i+1): the GPT-J pairing, not Qwen3's."""
+    x = np.asarray(qk, np.float32).reshape(num_tokens, num_heads, d // 2, 2).copy()
+    t = (np.arange(num_tokens, dtype=np.float32) + np.float32(pos0))[:, None, None]
+    a = t * np.asarray(inv_freq, np.float32)[None, None, :]
+    c, s = np.cos(a), np.sin(a)
+    x0, x1 = x[..., 0].copy(), x[..., 1].copy()
+    x[..., 0], x[..., 1] = x0 * c - x1 * s, x1 * c + x0 * s
+    return oracle.round_bf16(x.reshape(np.shape(qk)))
+
+
+@pytest.mark.parametrize("mistake", ["rope_pairing", "norm_after_rope", "kv_head_map",
+                                     "no_q_norm"])
+def test_qwen3_fixture_catches_planted_mistakes(monkeypatch, mistake):
+    """Plausible misreadings planted in the oracle (on the CPU) fail the pin."""
+    cfg, w, g = _qwen3_fixture()
+    if mistake == "rope_pairing":
+        monkeypatch.setattr(oracle, "rope", _interleaved_rope)
+    elif mistake == "norm_after_rope":
+        # RoPE first, then the per-head norm: swap the two calls' effects.
+        real_norm, real_rope = oracle.multi_rmsnorm, oracle.rope
+        pending = {}
+
+        def norm_later(x, wt, d, eps):
+            pending["args"] = (wt, d, eps)
+            return np.asarray(x, np.float32)
+
+        def rope_then_norm(qk, inv, T, H, d, pos0=0):
+            wt, dd, eps = pending.pop("args")
+            return real_norm(real_rope(qk, inv, T, H, d, pos0), wt, dd, eps)
+
+        monkeypatch.setattr(oracle, "multi_rmsnorm", norm_later)
+        monkeypatch.setattr(oracle, "rope", rope_then_norm)
+    elif mistake == "kv_head_map":
+        # Query head h reading KV head h % Hkv instead of h // (Hq/Hkv).
+        real_flash, real_dec = oracle.flash_reference, oracle.decode_attention
+        hq, hkv = cfg["num_q_heads"], cfg["num_kv_heads"]
+        perm = np.array([(h % hkv) * (hq // hkv) + h // hkv for h in range(hq)])
+
+        def flash_mod(q, k, v, rows=None, nthreads=0):
+            inv = np.argsort(perm)
+            return real_flash(q[:, perm], k, v, rows, nthreads)[:, inv]
+
+        def dec_mod(q, k, v, pos, msl):
+            inv = np.argsort(perm)
+            s, ob, o = real_dec(q[perm], k, v, pos, msl)
+            return s[inv], ob[inv], o[inv]
+
+        monkeypatch.setattr(oracle, "flash_reference", flash_mod)
+        monkeypatch.setattr(oracle, "decode_attention", dec_mod)
+    elif mistake == "no_q_norm":
+        real_norm = oracle.multi_rmsnorm
+        calls = {"n": 0}
+
+        def skip_every_other(x, wt, d, eps):  # q is normalised first in each layer
+            calls["n"] += 1
+            return oracle.round_bf16(x) if calls["n"] % 2 == 1 else real_norm(x, wt, d, eps)
+
+        monkeypatch.setattr(oracle, "multi_rmsnorm", skip_every_other)
+    got = _qwen3_oracle_logits(cfg, w, g)
+    d = np.abs(got.astype(np.float64) - g["logits_rounded"])
+    print(f"{mistake}: max {d.max():.3g} mean {d.mean():.3g}")
+    assert d.max() > QWEN3_PIN_MAX and d.mean() > 5 * QWEN3_PIN_MEAN, \
+        f"{mistake}: max {d.max():.3g} mean {d.mean():.3g} passed the pin"

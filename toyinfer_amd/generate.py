@@ -33,7 +33,12 @@ def generate(model: Qwen3, tokenizer: Tokenizer, user_prompt, system_prompt=None
     if budget < 1:
         raise ValueError("no room left in max_seq_len for a generated token")
     model.set_sampling(temperature, top_k, top_p, seed)
-    model.prefill(torch.from_numpy(ids.view(np.int32)).to("cuda"), n)
+    # The prefill copies the ids on the model's own stream: keep the device
+    # tensor alive until that stream has passed it.
+    ids_d = torch.from_numpy(ids.view(np.int32)).to("cuda")
+    model.prefill(ids_d, n)
+    model.synchronize()
+    del ids_d
     out: List[int] = []
     done = 1  # the prefill's pick is generated token 1
     while True:

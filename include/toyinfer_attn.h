@@ -120,6 +120,27 @@ uint32_t toyinfer_decode_default_splits(uint32_t batch, uint32_t num_q_heads,
 size_t toyinfer_decode_workspace_bytes(uint32_t batch, uint32_t num_q_heads, uint32_t heads_dim,
                                        uint32_t num_splits);
 
+/* toyinfer_decode_attention_bf16 without a workspace argument: the split
+ * partials live in a device array inside this library (one copy per GPU,
+ * TOYINFER_DECODE_SCRATCH_BYTES, held until the process ends), so the call
+ * allocates nothing.  No counterpart in the reference: it is for callers that
+ * cannot allocate device memory (code under graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc).  Same arguments, checks, kernels
+ * and results as toyinfer_decode_attention_bf16 with the same split count;
+ * TOYINFER_ERR_WORKSPACE when toyinfer_decode_workspace_bytes(batch,
+ * num_q_heads, heads_dim, splits) exceeds TOYINFER_DECODE_SCRATCH_BYTES.
+ * Every call on one GPU uses that GPU's array: calls that overlap on one GPU
+ * (other streams, other threads) race and must be ordered by the caller.
+ * The array's address is looked up on the first call on each device (the
+ * device current at the call). */
+#define TOYINFER_DECODE_SCRATCH_BYTES (8u << 20)
+int toyinfer_decode_attention_bf16_noalloc(const void* q, const void* k_cache,
+                                           const void* v_cache, void* o, uint32_t batch,
+                                           uint32_t num_q_heads, uint32_t num_kv_heads,
+                                           uint32_t heads_dim, const uint32_t* seq_lens_d,
+                                           uint32_t seq_len, uint64_t kv_batch_stride,
+                                           uint32_t num_splits, void* stream);
+
 /* --------------------------------------------- Qwen3 pre-attention ops
  * bf16 tensors and gamma are 16-byte aligned (rows are moved with 16-byte
  * accesses); inv_freq 4-byte aligned. */

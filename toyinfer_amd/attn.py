@@ -44,6 +44,8 @@ SIGNATURES = {
                                              _u32, _vp]),
     "toyinfer_decode_attention_bf16": (_i32, [_vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _vp,
                                               _u32, _u64, _u32, _vp, _sz, _vp]),
+    "toyinfer_decode_attention_bf16_noalloc": (_i32, [_vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32,
+                                                      _vp, _u32, _u64, _u32, _vp]),
     "toyinfer_decode_default_splits": (_u32, [_u32, _u32, _u32, _u32, _u32]),
     "toyinfer_decode_workspace_bytes": (_sz, [_u32, _u32, _u32, _u32]),
     "toyinfer_precompute_freq_f32": (_i32, [_vp, _i32, _f32, _vp]),
@@ -220,6 +222,22 @@ def decode_attention_bf16(q, k_cache, v_cache, o, batch: int, num_q_heads: int,
                                               _ptr(seq_lens_d), seq_len, kv_batch_stride,
                                               num_splits, _ptr(workspace), ws_bytes,
                                               _stream(stream)))
+
+
+DECODE_SCRATCH_BYTES = 8 << 20  # TOYINFER_DECODE_SCRATCH_BYTES
+
+
+def decode_attention_bf16_noalloc(q, k_cache, v_cache, o, batch: int, num_q_heads: int,
+                                  num_kv_heads: int, heads_dim: int, seq_lens_d, seq_len: int,
+                                  kv_batch_stride: int, num_splits: int, stream=None) -> None:
+    """decode_attention_bf16 with the split partials in the library's own
+    per-GPU device array (no workspace argument, nothing allocated)."""
+    _check("decode_attention_bf16_noalloc",
+           LIB.toyinfer_decode_attention_bf16_noalloc(_ptr(q), _ptr(k_cache), _ptr(v_cache),
+                                                      _ptr(o), batch, num_q_heads, num_kv_heads,
+                                                      heads_dim, _ptr(seq_lens_d), seq_len,
+                                                      kv_batch_stride, num_splits,
+                                                      _stream(stream)))
 
 
 # ------------------------------------------------------------ prologue ops

@@ -6,6 +6,8 @@
 // synchronisation, which keeps them legal inside stream capture.
 #include <stdint.h>
 
+#include <mutex>
+
 #include "../../include/toyinfer_attn.h"
 #include "kernels.hpp"
 
@@ -69,6 +71,40 @@ void compat_partials(uint32_t hq, uint32_t hkv, uint32_t d, uint32_t sizing_len,
     part->o = o_buffer;
     part->o_head = d;
     part->o_split = d;
+}
+
+// Split-K workspace of toyinfer_decode_attention_bf16_noalloc: a file-scope
+// device array, one copy per GPU, held until the process ends.  Host code
+// never uses its name as an address: the per-device address comes from
+// hipGetSymbolAddress, taken once per device (with that device current) on
+// the entry point's first call there.  Every call on a GPU shares that
+// GPU's copy, so calls that overlap on one GPU race; nothing in it needs to
+// start at zero (each call writes every partial it later reads).
+constexpr size_t kDecodeScratchBytes = TOYINFER_DECODE_SCRATCH_BYTES;
+}  // namespace
+
+static __device__ __align__(256) unsigned char scratch[kDecodeScratchBytes];
+
+namespace {
+constexpr int kScratchDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_addr[kScratchDevices];
+
+int decode_scratch_address(void** out) {
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return from_hip(e);
+    if (dev < 0 || dev >= kScratchDevices) return TOYINFER_ERR_UNSUPPORTED;
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_addr[dev]) {
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return from_hip(e);
+        if (!p) return TOYINFER_ERR_HIP;
+        g_scratch_addr[dev] = p;
+    }
+    *out = g_scratch_addr[dev];
+    return TOYINFER_OK;
 }
 
 }  // namespace
@@ -246,27 +282,36 @@ size_t toyinfer_decode_workspace_bytes(uint32_t batch, uint32_t num_q_heads, uin
            heads * num_splits * heads_dim * sizeof(float);
 }
 
-int toyinfer_decode_attention_bf16(const void* q, const void* k_cache, const void* v_cache,
-                                   void* o, uint32_t batch, uint32_t num_q_heads,
-                                   uint32_t num_kv_heads, uint32_t heads_dim,
-                                   const uint32_t* seq_lens_d, uint32_t seq_len,
-                                   uint64_t kv_batch_stride, uint32_t num_splits,
-                                   void* workspace, size_t workspace_bytes, void* stream) {
+// Host checks of the batched decode; on success *splits holds the split
+// count the call uses.
+static int decode_batched_checks(const void* q, const void* k_cache, const void* v_cache,
+                                 void* o, uint32_t batch, uint32_t num_q_heads,
+                                 uint32_t num_kv_heads, uint32_t heads_dim,
+                                 const uint32_t* seq_lens_d, uint32_t seq_len,
+                                 uint64_t kv_batch_stride, uint32_t num_splits,
+                                 uint32_t* splits) {
     if (int st = check_heads(num_q_heads, num_kv_heads, heads_dim)) return st;
     if (batch == 0 || batch > 65535u || seq_len == 0) return TOYINFER_ERR_INVALID_ARGUMENT;
-    if (!q || !k_cache || !v_cache || !o || !workspace) return TOYINFER_ERR_INVALID_ARGUMENT;
+    if (!q || !k_cache || !v_cache || !o) return TOYINFER_ERR_INVALID_ARGUMENT;
     if (!aligned(q, 16) || !aligned(k_cache, 16) || !aligned(v_cache, 16) || !aligned(o, 2) ||
-        !aligned(workspace, 256) || (seq_lens_d && !aligned(seq_lens_d, 4)))
+        (seq_lens_d && !aligned(seq_lens_d, 4)))
         return TOYINFER_ERR_INVALID_ARGUMENT;
     if (batch > 1 && kv_batch_stride < (uint64_t)seq_len * num_kv_heads * heads_dim)
         return TOYINFER_ERR_INVALID_ARGUMENT;
     if (kv_batch_stride % 8 != 0) return TOYINFER_ERR_INVALID_ARGUMENT;
-    const uint32_t splits =
-        num_splits ? num_splits
-                   : decode_default_splits(batch, num_q_heads, num_kv_heads, heads_dim, seq_len);
-    if (splits > decode_max_splits()) return TOYINFER_ERR_INVALID_ARGUMENT;
-    if (workspace_bytes < toyinfer_decode_workspace_bytes(batch, num_q_heads, heads_dim, splits))
-        return TOYINFER_ERR_WORKSPACE;
+    *splits = num_splits
+                  ? num_splits
+                  : decode_default_splits(batch, num_q_heads, num_kv_heads, heads_dim, seq_len);
+    if (*splits > decode_max_splits()) return TOYINFER_ERR_INVALID_ARGUMENT;
+    return TOYINFER_OK;
+}
+
+static int decode_batched_launch(const void* q, const void* k_cache, const void* v_cache,
+                                 void* o, uint32_t batch, uint32_t num_q_heads,
+                                 uint32_t num_kv_heads, uint32_t heads_dim,
+                                 const uint32_t* seq_lens_d, uint32_t seq_len,
+                                 uint64_t kv_batch_stride, uint32_t splits, void* workspace,
+                                 void* stream) {
     DecodeProblem p{};
     p.q = static_cast<const uint16_t*>(q);
     p.k = static_cast<const uint16_t*>(k_cache);
@@ -293,6 +338,46 @@ int toyinfer_decode_attention_bf16(const void* q, const void* k_cache, const voi
     hipError_t e = launch_decode_split(p, part, st);
     if (e != hipSuccess) return from_hip(e);
     return from_hip(launch_decode_combine(p, part, static_cast<uint16_t*>(o), st));
+}
+
+int toyinfer_decode_attention_bf16(const void* q, const void* k_cache, const void* v_cache,
+                                   void* o, uint32_t batch, uint32_t num_q_heads,
+                                   uint32_t num_kv_heads, uint32_t heads_dim,
+                                   const uint32_t* seq_lens_d, uint32_t seq_len,
+                                   uint64_t kv_batch_stride, uint32_t num_splits,
+                                   void* workspace, size_t workspace_bytes, void* stream) {
+    uint32_t splits = 0;
+    if (int st = decode_batched_checks(q, k_cache, v_cache, o, batch, num_q_heads, num_kv_heads,
+                                       heads_dim, seq_lens_d, seq_len, kv_batch_stride,
+                                       num_splits, &splits))
+        return st;
+    if (!workspace || !aligned(workspace, 256)) return TOYINFER_ERR_INVALID_ARGUMENT;
+    if (workspace_bytes < toyinfer_decode_workspace_bytes(batch, num_q_heads, heads_dim, splits))
+        return TOYINFER_ERR_WORKSPACE;
+    return decode_batched_launch(q, k_cache, v_cache, o, batch, num_q_heads, num_kv_heads,
+                                 heads_dim, seq_lens_d, seq_len, kv_batch_stride, splits,
+                                 workspace, stream);
+}
+
+int toyinfer_decode_attention_bf16_noalloc(const void* q, const void* k_cache,
+                                           const void* v_cache, void* o, uint32_t batch,
+                                           uint32_t num_q_heads, uint32_t num_kv_heads,
+                                           uint32_t heads_dim, const uint32_t* seq_lens_d,
+                                           uint32_t seq_len, uint64_t kv_batch_stride,
+                                           uint32_t num_splits, void* stream) {
+    uint32_t splits = 0;
+    if (int st = decode_batched_checks(q, k_cache, v_cache, o, batch, num_q_heads, num_kv_heads,
+                                       heads_dim, seq_lens_d, seq_len, kv_batch_stride,
+                                       num_splits, &splits))
+        return st;
+    if (toyinfer_decode_workspace_bytes(batch, num_q_heads, heads_dim, splits) >
+        kDecodeScratchBytes)
+        return TOYINFER_ERR_WORKSPACE;
+    void* ws = nullptr;
+    if (int st = decode_scratch_address(&ws)) return st;
+    return decode_batched_launch(q, k_cache, v_cache, o, batch, num_q_heads, num_kv_heads,
+                                 heads_dim, seq_lens_d, seq_len, kv_batch_stride, splits, ws,
+                                 stream);
 }
 
 // ------------------------------------------------------ prologue operators

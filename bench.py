@@ -68,7 +68,7 @@ def traffic_bytes(workload):
     r, w = PMC_KIB[workload]
     return int(round((r * FETCH_SCALE + w * WRITE_SCALE) * 1024))
 WORKLOADS = ("all", "prefill", "prefill_fused", "decode_b8_l4096", "decode_b1_l32768",
-             "decode_step", "decode_contract", "proj_gemv", "proj_gemm", "qwen3_e2e",
+             "decode_step", "decode_contract", "decode_engine_lean", "proj_gemv", "proj_gemm", "qwen3_e2e",
              "sample", "copy_calibration")
 
 
@@ -280,31 +280,43 @@ def bench_decode_step(dev, stream, steps, warmup, hq=32, hkv=8, d=128, msl=40960
 
 
 def bench_decode_contract(dev, stream, steps, warmup, hq=32, hkv=8, d=128, msl=40960, pos=32767,
-                          per_graph=10):
+                          per_graph=12, lean=False):
     """The reference-contract decode the engine calls (attention_bf16_graph:
     device position, score/O_buffer/O outputs, captured in a graph) at a 32k
-    position of a 40960-row cache; each replay runs `per_graph` calls."""
+    position of a 40960-row cache; each replay runs `per_graph` calls.  With
+    lean=True the same call site through attention_bf16_graph_lean (score as
+    scratch, no probabilities)."""
     import torch
 
     from toyinfer_amd import attn, synth
 
-    k = to_dev(synth.normal_bf16(SEED + 30, "k", (msl, hkv, d)), dev)
-    v = to_dev(synth.normal_bf16(SEED + 30, "v", (msl, hkv, d)), dev)
+    sets = 4  # rotating caches (4 x 168 MB) so no call finds its cache in the Infinity Cache
+    kv = [(to_dev(synth.normal_bf16(SEED + 30 + r, "k", (msl, hkv, d)), dev),
+           to_dev(synth.normal_bf16(SEED + 30 + r, "v", (msl, hkv, d)), dev)) for r in range(sets)]
     q = to_dev(synth.normal_bf16(SEED + 30, "q", (hq, d)), dev)
     score = torch.empty((hq, msl), dtype=torch.float32, device=dev)
     ob = torch.empty((hq, d), dtype=torch.float32, device=dev)
     o = torch.empty((hq, d), dtype=torch.bfloat16, device=dev)
     pos_d = torch.tensor([pos], dtype=torch.int32, device=dev)
+    call = attn.attention_bf16_graph_lean if lean else attn.attention_bf16_graph
     with torch.cuda.stream(stream):
-        attn.attention_bf16_graph(q, k, v, score, ob, o, hq, hkv, d, pos_d, msl, stream)
+        call(q, kv[0][0], kv[0][1], score, ob, o, hq, hkv, d, pos_d, msl, stream)
     torch.cuda.synchronize()
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph, stream=stream):
-        for _ in range(per_graph):
-            attn.attention_bf16_graph(q, k, v, score, ob, o, hq, hkv, d, pos_d, msl, stream)
+        for c in range(per_graph):
+            kc, vc = kv[c % sets]
+            call(q, kc, vc, score, ob, o, hq, hkv, d, pos_d, msl, stream)
     ms = time_steps(lambda i: graph.replay(), max(5, steps // per_graph), warmup, stream) / per_graph
     kv_bytes = 2.0 * (pos + 1) * hkv * d * 2
     gbs = kv_bytes / (ms * 1e-3) / 1e9
+    if lean:
+        return {"workload": f"decode_engine_lean_graph_msl{msl}_pos{pos}_hq{hq}_hkv{hkv}_d{d}",
+                "entry": "toyinfer_attention_bf16_graph_lean", "steps": steps,
+                "ms_per_step": round(ms, 5), "value": round(gbs, 1), "unit": "GB/s",
+                "note": "KV bytes attended per call / call time; O and O_buffer written, "
+                        "score used as scratch (the engine never reads it)",
+                "roofline": roofline("hbm", gbs, PEAK_HBM_GBS, "GB/s")}
     return {"workload": f"decode_contract_graph_msl{msl}_pos{pos}_hq{hq}_hkv{hkv}_d{d}",
             "entry": "toyinfer_attention_bf16_graph", "steps": steps,
             "ms_per_step": round(ms, 5), "value": round(gbs, 1), "unit": "GB/s",
@@ -594,6 +606,8 @@ def main():
                                                  b=1, L=32768),
         "decode_step": lambda: bench_decode_step(dev, stream, max(50, args.steps * 2), 10),
         "decode_contract": lambda: bench_decode_contract(dev, stream, max(50, args.steps * 2), 2),
+        "decode_engine_lean": lambda: bench_decode_contract(dev, stream, max(50, args.steps * 2),
+                                                            2, lean=True),
         "proj_gemv": lambda: bench_proj_gemv(dev, stream, max(50, args.steps), 10),
         "proj_gemm": lambda: bench_proj_gemm(dev, stream, max(200, args.steps), 50),
         "sample": lambda: bench_sample(dev, stream, max(200, args.steps), 50),
@@ -631,7 +645,8 @@ def main():
     if not args.no_components:
         line["components"] = [comp[n]() for n in
                               ("prefill", "decode_b8_l4096", "decode_b1_l32768", "decode_step",
-                               "decode_contract", "proj_gemv", "proj_gemm", "sample",
+                               "decode_contract", "decode_engine_lean", "proj_gemv",
+                               "proj_gemm", "sample",
                                "qwen3_e2e")]
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(host, gpu_out, args.cpu_seconds)

@@ -105,6 +105,25 @@ void attention_bf16_graph(const bf16* __restrict__ Q, const bf16* __restrict__ K
                    "attention_bf16_graph");
 }
 
+// Extension: the engine's decode call site (src/transformer.cpp:569-573) with
+// `score` used as scratch (no probabilities written) and O_buffer / O as the
+// contract defines them; a drop-in replacement there, since the engine reads
+// neither score nor O_buffer afterwards.
+template <const uint32_t NUM_THREADS, const uint32_t TILE_SEQ>
+void attention_bf16_graph_lean(const bf16* __restrict__ Q, const bf16* __restrict__ Ks,
+                               const bf16* __restrict__ Vs, float* __restrict__ score,
+                               float* __restrict__ O_buffer, bf16* __restrict__ O,
+                               const uint32_t num_q_heads, const uint32_t num_kv_heads,
+                               const uint32_t heads_dim, const uint32_t* __restrict__ pos_d,
+                               const uint32_t max_seq_len, hipStream_t stream_d = nullptr) {
+    static_assert(NUM_THREADS > 0 && NUM_THREADS <= 1024 && NUM_THREADS % 32 == 0 && TILE_SEQ > 0,
+                  "illegal launch shape");
+    TOYINFER_CHECK(toyinfer_attention_bf16_graph_lean(Q, Ks, Vs, score, O_buffer, O, num_q_heads,
+                                                      num_kv_heads, heads_dim, pos_d,
+                                                      max_seq_len, stream_d),
+                   "attention_bf16_graph_lean");
+}
+
 // ------------------------------------------- QK-norm, RoPE and inv_freq
 
 // include/kernel_warpper.h:23, src/decode.cu:43-50 (legacy default stream).

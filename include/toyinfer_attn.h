@@ -97,6 +97,21 @@ int toyinfer_attention_bf16_graph(const void* Q, const void* Ks, const void* Vs,
                                   uint32_t num_kv_heads, uint32_t heads_dim,
                                   const uint32_t* pos_d, uint32_t max_seq_len, void* stream);
 
+/* The engine's decode call (src/transformer.cpp:569-573) without the parts of
+ * the contract the engine never reads (extension, same arguments as
+ * toyinfer_attention_bf16_graph, pos read from pos_d on the device): O =
+ * bf16 attention output and O_buffer = the same in fp32, as the contract
+ * defines them; score is scratch (it holds the split partials, not the
+ * probabilities) and may hold anything afterwards.  Only kernels are
+ * launched, so a captured graph replays it at each new position.  For a
+ * caller that reads score (the reference's tests), keep
+ * toyinfer_attention_bf16_graph. */
+int toyinfer_attention_bf16_graph_lean(const void* Q, const void* Ks, const void* Vs,
+                                       float* score, float* O_buffer, void* O,
+                                       uint32_t num_q_heads, uint32_t num_kv_heads,
+                                       uint32_t heads_dim, const uint32_t* pos_d,
+                                       uint32_t max_seq_len, void* stream);
+
 /* Batched split-K decode attention (extension; the reference runs one
  * sequence per attention_bf16 call).  Only O is produced.
  * q [B][Hq][D]; sequence b's cache rows at k_cache/v_cache + b*kv_batch_stride

@@ -128,6 +128,44 @@ def test_reference_contract_engine_cache(dev):
         check_compat(score, ob, o, q, k, v, pos, msl, f"graph pos={pos}")
 
 
+@pytest.mark.parametrize("hq,hkv,d,msl,positions", [
+    (2, 1, 64, 5, (0, 3, 4)),               # one split: partials in O_buffer / O rows
+    (8, 2, 128, 40, (37, 0)),
+    (16, 4, 64, 3001, (2999, 0, 1234)),     # several splits, 4-byte-aligned score rows
+    (32, 8, 128, 40960, (32767, 0, 40959)),  # the engine's cache size
+])
+def test_graph_lean(dev, hq, hkv, d, msl, positions):
+    """attention_bf16_graph_lean (the engine's call site, score as scratch):
+    captured once, replayed at each device position; O and O_buffer against
+    the oracle at the contract's tolerances, O at the north-star bar."""
+    print(f"[decode] lean graph {hq}/{hkv} D={d} msl={msl}", flush=True)
+    qf, kf, vf = oracle.make_attention_case(hq, hkv, d, msl, 0.03, 0.017)
+    qb, kb, vb = oracle.f32_to_bf16(qf), oracle.f32_to_bf16(kf), oracle.f32_to_bf16(vf)
+    q, k, v = oracle.bf16_to_f32(qb), oracle.bf16_to_f32(kb), oracle.bf16_to_f32(vb)
+    qd, kd, vd = H.to_dev_bf16(qb, dev), H.to_dev_bf16(kb, dev), H.to_dev_bf16(vb, dev)
+    score, ob, o = dirty_buffers(hq, d, msl, dev)
+    pos_d = torch.zeros(1, dtype=torch.int32, device=dev)
+    stream = torch.cuda.Stream()
+    with torch.cuda.stream(stream):
+        attn.attention_bf16_graph_lean(qd, kd, vd, score, ob, o, hq, hkv, d, pos_d, msl, stream)
+    H.sync()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        attn.attention_bf16_graph_lean(qd, kd, vd, score, ob, o, hq, hkv, d, pos_d, msl, stream)
+    for pos in positions:
+        pos_d.fill_(pos)
+        H.sync()
+        graph.replay()
+        H.sync()
+        _, exp_ob, exp_o = oracle.decode_attention(q, k, v, pos, msl)
+        got_o = H.bf16_bits_to_f32(H.from_dev_bf16(o))
+        H.check_close(ob.cpu().numpy(), exp_ob, 5e-2, 5e-2, f"lean pos={pos} o_buffer")
+        H.check_close(got_o, H.bf16_bits_to_f32(exp_o), 5e-2, 5e-2, f"lean pos={pos} output")
+        H.check_bar(got_o, H.bf16_bits_to_f32(exp_o), f"lean pos={pos} output")
+        # O is O_buffer rounded to bf16, as in the contract.
+        assert np.array_equal(H.from_dev_bf16(o), oracle.f32_to_bf16(ob.cpu().numpy()))
+
+
 def run_batched(qb, kb, vb, lens, dev, splits=0, seq_lens_on_device=False):
     b, hq, d = qb.shape
     cap, hkv = kb.shape[1], kb.shape[2]

@@ -42,6 +42,8 @@ SIGNATURES = {
                                        _u32, _vp]),
     "toyinfer_attention_bf16_graph": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32, _vp,
                                              _u32, _vp]),
+    "toyinfer_attention_bf16_graph_lean": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32,
+                                                  _vp, _u32, _vp]),
     "toyinfer_decode_attention_bf16": (_i32, [_vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _vp,
                                               _u32, _u64, _u32, _vp, _sz, _vp]),
     "toyinfer_decode_attention_bf16_noalloc": (_i32, [_vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32,
@@ -189,6 +191,17 @@ def attention_bf16_graph(Q, Ks, Vs, score, O_buffer, O, num_q_heads: int, num_kv
                                              _ptr(O_buffer), _ptr(O), num_q_heads, num_kv_heads,
                                              heads_dim, _ptr(pos_d), max_seq_len,
                                              _stream(stream)))
+
+
+def attention_bf16_graph_lean(Q, Ks, Vs, score, O_buffer, O, num_q_heads: int,
+                              num_kv_heads: int, heads_dim: int, pos_d, max_seq_len: int,
+                              stream=None) -> None:
+    """The engine's decode call with score as scratch: O and O_buffer only."""
+    _check("attention_bf16_graph_lean",
+           LIB.toyinfer_attention_bf16_graph_lean(_ptr(Q), _ptr(Ks), _ptr(Vs), _ptr(score),
+                                                  _ptr(O_buffer), _ptr(O), num_q_heads,
+                                                  num_kv_heads, heads_dim, _ptr(pos_d),
+                                                  max_seq_len, _stream(stream)))
 
 
 def decode_default_splits(batch: int, num_q_heads: int, num_kv_heads: int, heads_dim: int,

@@ -267,6 +267,37 @@ int toyinfer_attention_bf16_graph(const void* Q, const void* Ks, const void* Vs,
                          kLenDevicePos, pos_d, 0, max_seq_len, stream);
 }
 
+int toyinfer_attention_bf16_graph_lean(const void* Q, const void* Ks, const void* Vs,
+                                       float* score, float* O_buffer, void* O,
+                                       uint32_t num_q_heads, uint32_t num_kv_heads,
+                                       uint32_t heads_dim, const uint32_t* pos_d,
+                                       uint32_t max_seq_len, void* stream) {
+    if (int st = decode_common_checks(Q, Ks, Vs, score, O_buffer, O, num_q_heads, num_kv_heads,
+                                      heads_dim, max_seq_len))
+        return st;
+    if (!pos_d || !aligned(pos_d, 4)) return TOYINFER_ERR_INVALID_ARGUMENT;
+    DecodeProblem p{};
+    p.q = static_cast<const uint16_t*>(Q);
+    p.k = static_cast<const uint16_t*>(Ks);
+    p.v = static_cast<const uint16_t*>(Vs);
+    p.batch = 1;
+    p.hq = num_q_heads;
+    p.hkv = num_kv_heads;
+    p.d = heads_dim;
+    p.len_mode = kLenDevicePos;
+    p.len_dev = pos_d;
+    p.len_cap = max_seq_len;
+    DecodePartials part{};
+    compat_partials(num_q_heads, num_kv_heads, heads_dim, max_seq_len, max_seq_len, score,
+                    O_buffer, O, &p.splits, &part);
+    hipStream_t st = as_stream(stream);
+    hipError_t e = launch_decode_split(p, part, st);
+    if (e != hipSuccess) return from_hip(e);
+    // Partials in score rows (or O_buffer/O rows) are 4-byte aligned only.
+    return from_hip(launch_decode_combine(p, part, static_cast<uint16_t*>(O), st, O_buffer,
+                                          false));
+}
+
 uint32_t toyinfer_decode_default_splits(uint32_t batch, uint32_t num_q_heads,
                                         uint32_t num_kv_heads, uint32_t heads_dim,
                                         uint32_t seq_len) {

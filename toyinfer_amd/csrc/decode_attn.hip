@@ -381,10 +381,15 @@ __device__ __forceinline__ void merge_partial(float& M, float& den, float* acc, 
     M = Mn;
 }
 
-template <int D>
+// VEC: partial rows are 8-byte aligned (the batched workspace), so a lane's
+// two dims load as one float2; else (partials in the reference contract's
+// score rows, 4-byte aligned) as two floats.  o_f32 (optional) receives the
+// fp32 result as well.
+template <int D, bool VEC>
 __global__ __launch_bounds__(64 * kCombineMaxWaves) void decode_combine_kernel(DecodePartials part,
                                                                              uint32_t splits,
-                                                                             uint16_t* o) {
+                                                                             uint16_t* o,
+                                                                             float* o_f32) {
     constexpr int DPL = D / 64;
     constexpr int U = 8;
     __shared__ float s_acc[kCombineMaxWaves][D];
@@ -407,12 +412,13 @@ __global__ __launch_bounds__(64 * kCombineMaxWaves) void decode_combine_kernel(D
             m[u] = ml[2 * sp];
             l[u] = ml[2 * sp + 1];
             const float* src = po + (int64_t)sp * part.o_split;
-            if constexpr (DPL == 2) {
+            if constexpr (DPL == 2 && VEC) {
                 const float2 x = *reinterpret_cast<const float2*>(src);
                 v[u][0] = x.x;
                 v[u][1] = x.y;
             } else {
-                v[u][0] = src[0];
+#pragma unroll
+                for (int e = 0; e < DPL; ++e) v[u][e] = src[e];
             }
         }
 #pragma unroll
@@ -438,6 +444,10 @@ __global__ __launch_bounds__(64 * kCombineMaxWaves) void decode_combine_kernel(D
         merge_partial(Mt, dt, tot, DPL, s_ml[w][0], s_ml[w][1], x);
     }
     const float inv = dt > 0.0f ? 1.0f / dt : 0.0f;
+    if (o_f32) {
+#pragma unroll
+        for (int e = 0; e < DPL; ++e) o_f32[bh * D + DPL * lane + e] = tot[e] * inv;
+    }
     if constexpr (DPL == 2)
         *reinterpret_cast<uint32_t*>(o + bh * D + 2 * lane) = pack_bf16x2(tot[0] * inv, tot[1] * inv);
     else
@@ -651,7 +661,7 @@ hipError_t launch_decode_split(const DecodeProblem& p, const DecodePartials& par
 }
 
 hipError_t launch_decode_combine(const DecodeProblem& p, const DecodePartials& part, uint16_t* o,
-                                 hipStream_t stream) {
+                                 hipStream_t stream, float* o_f32, bool aligned8) {
     // One wave per eight splits (one round of loads each), up to 16 waves.
     const uint32_t heads = p.batch * p.hq;
     uint32_t waves = (p.splits + 7) / 8;
@@ -659,9 +669,14 @@ hipError_t launch_decode_combine(const DecodeProblem& p, const DecodePartials& p
     if (waves < 1) waves = 1;
     const dim3 grid(heads), block(64 * waves);
     if (p.d == 64)
-        hipLaunchKernelGGL(decode_combine_kernel<64>, grid, block, 0, stream, part, p.splits, o);
+        hipLaunchKernelGGL((decode_combine_kernel<64, false>), grid, block, 0, stream, part,
+                           p.splits, o, o_f32);
+    else if (aligned8)
+        hipLaunchKernelGGL((decode_combine_kernel<128, true>), grid, block, 0, stream, part,
+                           p.splits, o, o_f32);
     else
-        hipLaunchKernelGGL(decode_combine_kernel<128>, grid, block, 0, stream, part, p.splits, o);
+        hipLaunchKernelGGL((decode_combine_kernel<128, false>), grid, block, 0, stream, part,
+                           p.splits, o, o_f32);
     return hipGetLastError();
 }
 

@@ -44,9 +44,11 @@ struct DecodeProblem {
 // Split pass: grid (splits, Hkv * head groups, B).
 hipError_t launch_decode_split(const DecodeProblem& p, const DecodePartials& part,
                                hipStream_t stream);
-// Combine partials into o [B][Hq][D] bf16.
+// Combine partials into o [B][Hq][D] bf16 (and o_f32 in fp32 when given);
+// aligned8: every partial row starts 8-byte aligned.
 hipError_t launch_decode_combine(const DecodeProblem& p, const DecodePartials& part, uint16_t* o,
-                                 hipStream_t stream);
+                                 hipStream_t stream, float* o_f32 = nullptr,
+                                 bool aligned8 = true);
 // Reference-contract finaliser (B == 1): combine partials, write O_buffer
 // (fp32), O (bf16) and score [Hq][msl] (probabilities, zeros past pos).
 hipError_t launch_decode_finalize_compat(const DecodeProblem& p, const DecodePartials& part,

@@ -65,8 +65,11 @@ __device__ __forceinline__ void split_range(uint32_t L, uint32_t splits, uint32_
     *end = *begin + per + (split < rem ? 1u : 0u);
 }
 
-// Row-major V tile of one wave in LDS: element (row, col) at
-// row*D + 8*((col/8) ^ swz(row)) + col%8.
+// Row-major K/V tile of one wave in LDS: element (row, col) at
+// row*D + 8*((col/8) ^ swz(row)) + col%8.  With swz(r) = 2r mod D/8 the
+// tile's stores, the K operand reads and the transposing V reads all run
+// without bank conflicts (measured with SQ_LDS_BANK_CONFLICT on each access
+// pattern alone).
 template <int D>
 __device__ __forceinline__ int vt_swz(int row) {
     return (2 * row) & (D / 8 - 1);
@@ -90,7 +93,9 @@ __global__ __launch_bounds__(256, 3) void decode_split_kernel(DecodeProblem p, D
     constexpr int V_ELEMS = kDecWaveRows * D;
     // LDS: per-wave V tiles during the loop, the cross-wave merge afterwards.
     constexpr int LDS_BYTES_V = kDecWaves * V_ELEMS * 2;
-    constexpr int LDS_BYTES_O = kDecWaves * kDecMaxHeads * D * 4;
+    constexpr int OP = D + 4;  // merge row pitch (floats): the 16-byte stores of 4 head rows
+                               // land in distinct banks
+    constexpr int LDS_BYTES_O = kDecWaves * kDecMaxHeads * OP * 4;
     __shared__ __align__(16) unsigned char s_raw[LDS_BYTES_V > LDS_BYTES_O ? LDS_BYTES_V
                                                                             : LDS_BYTES_O];
     __shared__ float s_ml[kDecWaves][kDecMaxHeads][2];
@@ -260,7 +265,7 @@ __global__ __launch_bounds__(256, 3) void decode_split_kernel(DecodeProblem p, D
     if ((uint32_t)n < nh) {
 #pragma unroll
         for (int db = 0; db < NDB; ++db)
-            *reinterpret_cast<f32x4_t*>(s_o + (wave * kDecMaxHeads + n) * D + 16 * db + 4 * g) = acc[db];
+            *reinterpret_cast<f32x4_t*>(s_o + (wave * kDecMaxHeads + n) * OP + 16 * db + 4 * g) = acc[db];
         if (g == 0) {
             s_ml[wave][n][0] = m_run;
             s_ml[wave][n][1] = l_run;
@@ -280,7 +285,7 @@ __global__ __launch_bounds__(256, 3) void decode_split_kernel(DecodeProblem p, D
         for (int w = 0; w < kDecWaves; ++w) {
             const float mw = s_ml[w][hs][0];
             const float sc = mw == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mw - M);
-            o += sc * *reinterpret_cast<const f32x4_t*>(s_o + (w * kDecMaxHeads + hs) * D + d);
+            o += sc * *reinterpret_cast<const f32x4_t*>(s_o + (w * kDecMaxHeads + hs) * OP + d);
             l = fmaf(sc, s_ml[w][hs][1], l);
         }
         const int64_t bh = bh0 + hs;

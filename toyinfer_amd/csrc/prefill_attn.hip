@@ -65,8 +65,11 @@ struct PfShape {
 // buffer loads that write LDS directly (each instruction fills 1 KiB: 64
 // lanes x 16 bytes in lane order, so a lane loads the global chunk that
 // belongs at its LDS slot).
-//   K rows (A operand reads, 8 rows per cycle): chunk c at c ^ (row & 7).
-//   V rows (transposing reads of 4 rows x 32 bytes): chunk c at c ^ 2*(row & 3).
+//   K rows (A operand reads): chunk c at c ^ (row mod D/8).
+//   V rows (transposing reads, 4 rows x 64 bytes per half-wave at D = 128):
+//   chunk c at c ^ 4*(row & 3) (D = 128), c ^ 2*(row & 3) (D = 64).
+// SQ_LDS_BANK_CONFLICT reads 0 for this kernel with these maps (the earlier
+// c ^ (row & 7) / c ^ 2*(row & 3) gave 6.8e7 conflict cycles per launch).
 template <int D>
 struct DmaShape {
     static constexpr int CPR = D / 8;
@@ -76,8 +79,10 @@ struct DmaShape {
     static constexpr int KSTEPS = D / 16;
     static constexpr int DBLK = D / 32;
 };
-__device__ __forceinline__ int k_swz(int row) { return row & 7; }
-__device__ __forceinline__ int v_swz(int row) { return 2 * (row & 3); }
+template <int D>
+__device__ __forceinline__ int k_swz(int row) { return row & (D / 8 - 1); }
+template <int D>
+__device__ __forceinline__ int v_swz(int row) { return D == 128 ? 4 * (row & 3) : 2 * (row & 3); }
 
 // Issue this wave's share of tile `tile_off` (K and V) into LDS tiles sk, sv.
 template <int D>
@@ -91,8 +96,8 @@ __device__ __forceinline__ void dma_tile(__amdgpu_buffer_rsrc_t rk, __amdgpu_buf
         const int blk = wave + (kPfThreads / 64) * j;
         const int slot = 64 * blk + lane;                // 16-byte slot within the tile
         const int row = slot / P::CPR, phys = slot % P::CPR;
-        const uint32_t koff = tile_off + row * row_bytes + 16 * (phys ^ k_swz(row));
-        const uint32_t vof = tile_off + row * row_bytes + 16 * (phys ^ v_swz(row));
+        const uint32_t koff = tile_off + row * row_bytes + 16 * (phys ^ k_swz<D>(row));
+        const uint32_t vof = tile_off + row * row_bytes + 16 * (phys ^ v_swz<D>(row));
         __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (__attribute__((address_space(3))) void*)(sk + 512 * blk), 16, koff, 0, 0, 0);
         __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (__attribute__((address_space(3))) void*)(sv + 512 * blk), 16, vof, 0, 0, 0);
     }
@@ -267,13 +272,13 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(PrefillProblem p
     const int s16 = lane & 15, g16 = lane >> 4;
     int k_off[P::KSTEPS], v_off[P::DBLK];
 #pragma unroll
-    for (int ks = 0; ks < P::KSTEPS; ++ks) k_off[ks] = ql * D + 8 * ((2 * ks + kg) ^ k_swz(ql));
+    for (int ks = 0; ks < P::KSTEPS; ++ks) k_off[ks] = ql * D + 8 * ((2 * ks + kg) ^ k_swz<D>(ql));
     {
         const int vrow = 4 * kg + (s16 >> 2);
 #pragma unroll
         for (int db = 0; db < P::DBLK; ++db) {
             const int c = 4 * db + 2 * (g16 & 1) + ((s16 & 3) >> 1);
-            v_off[db] = vrow * D + 8 * (c ^ v_swz(vrow)) + 4 * (s16 & 1);
+            v_off[db] = vrow * D + 8 * (c ^ v_swz<D>(vrow)) + 4 * (s16 & 1);
         }
     }
     __syncthreads();
@@ -640,46 +645,38 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_splitkv_kernel(PrefillP
             s_ml[wave][ql][1] = l_tot;
         }
         lds_barrier();
-        // Final pass: lane (row 8*wave + lane%8, columns 16*(lane/8) .. +15);
-        // eight consecutive lanes read eight rows, again in distinct bank
-        // groups.  Every load is unconditional: a wave that saw no key has
-        // o = 0 and weight 0.
-        constexpr int PER = D / 8;
-        const int row = 8 * wave + (lane & 7), part = lane >> 3;
-        const uint32_t orow_q = q0 + row;
-        float M = -INFINITY;
+        // Final pass: float4 f = tid + 256 k of the 32 x D/4 output block
+        // (row f / (D/4), column group f % (D/4)), so each 16 lanes read 256
+        // contiguous bytes of one merge row: no bank conflicts.  Every load is
+        // unconditional: a wave that saw no key has o = 0 and weight 0.
+        constexpr int C4 = D / 4;
+        constexpr int NF = kSkBM * C4 / kPfThreads;
 #pragma unroll
-        for (int w = 0; w < 4; ++w) M = fmaxf(M, s_ml[w][row][0]);
-        float wgt[4], den = 0.0f;
+        for (int k = 0; k < NF; ++k) {
+            const int f = threadIdx.x + kPfThreads * k;
+            const int row = f / C4, c4 = f % C4;
+            float M = -INFINITY;
 #pragma unroll
-        for (int w = 0; w < 4; ++w) {
-            const float mw = s_ml[w][row][0];
-            wgt[w] = mw == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mw - M);
-            den = fmaf(wgt[w], s_ml[w][row][1], den);
-        }
-        const float inv = 1.0f / den;
-        float acc[PER];
+            for (int w = 0; w < 4; ++w) M = fmaxf(M, s_ml[w][row][0]);
+            float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            float den = 0.0f;
 #pragma unroll
-        for (int e = 0; e < PER; ++e) acc[e] = 0.0f;
-#pragma unroll
-        for (int w = 0; w < 4; ++w) {
-            const float* src = s_o + (w * kSkBM + row) * P::OPITCH + part * PER;
-#pragma unroll
-            for (int e = 0; e < PER; e += 4) {
-                const float4 x = *reinterpret_cast<const float4*>(src + e);
-                acc[e] = fmaf(wgt[w], x.x, acc[e]);
-                acc[e + 1] = fmaf(wgt[w], x.y, acc[e + 1]);
-                acc[e + 2] = fmaf(wgt[w], x.z, acc[e + 2]);
-                acc[e + 3] = fmaf(wgt[w], x.w, acc[e + 3]);
+            for (int w = 0; w < 4; ++w) {
+                const float mw = s_ml[w][row][0];
+                const float wgt = mw == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mw - M);
+                den = fmaf(wgt, s_ml[w][row][1], den);
+                const float4 x = *reinterpret_cast<const float4*>(s_o + (w * kSkBM + row) * P::OPITCH + 4 * c4);
+                acc.x = fmaf(wgt, x.x, acc.x);
+                acc.y = fmaf(wgt, x.y, acc.y);
+                acc.z = fmaf(wgt, x.z, acc.z);
+                acc.w = fmaf(wgt, x.w, acc.w);
             }
-        }
-        if (orow_q < p.s) {
-            uint16_t* orow = p.o + ((int64_t)orow_q * p.hq + h) * D + part * PER;
-#pragma unroll
-            for (int e = 0; e < PER; e += 8)
-                *reinterpret_cast<uint4*>(orow + e) = make_uint4(
-                    pack_bf16x2(acc[e] * inv, acc[e + 1] * inv), pack_bf16x2(acc[e + 2] * inv, acc[e + 3] * inv),
-                    pack_bf16x2(acc[e + 4] * inv, acc[e + 5] * inv), pack_bf16x2(acc[e + 6] * inv, acc[e + 7] * inv));
+            const uint32_t orow_q = q0 + row;
+            if (orow_q < p.s) {
+                const float inv = 1.0f / den;
+                *reinterpret_cast<uint2*>(p.o + ((int64_t)orow_q * p.hq + h) * D + 4 * c4) =
+                    make_uint2(pack_bf16x2(acc.x * inv, acc.y * inv), pack_bf16x2(acc.z * inv, acc.w * inv));
+            }
         }
         if (!more) break;
         lds_barrier();  // the merge buffer's reads are done before tiles are written again

@@ -153,7 +153,9 @@ __device__ __forceinline__ void load_q(bf16x8_t (&qf)[PfShape<D>::KSTEPS], const
     const uint32_t qc = qq < p.s ? qq : p.s - 1;
     const uint16_t* qrow = p.q + ((int64_t)qc * p.hq + h) * D + 8 * kg;
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) raw[ks] = ldg16(qrow + ks * 16);
+    // Q is read once: the non-temporal hint keeps it from displacing the
+    // K/V tiles that every query tile of the KV head re-reads from L2.
+    for (int ks = 0; ks < KS; ++ks) raw[ks] = ldg16_nt(qrow + ks * 16);
     if constexpr (!FUSED) {
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks) qf[ks] = as_bf16x8(raw[ks]);  // rows past S: row S-1, never stored

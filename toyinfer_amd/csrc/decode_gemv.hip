@@ -80,8 +80,45 @@ __global__ __launch_bounds__(kDgThreads) void decode_gemv_kernel(DecodeGemvArgs 
         load_trip(c < nchunk ? c * 16 : kDgOob, c2 < nchunk ? c2 * 16 : kDgOob);
     }
 
-    // Stage the input (normalised if asked) in LDS.
-    if constexpr (NORM) {
+    // Stage the input (normalised if asked) in LDS.  With up to four chunks
+    // per lane (N <= 8192) the input and norm weights are read from global
+    // memory once, the raw chunks parked in LDS for the normalising pass.
+    if (NORM && nchunk <= 4 * kDgThreads) {
+        constexpr int MC = 4;
+        uint4 gv[MC];
+        float ss = 0.0f;
+#pragma unroll
+        for (int k = 0; k < MC; ++k) {
+            const uint32_t c = threadIdx.x + k * kDgThreads;
+            if (c < nchunk) {
+                const uint4 v = ldg16(a.x + 8 * c);
+                gv[k] = ldg16(a.norm_w + 8 * c);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const uint32_t wd = word_of(v, i);
+                    ss = fmaf(bf16_lo(wd), bf16_lo(wd), ss);
+                    ss = fmaf(bf16_hi(wd), bf16_hi(wd), ss);
+                }
+                *reinterpret_cast<uint4*>(s_x + 8 * c) = v;
+            }
+        }
+        const float inv = rsqrtf(fmaf(dg_block_sum(ss, s_red), 1.0f / (float)N, a.eps));
+#pragma unroll
+        for (int k = 0; k < MC; ++k) {
+            const uint32_t c = threadIdx.x + k * kDgThreads;
+            if (c < nchunk) {
+                const uint4 v = *reinterpret_cast<const uint4*>(s_x + 8 * c), g = gv[k];
+                uint4 o;
+                uint32_t* ow = reinterpret_cast<uint32_t*>(&o);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const uint32_t p = word_of(v, i), q = word_of(g, i);
+                    ow[i] = pack_bf16x2(bf16_lo(p) * inv * bf16_lo(q), bf16_hi(p) * inv * bf16_hi(q));
+                }
+                *reinterpret_cast<uint4*>(s_x + 8 * c) = o;
+            }
+        }
+    } else if constexpr (NORM) {
         float ss = 0.0f;
         for (uint32_t c = threadIdx.x; c < nchunk; c += kDgThreads) {
             const uint4 v = ldg16(a.x + 8 * c);
@@ -151,6 +188,138 @@ __global__ __launch_bounds__(kDgThreads) void decode_gemv_kernel(DecodeGemvArgs 
     }
 }
 
+// Wave-autonomous form for the harness's layer sizes (N <= 4096): 4-wave
+// workgroups, each wave owning RPW output rows (RPW gate and RPW up rows for
+// SwiGLU) whole.  A lane loads chunks l, l+64, ... of the input and of each
+// of its rows in one round (NCH = ceil(N/512) chunks per row), so a wave
+// needs no LDS and no barrier: the RMSNorm statistics and every row's dot
+// product are wave sums.  A one-token projection is latency-bound, so the
+// grid aims at about 2048 waves (8 per CU) with every load of a wave issued
+// before its first use.  Measured on MI355X for Qwen3-0.6B's shapes
+// (4-12 MB of weights): 3.4-4.9 us per projection, against 4-6 us for the
+// block-cooperative kernel below; 16-wave workgroups on 32-48 CUs stream the
+// same matrices from HBM at under half the rate (8.5 us for 4 MB).  The
+// residual row is read at the start, with the weights.
+constexpr int kDwWaves = 4;
+
+template <int RPW, int NCH, bool NORM, int EPI>
+__global__ __launch_bounds__(64 * kDwWaves) void decode_gemv_wave_kernel(DecodeGemvArgs a) {
+    constexpr int NR = EPI == kDgSwiglu ? 2 * RPW : RPW;
+    const int lane = threadIdx.x & 63;
+    const uint32_t wave = blockIdx.x * kDwWaves + (threadIdx.x >> 6);
+    const uint32_t N = a.n;
+    uint32_t r0 = wave * RPW;
+    int seg = 0;
+    while (seg + 1 < a.nseg && r0 >= (a.rows[seg] + RPW - 1) / RPW * RPW) {
+        r0 -= (a.rows[seg] + RPW - 1) / RPW * RPW;
+        ++seg;
+    }
+    if (r0 >= a.rows[seg]) return;  // a grid's last waves may have no rows
+    const uint32_t nrows = min((uint32_t)RPW, a.rows[seg] - r0);
+    const uint32_t row_bytes = 2 * N;
+    __amdgpu_buffer_rsrc_t rw[EPI == kDgSwiglu ? 2 : 1];
+    rw[0] = make_rsrc(a.w[seg] + (size_t)r0 * N, nrows * row_bytes);
+    if constexpr (EPI == kDgSwiglu) rw[1] = make_rsrc(a.w[1] + (size_t)r0 * N, nrows * row_bytes);
+    const __amdgpu_buffer_rsrc_t rx = make_rsrc(a.x, row_bytes);
+    uint4 wv[NR][NCH], xv[NCH], gv[NCH];
+#pragma unroll
+    for (int k = 0; k < NCH; ++k) {
+        // Chunks past the row's end read zeros: their offset is moved past
+        // every buffer's range (not into the next row).
+        const uint32_t off = 16 * (lane + 64 * k);
+        const bool in = off < row_bytes;
+#pragma unroll
+        for (int r = 0; r < NR; ++r)
+            wv[r][k] = buf_load16(rw[r / RPW], in ? (r % RPW) * row_bytes + off : 0x80000000u);
+        xv[k] = buf_load16(rx, off);
+        if constexpr (NORM) gv[k] = buf_load16(make_rsrc(a.norm_w, row_bytes), off);
+    }
+    uint16_t res = 0;
+    if (EPI == kDgResidual && (uint32_t)lane < nrows) res = a.y[seg][r0 + lane];
+
+    if constexpr (NORM) {
+        float ss = 0.0f;
+#pragma unroll
+        for (int k = 0; k < NCH; ++k)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t wd = word_of(xv[k], i);
+                ss = fmaf(bf16_lo(wd), bf16_lo(wd), ss);
+                ss = fmaf(bf16_hi(wd), bf16_hi(wd), ss);
+            }
+        const float inv = rsqrtf(fmaf(wave_sum(ss), 1.0f / (float)N, a.eps));
+#pragma unroll
+        for (int k = 0; k < NCH; ++k) {
+            uint32_t* ow = reinterpret_cast<uint32_t*>(&xv[k]);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t p = ow[i], q = word_of(gv[k], i);
+                ow[i] = pack_bf16x2(bf16_lo(p) * inv * bf16_lo(q), bf16_hi(p) * inv * bf16_hi(q));
+            }
+        }
+    }
+    float sum[NR];
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+        float acc = 0.0f;
+#pragma unroll
+        for (int k = 0; k < NCH; ++k) acc = dot8(wv[r][k], xv[k], acc);
+        sum[r] = wave_sum(acc);
+    }
+    // Lane r writes row r (sums are in every lane; pick lane r's by a chain
+    // of selects, no dynamic register indexing).
+    float v = 0.0f, u = 0.0f;
+#pragma unroll
+    for (int r = 0; r < RPW; ++r) {
+        v = lane == r ? sum[r] : v;
+        if constexpr (EPI == kDgSwiglu) u = lane == r ? sum[RPW + r] : u;
+    }
+    if ((uint32_t)lane < nrows) {
+        const uint32_t m = r0 + lane;
+        if constexpr (EPI == kDgPlain) {
+            a.y[seg][m] = f32_to_bf16(v);
+        } else if constexpr (EPI == kDgResidual) {
+            a.y[seg][m] = f32_to_bf16(bf16_to_f32(res) + bf16_round(v));
+        } else {
+            const float g = bf16_round(v), up = bf16_round(u);
+            a.y[0][m] = f32_to_bf16(up * (g * (1.0f / (1.0f + expf(-g)))));
+        }
+    }
+}
+
+template <int RPW, int NCH, bool NORM, int EPI>
+hipError_t dw_launch(const DecodeGemvArgs& a, hipStream_t stream) {
+    uint32_t waves = 0;
+    for (int s = 0; s < a.nseg; ++s) waves += (a.rows[s] + RPW - 1) / RPW;
+    const uint32_t groups = (waves + kDwWaves - 1) / kDwWaves;
+    decode_gemv_wave_kernel<RPW, NCH, NORM, EPI><<<groups, 64 * kDwWaves, 0, stream>>>(a);
+    return hipGetLastError();
+}
+
+template <int NCH, bool NORM, int EPI>
+hipError_t dw_rows(const DecodeGemvArgs& a, uint32_t total, hipStream_t stream) {
+    // Rows per wave: about 2048 waves in the grid, at most 16 row loads per
+    // lane.
+    constexpr int PAIRS = EPI == kDgSwiglu ? 2 : 1;
+    constexpr int CAP = 16 / (NCH * PAIRS) >= 8 ? 8 : 16 / (NCH * PAIRS) >= 4 ? 4 : 16 / (NCH * PAIRS) >= 2 ? 2 : 1;
+    const uint32_t want = total / 2048;
+    const int rpw = want >= 8 ? 8 : want >= 4 ? 4 : want >= 2 ? 2 : 1;
+    const int r = rpw < CAP ? rpw : CAP;
+    if (r >= 8 && CAP >= 8) return dw_launch<(CAP >= 8 ? 8 : 1), NCH, NORM, EPI>(a, stream);
+    if (r >= 4 && CAP >= 4) return dw_launch<(CAP >= 4 ? 4 : 1), NCH, NORM, EPI>(a, stream);
+    if (r >= 2 && CAP >= 2) return dw_launch<(CAP >= 2 ? 2 : 1), NCH, NORM, EPI>(a, stream);
+    return dw_launch<1, NCH, NORM, EPI>(a, stream);
+}
+
+template <bool NORM, int EPI>
+hipError_t dw_dispatch(const DecodeGemvArgs& a, uint32_t total, hipStream_t stream) {
+    const uint32_t nch = (a.n / 8 + 63) / 64;
+    if (nch <= 2) return dw_rows<2, NORM, EPI>(a, total, stream);
+    if (nch <= 4) return dw_rows<4, NORM, EPI>(a, total, stream);
+    if (nch <= 6) return dw_rows<6, NORM, EPI>(a, total, stream);
+    return dw_rows<8, NORM, EPI>(a, total, stream);
+}
+
 template <int RB, bool NORM, int EPI>
 hipError_t dg_launch(const DecodeGemvArgs& a, uint32_t total_groups, hipStream_t stream) {
     decode_gemv_kernel<RB, NORM, EPI><<<total_groups, kDgThreads, 2 * a.n, stream>>>(a);
@@ -161,6 +330,7 @@ template <bool NORM, int EPI>
 hipError_t dg_rows(const DecodeGemvArgs& a, hipStream_t stream) {
     uint32_t total = 0;
     for (int s = 0; s < a.nseg; ++s) total += a.rows[s];
+    if (a.n <= 4096 && a.n % 8 == 0) return dw_dispatch<NORM, EPI>(a, total, stream);
     // Rows per workgroup: about two workgroups per CU at least.
     const int rb = total >= 4096 ? 8 : total >= 2048 ? 4 : 2;
     auto groups = [&](uint32_t r) {

@@ -357,14 +357,8 @@ static int decode_batched_launch(const void* q, const void* k_cache, const void*
     p.len_host = seq_len;
     p.len_cap = seq_len;
     p.splits = splits;
-    const size_t heads = (size_t)batch * num_q_heads;
-    char* ws = static_cast<char*>(workspace);
-    DecodePartials part{};
-    part.ml = reinterpret_cast<float*>(ws);
-    part.ml_head = 2 * (int64_t)splits;
-    part.o = reinterpret_cast<float*>(ws + align_up(heads * splits * 2 * sizeof(float), 256));
-    part.o_head = (int64_t)splits * heads_dim;
-    part.o_split = heads_dim;
+    const DecodePartials part =
+        decode_partials_in(workspace, (size_t)batch * num_q_heads, splits, heads_dim);
     hipStream_t st = as_stream(stream);
     hipError_t e = launch_decode_split(p, part, st);
     if (e != hipSuccess) return from_hip(e);

@@ -34,6 +34,7 @@
 
 #include "common.hpp"
 #include "kernels.hpp"
+#include "norm_rope.hpp"
 
 namespace tiattn {
 namespace {
@@ -85,9 +86,12 @@ constexpr int kMaxSplits = 1024;
 
 // Workgroup blockIdx.x takes a fixed slice [t_begin, t_end) of the positions
 // (split_range), its wave w the 32-row chunks w, w+4, ... of that slice.
-template <int D>
-__global__ __launch_bounds__(256, 3) void decode_split_kernel(DecodeProblem p, DecodePartials part,
-                                                              float scale_log2) {
+// PRO: the engine's form with the token's q/k norm + RoPE and cache-row
+// writes folded in (DecodePrologue).
+template <int D, bool PRO>
+__device__ __forceinline__ void decode_split_body(const DecodeProblem& p,
+                                                  const DecodePartials& part, float scale_log2,
+                                                  const DecodePrologue& pro) {
     constexpr int NLD = D / 32;  // 16-byte loads per row and lane == QK k-steps
     constexpr int NDB = D / 16;  // PV output blocks of 16 dims
     constexpr int V_ELEMS = kDecWaveRows * D;
@@ -122,9 +126,37 @@ __global__ __launch_bounds__(256, 3) void decode_split_kernel(DecodeProblem p, D
         return;
     }
 
+    // PRO: rows of LPR lanes each (lane group prow) load the q heads (rows
+    // 0 .. nh-1) and, in the workgroup whose slice holds the token, its raw
+    // k and v rows (rows kDecMaxHeads, kDecMaxHeads + 1); these loads go out
+    // before the first K/V chunk's, the arithmetic waits for them alone.
+    constexpr int LPR = D / 16;
+    constexpr int kNewK = kDecMaxHeads, kNewV = kDecMaxHeads + 1;
+    __shared__ __align__(16) uint16_t s_pro[PRO ? (kDecMaxHeads + 2) * D : 8];
+    const uint32_t pos = L - 1;
+    const bool has_new = PRO && t_end == L;
+    const int prow = threadIdx.x / LPR, pc = threadIdx.x % LPR;
+    int pmode = -1;  // -1: no prologue row in this lane
+    NormRopeIn pin;
+    if constexpr (PRO) {
+        if ((uint32_t)prow < nh) {
+            pmode = kRowNorm | kRowRope;
+            pin = norm_rope_load<D>(p.q + (bh0 + prow) * D, pro.q_w, nullptr, pro.rope, pos, pc,
+                                    pmode);
+        } else if (has_new && prow == kNewK) {
+            pmode = kRowNorm | kRowRope;
+            pin = norm_rope_load<D>(pro.k_raw + (int64_t)kvh * D, pro.k_w, nullptr, pro.rope, pos,
+                                    pc, pmode);
+        } else if (has_new && prow == kNewV) {
+            pmode = 0;
+            pin = norm_rope_load<D>(pro.v_raw + (int64_t)kvh * D, nullptr, nullptr, nullptr, pos,
+                                    pc, pmode);
+        }
+    }
+
     // B operand Q^T: column n = head h0 + n (zero beyond the group).
     bf16x8_t qb[NLD];
-    {
+    if constexpr (!PRO) {
         const bool has = (uint32_t)n < nh;
         const uint16_t* qrow = p.q + (bh0 + (has ? n : 0)) * D + 8 * g;
 #pragma unroll
@@ -181,18 +213,54 @@ __global__ __launch_bounds__(256, 3) void decode_split_kernel(DecodeProblem p, D
             const int64_t off = (int64_t)tc * row_stride + 8 * (lchunk + 8 * (j % CPL));
             kr[j] = ldg16_nt(kbase + off);
             vr[j] = ldg16_nt(vbase + off);
+            // PRO: row t_end - 1 is not written yet, so the rows clamped to it
+            // get zero V (their scores are masked, but 0 * NaN is NaN).
+            if (PRO && t >= t_end) vr[j] = make_uint4(0, 0, 0, 0);
         }
     };
     // Chunk c = rows [t_begin + 32c, t_begin + 32c + 32) (masked at t_end).
     const uint32_t nchunks = (t_end - t_begin + kDecWaveRows - 1) / kDecWaveRows;
     uint32_t cur = wave;
     if (cur < nchunks) load_kv(t_begin + cur * kDecWaveRows);
+
+    // PRO: normalise + rotate the rows into LDS (row kNewV is a copy), the
+    // token's k/v rows also to cache row pos (one head group writes them),
+    // then Q^T from LDS.
+    if constexpr (PRO) {
+        if (pmode >= 0) {
+            uint4 a, b;
+            norm_rope_compute<D>(pin, true, pro.eps, pos, pmode, &a, &b);
+            *reinterpret_cast<uint4*>(s_pro + prow * D + 8 * pc) = a;
+            *reinterpret_cast<uint4*>(s_pro + prow * D + 8 * pc + D / 2) = b;
+            if (prow >= kNewK && hgi == 0) {
+                uint16_t* crow = (prow == kNewK ? pro.k_cache : pro.v_cache) +
+                                 ((int64_t)pos * p.hkv + kvh) * D;
+                *reinterpret_cast<uint4*>(crow + 8 * pc) = a;
+                *reinterpret_cast<uint4*>(crow + 8 * pc + D / 2) = b;
+            }
+        }
+        lds_barrier();
+        const bool has = (uint32_t)n < nh;
+#pragma unroll
+        for (int i = 0; i < NLD; ++i) {
+            uint4 x = *reinterpret_cast<const uint4*>(s_pro + (has ? n : 0) * D + 8 * g + 32 * i);
+            if (!has) x = make_uint4(0, 0, 0, 0);
+            qb[i] = as_bf16x8(x);
+        }
+    }
     while (cur < nchunks) {
         const uint32_t t0 = t_begin + cur * kDecWaveRows;
         // K -> this wave's LDS tile, then the A operand (row 16*tt + n, chunk
         // 4i + g) back out of it.
 #pragma unroll
         for (int j = 0; j < NJ; ++j) *reinterpret_cast<uint4*>(vs + st_off[j]) = kr[j];
+        // PRO: the token's own row, from s_pro (LDS operations of a wave
+        // complete in order, so this lands after the tile store above).
+        const uint32_t rnew = pos - t0;
+        const bool put_new = has_new && rnew < (uint32_t)kDecWaveRows && lane < D / 8;
+        if (PRO && put_new)
+            *reinterpret_cast<uint4*>(vs + rnew * D + 8 * (lane ^ vt_swz<D>(rnew))) =
+                *reinterpret_cast<const uint4*>(s_pro + kNewK * D + 8 * lane);
         bf16x8_t ka[2][NLD];
 #pragma unroll
         for (int tt = 0; tt < 2; ++tt) {
@@ -206,6 +274,9 @@ __global__ __launch_bounds__(256, 3) void decode_split_kernel(DecodeProblem p, D
         // the K reads above see K).
 #pragma unroll
         for (int j = 0; j < NJ; ++j) *reinterpret_cast<uint4*>(vs + st_off[j]) = vr[j];
+        if (PRO && put_new)
+            *reinterpret_cast<uint4*>(vs + rnew * D + 8 * (lane ^ vt_swz<D>(rnew))) =
+                *reinterpret_cast<const uint4*>(s_pro + kNewV * D + 8 * lane);
         // S^T: lane (head n, g) value r of tile tt = position t0 + 16*tt + 4g + r.
         f32x4_t st[2];
 #pragma unroll
@@ -300,6 +371,23 @@ __global__ __launch_bounds__(256, 3) void decode_split_kernel(DecodeProblem p, D
             ml[1] = l;
         }
     }
+}
+
+// Three 4-wave workgroups per CU (the batched grids fill the chip).
+template <int D>
+__global__ __launch_bounds__(256, 3) void decode_split_kernel(DecodeProblem p, DecodePartials part,
+                                                              float scale_log2) {
+    decode_split_body<D, false>(p, part, scale_log2, DecodePrologue{});
+}
+
+// The engine's single-sequence grid (splits x Hkv workgroups) is far below
+// one per CU, so the register budget is not cut for occupancy.
+template <int D>
+__global__ __launch_bounds__(256, 1) void decode_split_pro_kernel(DecodeProblem p,
+                                                                  DecodePartials part,
+                                                                  float scale_log2,
+                                                                  DecodePrologue pro) {
+    decode_split_body<D, true>(p, part, scale_log2, pro);
 }
 
 // Merge the splits of one (sequence, q-head) in a 256-thread block.  The
@@ -513,6 +601,16 @@ hipError_t launch_split_t(const DecodeProblem& p, const DecodePartials& part, hi
     return hipGetLastError();
 }
 
+template <int D>
+hipError_t launch_split_pro_t(const DecodeProblem& p, const DecodePartials& part,
+                              const DecodePrologue& pro, hipStream_t st) {
+    const uint32_t group = p.hq / p.hkv;
+    const dim3 grid(p.splits, p.hkv * decode_head_groups(group), 1);
+    const float sl2 = kLog2e / sqrtf((float)D);
+    hipLaunchKernelGGL((decode_split_pro_kernel<D>), grid, dim3(256), 0, st, p, part, sl2, pro);
+    return hipGetLastError();
+}
+
 // Concurrent split workgroups the device holds (CUs x resident blocks per
 // CU), queried once per device; 256 CUs x 3 when no device is visible.
 uint32_t split_slots(uint32_t d) {
@@ -663,6 +761,13 @@ hipError_t launch_decode_split(const DecodeProblem& p, const DecodePartials& par
                                hipStream_t stream) {
     if (p.d == 64) return launch_split_t<64>(p, part, stream);
     return launch_split_t<128>(p, part, stream);
+}
+
+hipError_t launch_decode_split_prologue(const DecodeProblem& p, const DecodePartials& part,
+                                        const DecodePrologue& pro, hipStream_t stream) {
+    if (p.batch != 1 || p.len_mode != kLenDevice) return hipErrorInvalidValue;
+    if (p.d == 64) return launch_split_pro_t<64>(p, part, pro, stream);
+    return launch_split_pro_t<128>(p, part, pro, stream);
 }
 
 hipError_t launch_decode_combine(const DecodeProblem& p, const DecodePartials& part, uint16_t* o,

@@ -22,6 +22,21 @@ struct DecodePartials {
     int64_t o_split;
 };
 
+// Partials carved from a decode workspace of `heads` (sequence, q-head)
+// pairs: the (m, l) pairs first, the o rows from the next 256-byte boundary.
+inline DecodePartials decode_partials_in(void* workspace, size_t heads, uint32_t splits,
+                                         uint32_t d) {
+    char* ws = static_cast<char*>(workspace);
+    const size_t ml_bytes = (heads * splits * 2 * sizeof(float) + 255) / 256 * 256;
+    DecodePartials part{};
+    part.ml = reinterpret_cast<float*>(ws);
+    part.ml_head = 2 * (int64_t)splits;
+    part.o = reinterpret_cast<float*>(ws + ml_bytes);
+    part.o_head = (int64_t)splits * d;
+    part.o_split = d;
+    return part;
+}
+
 enum LenMode : int {
     kLenHost = 0,        // every sequence has length len_host
     kLenDevice = 1,      // lengths in len_dev[B]
@@ -44,6 +59,25 @@ struct DecodeProblem {
 // Split pass: grid (splits, Hkv * head groups, B).
 hipError_t launch_decode_split(const DecodeProblem& p, const DecodePartials& part,
                                hipStream_t stream);
+
+// The engine's decode step (one sequence, the token at position L - 1 with
+// L from len_dev) folds its pre-attention row work into the split pass:
+// p.q holds the raw q projection, each workgroup applies q RMSNorm + RoPE to
+// its heads, and the workgroup whose slice ends at L normalises and rotates
+// the raw k row, writes k and v to cache row L - 1 and uses them in place of
+// that row.  Results equal the prologue kernel followed by the split pass.
+struct DecodePrologue {
+    const uint16_t* q_w;    // q RMSNorm weight [D]
+    const uint16_t* k_raw;  // the token's raw k projection [Hkv][D]
+    const uint16_t* k_w;    // k RMSNorm weight [D]
+    const uint16_t* v_raw;  // [Hkv][D]
+    const float2* rope;     // rotary table [positions][D/2] (cos, sin)
+    uint16_t* k_cache;      // p.k and p.v, writable
+    uint16_t* v_cache;
+    float eps;
+};
+hipError_t launch_decode_split_prologue(const DecodeProblem& p, const DecodePartials& part,
+                                        const DecodePrologue& pro, hipStream_t stream);
 // Combine partials into o [B][Hq][D] bf16 (and o_f32 in fp32 when given);
 // aligned8: every partial row starts 8-byte aligned.
 hipError_t launch_decode_combine(const DecodeProblem& p, const DecodePartials& part, uint16_t* o,

@@ -19,6 +19,7 @@
 
 #include "common.hpp"
 #include "kernels.hpp"
+#include "norm_rope.hpp"
 
 namespace tiattn {
 namespace {
@@ -38,101 +39,6 @@ __global__ void rope_table_kernel(float2* table, const float* __restrict__ inv_f
     float sn, cs;
     sincosf((float)t * inv_freq[i], &sn, &cs);
     table[e] = make_float2(cs, sn);
-}
-
-// One D-element row handled by its LPR = D/16 lanes (lane c of the row owns
-// the RoPE pairs (8c + k, 8c + k + D/2), k < 8): mode bit kRowNorm applies
-// RMSNorm with `weight`, bit kRowRope RoPE at position t (angles from `table`
-// row t when non-null, else sincosf(t * inv_freq[i])); mode 0 copies the row
-// bit for bit.  in and out may alias.  All LPR lanes of the row must call it
-// (the sum of squares is reduced across them).
-template <int D>
-__device__ __forceinline__ void norm_rope_row(const uint16_t* in, uint16_t* out,
-                                              const uint16_t* __restrict__ weight,
-                                              const float* __restrict__ inv_freq,
-                                              const float2* __restrict__ table, float eps,
-                                              uint32_t t, int c, int mode) {
-#pragma clang fp contract(off)
-    constexpr int HALF = D / 2;
-    constexpr int LPR = HALF / 8;
-    // Every load goes out before the first use.
-    const uint4 xr = ldg16(in + 8 * c), xi = ldg16(in + 8 * c + HALF);
-    if (mode == 0) {
-        *reinterpret_cast<uint4*>(out + 8 * c) = xr;
-        *reinterpret_cast<uint4*>(out + 8 * c + HALF) = xi;
-        return;
-    }
-    uint4 wr = make_uint4(0, 0, 0, 0), wi = wr;
-    if (mode & kRowNorm) {
-        wr = ldg16(weight + 8 * c);
-        wi = ldg16(weight + 8 * c + HALF);
-    }
-    float4 cs[4];
-    if ((mode & kRowRope) && table) {
-        const float4* tp = reinterpret_cast<const float4*>(table + (uint64_t)t * HALF + 8 * c);
-#pragma unroll
-        for (int k = 0; k < 4; ++k) cs[k] = tp[k];
-    }
-    float re[8], im[8];
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-        const uint32_t a = word_of(xr, k), b = word_of(xi, k);
-        re[2 * k] = bf16_lo(a);
-        re[2 * k + 1] = bf16_hi(a);
-        im[2 * k] = bf16_lo(b);
-        im[2 * k + 1] = bf16_hi(b);
-    }
-    if (mode & kRowNorm) {
-        float ss = 0.0f;
-#pragma unroll
-        for (int k = 0; k < 8; ++k) ss += re[k] * re[k];
-#pragma unroll
-        for (int k = 0; k < 8; ++k) ss += im[k] * im[k];
-#pragma unroll
-        for (int m = LPR / 2; m >= 1; m >>= 1) ss += __shfl_xor(ss, m, LPR);
-        const float inv = 1.0f / sqrtf(ss / (float)D + eps);
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            const uint32_t a = word_of(wr, k), b = word_of(wi, k);
-            re[2 * k] = bf16_lo(pack_bf16x2(re[2 * k] * inv * bf16_lo(a), 0.0f));
-            re[2 * k + 1] = bf16_lo(pack_bf16x2(re[2 * k + 1] * inv * bf16_hi(a), 0.0f));
-            im[2 * k] = bf16_lo(pack_bf16x2(im[2 * k] * inv * bf16_lo(b), 0.0f));
-            im[2 * k + 1] = bf16_lo(pack_bf16x2(im[2 * k + 1] * inv * bf16_hi(b), 0.0f));
-        }
-    }
-    if (mode & kRowRope) {
-        float cv[8], sv[8];
-        if (table) {
-#pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                cv[2 * k] = cs[k].x;
-                sv[2 * k] = cs[k].y;
-                cv[2 * k + 1] = cs[k].z;
-                sv[2 * k + 1] = cs[k].w;
-            }
-        } else {
-#pragma unroll
-            for (int k = 0; k < 8; ++k) sincosf((float)t * inv_freq[8 * c + k], &sv[k], &cv[k]);
-        }
-#pragma unroll
-        for (int k = 0; k < 8; ++k) {
-            const float a = cv[k] * re[k] - sv[k] * im[k];
-            const float b = cv[k] * im[k] + sv[k] * re[k];
-            re[k] = a;
-            im[k] = b;
-        }
-    }
-    uint4 orr, oi;
-    orr.x = pack_bf16x2(re[0], re[1]);
-    orr.y = pack_bf16x2(re[2], re[3]);
-    orr.z = pack_bf16x2(re[4], re[5]);
-    orr.w = pack_bf16x2(re[6], re[7]);
-    oi.x = pack_bf16x2(im[0], im[1]);
-    oi.y = pack_bf16x2(im[2], im[3]);
-    oi.z = pack_bf16x2(im[4], im[5]);
-    oi.w = pack_bf16x2(im[6], im[7]);
-    *reinterpret_cast<uint4*>(out + 8 * c) = orr;
-    *reinterpret_cast<uint4*>(out + 8 * c + HALF) = oi;
 }
 
 // Rows (token, head) of a token-major [tokens][nums_head][D] tensor; RoPE

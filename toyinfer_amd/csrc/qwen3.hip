@@ -153,11 +153,13 @@ hipError_t launch_pick(toyinfer_qwen3* m) {
 }
 
 // One decode step for the token at tokens[*pos]; ends with tokens[*pos + 1]
-// and *pos += 1.  Seven launches per layer, one stream, kernel launches only
+// and *pos += 1.  Six launches per layer, one stream, kernel launches only
 // (capturable):
 //   RMSNorm + q/k/v projections (one grid over the three weight segments,
 //     where the reference forks them over three streams, :513-533);
-//   q/k norm + RoPE + cache write; split-K attention + combine;
+//   split-K attention with the q/k norm + RoPE and the cache-row writes
+//     folded in (the reference's separate norm, RoPE and cache-write
+//     kernels); the split combine;
 //   o projection + residual add; RMSNorm + gate/up + SwiGLU;
 //   down projection + residual add;
 // then the final norm, the lm-head and the token pick.
@@ -192,11 +194,30 @@ int decode_body(toyinfer_qwen3* m) {
         qkv.rows[1] = kv;
         qkv.rows[2] = kv;
         TRYH(launch_decode_gemv(qkv, st));
-        TRY(toyinfer_decode_qkv_prologue_bf16(m->d_q, m->d_k, m->d_v, L.q_norm, L.k_norm,
-                                              m->inv_freq, m->pos, msl, eps, m->d_q, kc, vc, hq,
-                                              hkv, d, s0));
-        TRY(toyinfer_decode_attention_bf16(m->d_q, kc, vc, m->d_o, 1, hq, hkv, d, m->seq_len, msl,
-                                           0, m->splits, m->attn_ws, m->attn_ws_bytes, s0));
+        DecodeProblem ap{};
+        ap.q = m->d_q;
+        ap.k = kc;
+        ap.v = vc;
+        ap.batch = 1;
+        ap.hq = hq;
+        ap.hkv = hkv;
+        ap.d = d;
+        ap.len_mode = kLenDevice;
+        ap.len_dev = m->seq_len;
+        ap.len_cap = msl;
+        ap.splits = m->splits;
+        DecodePrologue pro;
+        pro.q_w = u16(L.q_norm);
+        pro.k_raw = m->d_k;
+        pro.k_w = u16(L.k_norm);
+        pro.v_raw = m->d_v;
+        pro.rope = reinterpret_cast<const float2*>(m->rope);
+        pro.k_cache = kc;
+        pro.v_cache = vc;
+        pro.eps = eps;
+        const DecodePartials part = decode_partials_in(m->attn_ws, hq, m->splits, d);
+        TRYH(launch_decode_split_prologue(ap, part, pro, st));
+        TRYH(launch_decode_combine(ap, part, m->d_o, st));
         DecodeGemvArgs o;
         o.x = m->d_o;
         o.n = qd;

@@ -299,13 +299,28 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(PrefillProblem p
                 st0[i] = 0.0f;
                 st1[i] = 0.0f;
             }
+            // K operands one k-step ahead of their MFMAs.
+            uint4 ka[2][2];
+            ka[0][0] = *reinterpret_cast<const uint4*>(kb + k_off[0]);
+            ka[0][1] = *reinterpret_cast<const uint4*>(kb + 32 * D + k_off[0]);
 #pragma unroll
             for (int ks = 0; ks < P::KSTEPS; ++ks) {
-                const uint4 a0 = *reinterpret_cast<const uint4*>(kb + k_off[ks]);
-                const uint4 a1 = *reinterpret_cast<const uint4*>(kb + 32 * D + k_off[ks]);
-                st0 = mfma32x32x16(as_bf16x8(a0), qf[ks], st0);
-                st1 = mfma32x32x16(as_bf16x8(a1), qf[ks], st1);
+                if (ks + 1 < P::KSTEPS) {
+                    ka[(ks + 1) & 1][0] = *reinterpret_cast<const uint4*>(kb + k_off[ks + 1]);
+                    ka[(ks + 1) & 1][1] = *reinterpret_cast<const uint4*>(kb + 32 * D + k_off[ks + 1]);
+                }
+                st0 = mfma32x32x16(as_bf16x8(ka[ks & 1][0]), qf[ks], st0);
+                st1 = mfma32x32x16(as_bf16x8(ka[ks & 1][1]), qf[ks], st1);
             }
+            // Keep the reads a k-step ahead (the scheduler would otherwise
+            // pair each read with its MFMA and expose the LDS latency).
+            __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+#pragma unroll
+            for (int ks = 0; ks + 2 < P::KSTEPS; ++ks) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+                __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+            }
+            __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
             // Causal mask: lane holds keys n0 + 32*blk + 8*(i/4) + 4*kg + i%4.
             if (n0 + kPfBN - 1 > q0) {
 #pragma unroll
@@ -363,18 +378,34 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(PrefillProblem p
                                 sum_bf16x8(__builtin_bit_cast(uint4, pf[3]), 0.0f));
             // A = V^T for k-step tt: lane group G = lane/16 (kg = G/2) reads key
             // rows 16*tt + 4*kg + s/4 (+8 for the second half) at dims
-            // 32*db + 16*(G%2) + 4*(s%4), s = lane%16.
+            // 32*db + 16*(G%2) + 4*(s%4), s = lane%16.  The d-blocks are
+            // independent accumulators, so each k-step issues DBLK
+            // independent MFMAs, their operands read one k-step ahead.
+            uint4 va[2][P::DBLK];
+            auto read_v = [&](int tt, uint4 (&a)[P::DBLK]) __attribute__((always_inline)) {
 #pragma unroll
-            for (int db = 0; db < P::DBLK; ++db) {
-#pragma unroll
-                for (int tt = 0; tt < 4; ++tt) {
+                for (int db = 0; db < P::DBLK; ++db) {
                     const v4i16_t lo = ds_read_tr16(vb + v_off[db] + 16 * tt * D);
                     const v4i16_t hi = ds_read_tr16(vb + v_off[db] + (16 * tt + 8) * D);
-                    const uint4 a = make_uint4(__builtin_bit_cast(uint2, lo).x, __builtin_bit_cast(uint2, lo).y,
-                                               __builtin_bit_cast(uint2, hi).x, __builtin_bit_cast(uint2, hi).y);
-                    oacc[db] = mfma32x32x16(as_bf16x8(a), pf[tt], oacc[db]);
+                    a[db] = make_uint4(__builtin_bit_cast(uint2, lo).x, __builtin_bit_cast(uint2, lo).y,
+                                       __builtin_bit_cast(uint2, hi).x, __builtin_bit_cast(uint2, hi).y);
                 }
+            };
+            read_v(0, va[0]);
+#pragma unroll
+            for (int tt = 0; tt < 4; ++tt) {
+                if (tt + 1 < 4) read_v(tt + 1, va[(tt + 1) & 1]);
+#pragma unroll
+                for (int db = 0; db < P::DBLK; ++db)
+                    oacc[db] = mfma32x32x16(as_bf16x8(va[tt & 1][db]), pf[tt], oacc[db]);
             }
+            __builtin_amdgcn_sched_group_barrier(0x100, 4 * P::DBLK, 0);
+#pragma unroll
+            for (int tt = 0; tt < 3; ++tt) {
+                __builtin_amdgcn_sched_group_barrier(0x008, P::DBLK, 0);
+                __builtin_amdgcn_sched_group_barrier(0x100, 2 * P::DBLK, 0);
+            }
+            __builtin_amdgcn_sched_group_barrier(0x008, P::DBLK, 0);
         }
 
         __syncthreads();  // (waits for this wave's tile loads, then for every wave)

@@ -137,6 +137,14 @@ __device__ __forceinline__ uint4 ldg16_nt(const void* p) {
     return make_uint4(v.x, v.y, v.z, v.w);
 }
 
+// 16-byte store with the non-temporal hint, for output that is not read
+// again by the kernel; whole 128-byte lines per instruction keep it from
+// being split into partial-line writes.
+__device__ __forceinline__ void stg16_nt(void* p, uint4 v) {
+    typedef unsigned v4u_t __attribute__((ext_vector_type(4)));
+    __builtin_nontemporal_store(v4u_t{v.x, v.y, v.z, v.w}, reinterpret_cast<v4u_t*>(p));
+}
+
 __device__ __forceinline__ bf16x8_t as_bf16x8(uint4 v) { return __builtin_bit_cast(bf16x8_t, v); }
 
 __device__ __forceinline__ f32x16_t mfma32x32x16(bf16x8_t a, bf16x8_t b, f32x16_t c) {

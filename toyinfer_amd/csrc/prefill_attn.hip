@@ -415,10 +415,19 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(PrefillProblem p
         if (t + 1 < n_tiles) step(t + 1, s_k1, s_v1, s_k0, s_v0);
     }
 
+    // O goes out through LDS, so that each store instruction writes whole
+    // 256-byte rows (16 lanes per row) with the non-temporal hint: O is not
+    // read again, and the per-lane 8-byte pieces would otherwise occupy L2
+    // lines beside the K/V tiles the other query tiles of this KV head
+    // re-read.  The tile buffers are free: every wave passed the last
+    // step's barrier.  Each wave uses its own 32 x D region (16-byte chunk c
+    // of row r at c ^ (r mod D/8)) and reads back only what it wrote (LDS
+    // operations of a wave complete in order).
     const float l_tot = xor32_sum(l_run);  // all lanes take part in the exchange
-    if (qq < p.s) {
-        const float inv = 1.0f / l_tot;
-        uint16_t* orow = p.o + ((int64_t)qq * p.hq + h) * D;
+    {
+        constexpr int CPR = D / 8;
+        const float inv = 1.0f / l_tot;  // (rows past S: not stored)
+        uint16_t* so = (wave < 2 ? s_k0 : s_k1) + (wave & 1) * 32 * D;
 #pragma unroll
         for (int db = 0; db < P::DBLK; ++db)
 #pragma unroll
@@ -426,8 +435,16 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(PrefillProblem p
                 uint2 w;
                 w.x = pack_bf16x2(oacc[db][4 * i4] * inv, oacc[db][4 * i4 + 1] * inv);
                 w.y = pack_bf16x2(oacc[db][4 * i4 + 2] * inv, oacc[db][4 * i4 + 3] * inv);
-                *reinterpret_cast<uint2*>(orow + db * 32 + 8 * i4 + 4 * kg) = w;
+                const int c = 4 * db + i4;
+                *reinterpret_cast<uint2*>(so + ql * D + 8 * (c ^ (ql & (CPR - 1))) + 4 * kg) = w;
             }
+#pragma unroll
+        for (int j = 0; j < 32 * CPR / 64; ++j) {
+            const int f = 64 * j + lane, row = f / CPR, c = f % CPR;
+            const uint4 v = *reinterpret_cast<const uint4*>(so + row * D + 8 * (c ^ (row & (CPR - 1))));
+            const uint32_t q = q0 + row;
+            if (q < p.s) stg16_nt(p.o + ((int64_t)q * p.hq + h) * D + 8 * c, v);
+        }
     }
 }
 

@@ -84,22 +84,46 @@ __device__ __forceinline__ int k_swz(int row) { return row & (D / 8 - 1); }
 template <int D>
 __device__ __forceinline__ int v_swz(int row) { return D == 128 ? 4 * (row & 3) : 2 * (row & 3); }
 
-// Issue this wave's share of tile `tile_off` (K and V) into LDS tiles sk, sv.
+// This lane's byte offsets, within a tile, of the global chunks it loads
+// into its LDS slots (K and V maps), for each of the wave's 1 KiB blocks.
 template <int D>
-__device__ __forceinline__ void dma_tile(__amdgpu_buffer_rsrc_t rk, __amdgpu_buffer_rsrc_t rv,
-                                         uint32_t row_bytes, uint32_t tile_off, uint16_t* sk,
-                                         uint16_t* sv) {
+struct DmaOffsets {
+    uint32_t k[DmaShape<D>::BLOCKS_PER_WAVE];
+    uint32_t v[DmaShape<D>::BLOCKS_PER_WAVE];
+};
+
+template <int D>
+__device__ __forceinline__ DmaOffsets<D> dma_offsets(uint32_t row_bytes, int wave, int lane) {
     using P = DmaShape<D>;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    DmaOffsets<D> r;
+#pragma unroll
+    for (int j = 0; j < P::BLOCKS_PER_WAVE; ++j) {
+        const int slot = 64 * (wave + (kPfThreads / 64) * j) + lane;  // 16-byte slot within the tile
+        const int row = slot / P::CPR, phys = slot % P::CPR;
+        r.k[j] = row * row_bytes + 16 * (phys ^ k_swz<D>(row));
+        r.v[j] = row * row_bytes + 16 * (phys ^ v_swz<D>(row));
+    }
+    return r;
+}
+
+// Issue this wave's share of the tile at byte `tile_off` (K and V) into LDS
+// tiles sk, sv.  The buffer resources are rebased at the tile (scalar
+// arithmetic; the range check then still covers every byte past row S-1,
+// which the scalar offset operand would escape), `wave` is a scalar (the
+// LDS destination, M0, is then a scalar sum), and the per-lane offsets are
+// loop invariants: a tile's issue costs no vector instructions.
+template <int D>
+__device__ __forceinline__ void dma_tile(const uint16_t* k_head, const uint16_t* v_head, uint32_t kv_bytes,
+                                         const uint32_t* offk, const uint32_t* offv, int wave, uint32_t tile_off,
+                                         uint16_t* sk, uint16_t* sv) {
+    using P = DmaShape<D>;
+    const __amdgpu_buffer_rsrc_t rk = make_rsrc(reinterpret_cast<const char*>(k_head) + tile_off, kv_bytes - tile_off);
+    const __amdgpu_buffer_rsrc_t rv = make_rsrc(reinterpret_cast<const char*>(v_head) + tile_off, kv_bytes - tile_off);
 #pragma unroll
     for (int j = 0; j < P::BLOCKS_PER_WAVE; ++j) {
         const int blk = wave + (kPfThreads / 64) * j;
-        const int slot = 64 * blk + lane;                // 16-byte slot within the tile
-        const int row = slot / P::CPR, phys = slot % P::CPR;
-        const uint32_t koff = tile_off + row * row_bytes + 16 * (phys ^ k_swz<D>(row));
-        const uint32_t vof = tile_off + row * row_bytes + 16 * (phys ^ v_swz<D>(row));
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (__attribute__((address_space(3))) void*)(sk + 512 * blk), 16, koff, 0, 0, 0);
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (__attribute__((address_space(3))) void*)(sv + 512 * blk), 16, vof, 0, 0, 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (__attribute__((address_space(3))) void*)(sk + 512 * blk), 16, offk[j], 0, 0, 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (__attribute__((address_space(3))) void*)(sv + 512 * blk), 16, offv[j], 0, 0, 0);
     }
 }
 
@@ -254,10 +278,12 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(PrefillProblem p
     // first element; the buffer range ends after row S-1's D elements.
     const uint32_t row_bytes = p.hkv * D * 2;
     const uint32_t kv_bytes = (p.s - 1) * row_bytes + D * 2;
-    const __amdgpu_buffer_rsrc_t rk = make_rsrc(p.k + (int64_t)kvh * D, kv_bytes);
-    const __amdgpu_buffer_rsrc_t rv = make_rsrc(p.v + (int64_t)kvh * D, kv_bytes);
+    const uint16_t* k_head = p.k + (int64_t)kvh * D;
+    const uint16_t* v_head = p.v + (int64_t)kvh * D;
 
-    dma_tile<D>(rk, rv, row_bytes, 0, s_k0, s_v0);
+    const int swave = __builtin_amdgcn_readfirstlane(wave);
+    const DmaOffsets<D> doff = dma_offsets<D>(row_bytes, swave, lane);
+    dma_tile<D>(k_head, v_head, kv_bytes, doff.k, doff.v, swave, 0, s_k0, s_v0);
     bf16x8_t qf[P::KSTEPS];
     load_q<D, FUSED>(qf, p, qq, h, kg);
 
@@ -289,7 +315,7 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(PrefillProblem p
     // whose last readers passed the previous barrier.
     auto step = [&](uint32_t t, const uint16_t* kb, const uint16_t* vb, uint16_t* kn,
                     uint16_t* vn) __attribute__((always_inline)) {
-        if (t + 1 < n_tiles) dma_tile<D>(rk, rv, row_bytes, (t + 1) * kPfBN * row_bytes, kn, vn);
+        if (t + 1 < n_tiles) dma_tile<D>(k_head, v_head, kv_bytes, doff.k, doff.v, swave, (t + 1) * kPfBN * row_bytes, kn, vn);
 
         if (t < wave_tiles) {
             const uint32_t n0 = t * kPfBN;

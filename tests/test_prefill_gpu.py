@@ -122,6 +122,47 @@ def test_config2_full(dev, algo):
     print(f"[prefill] config2 max-abs {mx:.3g} mean-abs {mn:.3g}", flush=True)
 
 
+def extreme_case(kind, s, hq, hkv, d):
+    """Scores far outside what a fixed softmax reference could hold.
+
+    "negative"/"positive": every key row is -u / +u and every query row 12u,
+    so each row's scores are all equal, about -/+226 in log2 units here
+    (2^226 overflows fp32; 2^-226 underflows): the output is the mean of V
+    over the row's visible keys.  "wide": q, k ~ 4 N(0,1), score spread of
+    about +-80 in log2 units within a row.
+    """
+    v = synth.normal_bf16(31, "v", (s, hkv, d))
+    if kind == "wide":
+        q = oracle.f32_to_bf16(4.0 * oracle.bf16_to_f32(synth.normal_bf16(31, "q", (s, hq, d))))
+        k = oracle.f32_to_bf16(4.0 * oracle.bf16_to_f32(synth.normal_bf16(31, "k", (s, hkv, d))))
+        return q, k, v
+    u = oracle.bf16_to_f32(synth.normal_bf16(31, "u", (d,)))
+    sign = -1.0 if kind == "negative" else 1.0
+    q = oracle.f32_to_bf16(np.broadcast_to(12.0 * u, (s, hq, d)).astype(np.float32))
+    k = oracle.f32_to_bf16(np.broadcast_to(sign * u, (s, hkv, d)).astype(np.float32))
+    return q, k, v
+
+
+@pytest.mark.parametrize("algo", ALGOS)
+@pytest.mark.parametrize("kind", ["negative", "positive", "wide"])
+def test_extreme_scores(dev, kind, algo):
+    """Rows whose scores overflow or underflow exp2 without a running maximum
+    (the kernels' reference for the exponentials moves only when a tile's
+    probabilities would leave range): vs the oracle and, for equal scores,
+    vs the prefix mean of V."""
+    s, hq, hkv, d = 700, 4, 2, 128
+    print(f"[prefill] extreme scores {kind} algo={algo}", flush=True)
+    qb, kb, vb = extreme_case(kind, s, hq, hkv, d)
+    got = H.bf16_bits_to_f32(run_prefill(qb, kb, vb, dev, algo))
+    exp = oracle.round_bf16(oracle.flash_reference(qb, kb, vb))
+    H.check_bar(got, exp, f"{kind} algo={algo}")
+    if kind != "wide":
+        vf = oracle.bf16_to_f32(vb).astype(np.float64)
+        mean = np.cumsum(vf, axis=0) / np.arange(1, s + 1)[:, None, None]
+        mean = np.repeat(mean, hq // hkv, axis=1)
+        H.check_bar(got, oracle.round_bf16(mean.astype(np.float32)), f"{kind} prefix mean")
+
+
 @pytest.mark.parametrize("s,hq,hkv,d", [(3000, 32, 8, 128), (2600, 16, 4, 64)])
 def test_algos_agree_at_long_s(dev, s, hq, hkv, d):
     """Both kernels agree closely on problems with several times more query

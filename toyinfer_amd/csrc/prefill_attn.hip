@@ -20,8 +20,11 @@
 //   row base + s/4, dims d0 + 4*(s%4); lane i receives keys base..base+3 of
 //   dim d0 + i).  The output lane again owns one query row, so the running
 //   rescale is in-lane.
-// * The running max is only moved when it grows by more than 2^8 (the sum
-//   and output share the stale max, so the result is exact); fully masked
+// * The exponentials are taken against a running reference (0 at first)
+//   that moves only when a tile's probabilities would leave range: then the
+//   tile's row maximum is computed, a row's first tile takes it, and later
+//   tiles move the reference up by more than 2^8 only.  The sum and output
+//   share the reference, so the result does not depend on it; fully masked
 //   tiles past the diagonal are never visited.
 // * K and V tiles are double-buffered in LDS: the next tile's global loads
 //   (buffer loads whose range check returns zeros past row S-1) are in
@@ -44,6 +47,8 @@ constexpr int kPfThreads = 256;
 constexpr int kPfBM = 128;  // query rows per workgroup
 constexpr int kPfBN = 64;   // keys per tile
 constexpr float kRescaleThreshold = 8.0f;
+constexpr float kMassMax = 0x1p64f;   // largest tile row-sum share a lane may take without a rescale
+constexpr float kMassMin = 0x1p-64f;  // smallest row mass after a tile without a new reference
 
 typedef short v4i16_t __attribute__((ext_vector_type(4)));
 
@@ -292,7 +297,7 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(PrefillProblem p
     for (int db = 0; db < P::DBLK; ++db)
 #pragma unroll
         for (int i = 0; i < 16; ++i) oacc[db][i] = 0.0f;
-    float m_run = -INFINITY, l_run = 0.0f;
+    float m_run = 0.0f, l_run = 0.0f;
 
     // Operand read offsets (elements) within a tile.  K: row ql (and +32),
     // chunk 2*ks + kg; V^T (transposing read): rows 4*kg + s16/4 (+16*tt, +8),
@@ -356,52 +361,65 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(PrefillProblem p
                     if (key + 32 > qq) st1[i] = -INFINITY;
                 }
             }
-            // Row max: two chains of three-input maxima.
-            float ma = fmaxf(st0[0], st0[1]), mb = fmaxf(st1[0], st1[1]);
-#pragma unroll
-            for (int i = 2; i < 16; i += 2) {
-                ma = fmaxf(fmaxf(ma, st0[i]), st0[i + 1]);
-                mb = fmaxf(fmaxf(mb, st1[i]), st1[i + 1]);
-            }
-            float mx = fmaxf(ma, mb);
-            mx = xor32_max(mx);
-            const float mt = mx * scale_log2;
-            const bool need = mt > m_run + kRescaleThreshold;
-            if (__any(need)) {
-                float alpha = 1.0f;
-                if (need) {
-                    alpha = __builtin_amdgcn_exp2f(m_run - mt);
-                    m_run = mt;
-                }
-                l_run *= alpha;
-#pragma unroll
-                for (int db = 0; db < P::DBLK; ++db)
-#pragma unroll
-                    for (int i = 0; i < 16; ++i) oacc[db][i] *= alpha;
-            }
-            const float mref = m_run == -INFINITY ? 0.0f : m_run;
-#pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                st0[i] = __builtin_amdgcn_exp2f(fmaf(st0[i], scale_log2, -mref));
-                st1[i] = __builtin_amdgcn_exp2f(fmaf(st1[i], scale_log2, -mref));
-            }
+            // Probabilities against the running reference m_run (a row
+            // constant, 0 before the first tile): P = bf16(2^(s*c - m_run)),
+            // and this lane's share of the tile's row sum, taken from the
+            // bf16 values the P.V product uses.  The quotient O / l does not
+            // depend on m_run; it only has to keep P finite and the row's
+            // mass clear of underflow, so the tile's row maximum is computed
+            // only for a tile that fails that check.
             bf16x8_t pf[4];
+            auto probs = [&](float mref) __attribute__((always_inline)) {
 #pragma unroll
-            for (int tt = 0; tt < 4; ++tt) {
-                const f32x16_t& src = tt < 2 ? st0 : st1;
-                const int o8 = 8 * (tt & 1);
-                uint4 w;
-                w.x = pack_bf16x2(src[o8 + 0], src[o8 + 1]);
-                w.y = pack_bf16x2(src[o8 + 2], src[o8 + 3]);
-                w.z = pack_bf16x2(src[o8 + 4], src[o8 + 5]);
-                w.w = pack_bf16x2(src[o8 + 6], src[o8 + 7]);
-                pf[tt] = as_bf16x8(w);
+                for (int tt = 0; tt < 4; ++tt) {
+                    const f32x16_t& src = tt < 2 ? st0 : st1;
+                    const int o8 = 8 * (tt & 1);
+                    float e[8];
+#pragma unroll
+                    for (int j = 0; j < 8; ++j)
+                        e[j] = __builtin_amdgcn_exp2f(fmaf(src[o8 + j], scale_log2, -mref));
+                    pf[tt] = as_bf16x8(make_uint4(pack_bf16x2(e[0], e[1]), pack_bf16x2(e[2], e[3]),
+                                                  pack_bf16x2(e[4], e[5]), pack_bf16x2(e[6], e[7])));
+                }
+                return sum_bf16x8(__builtin_bit_cast(uint4, pf[0]),
+                                  sum_bf16x8(__builtin_bit_cast(uint4, pf[1]), 0.0f)) +
+                       sum_bf16x8(__builtin_bit_cast(uint4, pf[2]),
+                                  sum_bf16x8(__builtin_bit_cast(uint4, pf[3]), 0.0f));
+            };
+            float ts = probs(m_run);
+            // The check: every lane's share at most 2^64 (a NaN fails too)
+            // and the row's mass after this tile at least 2^-64.
+            const float row_mass = xor32_sum(l_run + ts);
+            if (__any(!(ts <= kMassMax) || !(row_mass >= kMassMin))) {
+                // The tile's row maximum (two chains of three-input maxima).
+                float ma = fmaxf(st0[0], st0[1]), mb = fmaxf(st1[0], st1[1]);
+#pragma unroll
+                for (int i = 2; i < 16; i += 2) {
+                    ma = fmaxf(fmaxf(ma, st0[i]), st0[i + 1]);
+                    mb = fmaxf(fmaxf(mb, st1[i]), st1[i + 1]);
+                }
+                const float mt = xor32_max(fmaxf(ma, mb)) * scale_log2;
+                // A row's first tile (no mass yet) takes its maximum as the
+                // reference; later tiles move it only up, and only by more
+                // than 2^8, rescaling what has accumulated.
+                const bool first = xor32_sum(l_run) == 0.0f;
+                const bool need = !first && mt > m_run + kRescaleThreshold;
+                if (first) m_run = mt;
+                if (__any(need)) {
+                    float alpha = 1.0f;
+                    if (need) {
+                        alpha = __builtin_amdgcn_exp2f(m_run - mt);
+                        m_run = mt;
+                    }
+                    l_run *= alpha;
+#pragma unroll
+                    for (int db = 0; db < P::DBLK; ++db)
+#pragma unroll
+                        for (int i = 0; i < 16; ++i) oacc[db][i] *= alpha;
+                }
+                ts = probs(m_run);
             }
-            // The row sum takes the bf16 probabilities the P.V product uses.
-            l_run += sum_bf16x8(__builtin_bit_cast(uint4, pf[0]),
-                                sum_bf16x8(__builtin_bit_cast(uint4, pf[1]), 0.0f)) +
-                     sum_bf16x8(__builtin_bit_cast(uint4, pf[2]),
-                                sum_bf16x8(__builtin_bit_cast(uint4, pf[3]), 0.0f));
+            l_run += ts;
             // A = V^T for k-step tt: lane group G = lane/16 (kg = G/2) reads key
             // rows 16*tt + 4*kg + s/4 (+8 for the second half) at dims
             // 32*db + 16*(G%2) + 4*(s%4), s = lane%16.  The d-blocks are

@@ -167,11 +167,12 @@ def test_batch_proj_shapes(dev, T, M, N):
     assert (got[T * M:] == SENTINEL).all()
 
 
-# The first two tile the chip with 256 x 256 tiles (4-stage ring kernel),
-# with ragged tiles and slice counts that are not a multiple of 4 or tiny.
+# The first two tile the chip with 256 x 256 tiles, with ragged tiles and
+# slice counts that are odd or tiny; 1371 x 6144 takes the 128 x 192 tiles
+# (its 128 x 128 grid would overflow the resident workgroups).
 @pytest.mark.parametrize("T,M,N", [(4096, 4096, 4096), (4000, 4100, 4160), (4096, 4096, 64),
                                    (2048, 4096, 4096), (1000, 1024, 4096), (512, 12288, 4096),
-                                   (512, 4096, 12288)])
+                                   (512, 4096, 12288), (1371, 6144, 1024)])
 def test_batch_proj_full_size_vs_torch_fp32(dev, T, M, N):
     """Prefill projection shapes of an 8B model against a torch fp32 product
     of the same bf16 inputs."""
@@ -214,7 +215,8 @@ def test_batch_proj_graph_replay(dev):
 
 
 @pytest.mark.parametrize("T,hid,rows", [(1371, 1024, (2048, 1024, 1024)), (4096, 1024, (2048, 1024, 1024)),
-                                      (300, 512, (3072, 3072)), (17, 256, (200, 64, 130))])
+                                      (300, 512, (3072, 3072)), (1371, 1024, (3072, 3072)),
+                                      (17, 256, (200, 64, 130))])
 def test_gemm_segments_equal_separate_projections(dev, T, hid, rows):
     """Stacked segments in one launch (whichever tile size the stacked grid
     picks) give each element bit for bit what the separate projection gives:

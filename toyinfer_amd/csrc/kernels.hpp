@@ -110,6 +110,8 @@ struct PrefillProblem {
     int variant;              // 0: pick by shape, 1: split over keys, 2: 128-row tiles
 };
 hipError_t launch_prefill(const PrefillProblem& p, hipStream_t stream);
+// Whether launch_prefill takes the split-over-keys kernel for this problem.
+bool prefill_uses_split(const PrefillProblem& p);
 
 // ------------------------------------------------------ prologue kernels
 hipError_t launch_precompute_freq(float* inv_freq, int d, float theta, hipStream_t stream);
@@ -121,6 +123,12 @@ hipError_t launch_row_norm_rope(const uint16_t* in, uint16_t* out, const uint16_
                                 const float* inv_freq, const float* table, float eps,
                                 uint32_t num_tokens, uint32_t nums_head, uint32_t d, int mode,
                                 hipStream_t stream);
+// Per-head RMSNorm + RoPE (rotary table rows) of Q [T][hq][D] and K
+// [T][hkv][D] in one launch: q -> q_out (may alias), k -> k_out (may alias).
+hipError_t launch_qk_norm_rope_rows(const uint16_t* q, uint16_t* q_out, const uint16_t* q_weight,
+                                    const uint16_t* k, uint16_t* k_out, const uint16_t* k_weight,
+                                    const float* table, float eps, uint32_t num_tokens,
+                                    uint32_t hq, uint32_t hkv, uint32_t d, hipStream_t stream);
 hipError_t launch_rope_table(float* table, const float* inv_freq, uint32_t num_pos, uint32_t d,
                              hipStream_t stream);
 // One decoded token's rows at a single position (device pos_d, else

@@ -811,7 +811,7 @@ template <int D, bool FUSED>
 hipError_t launch_t(const PrefillProblem& p, hipStream_t st) {
     const uint32_t n_qtiles = (p.s + kPfBM - 1) / kPfBM;
     const float sl2 = kLog2e / sqrtf((float)D);
-    const bool split = p.variant == 1 || (p.variant == 0 && n_qtiles * p.hq < kSplitKvBelowWgs);
+    const bool split = prefill_uses_split(p);
     if (split) {
         const uint32_t items = ((p.s + kSkBM - 1) / kSkBM) * p.hq;
         const dim3 grid(FUSED ? items : min(items, splitkv_slots<D, FUSED>()));
@@ -825,6 +825,11 @@ hipError_t launch_t(const PrefillProblem& p, hipStream_t st) {
 }
 
 }  // namespace
+
+bool prefill_uses_split(const PrefillProblem& p) {
+    const uint32_t n_qtiles = (p.s + kPfBM - 1) / kPfBM;
+    return p.variant == 1 || (p.variant == 0 && n_qtiles * p.hq < kSplitKvBelowWgs);
+}
 
 hipError_t launch_prefill(const PrefillProblem& p, hipStream_t stream) {
     if (p.d == 64) return p.fused_q ? launch_t<64, true>(p, stream) : launch_t<64, false>(p, stream);

@@ -181,6 +181,7 @@ struct GmCfg {
 using GmMini = GmCfg<64, 64, 2, 2, 4, 128>;  // 4 waves of 32 x 32
 using GmMini64 = GmCfg<64, 64, 2, 2, 4, 64>;
 using GmSmall = GmCfg<128, 128, 2, 2, 2>;  // 4 waves of 64 x 64, 2 workgroups per CU
+using GmMid = GmCfg<128, 192, 2, 2, 2>;    // 4 waves of 64 x 96, 2 workgroups per CU (80 KB LDS each)
 using GmLarge = GmCfg<256, 256, 2, 4, 1>;  // 8 waves of 128 x 64
 
 // LDS rows of BK bf16 (CPR 16-byte chunks); chunk c of row r sits at
@@ -354,6 +355,13 @@ uint32_t gemm_tiles(const GemmArgs& g) {
 }
 
 template <typename C>
+bool gemm_whole(const GemmArgs& g) {
+    for (int sg = 0; sg < g.nseg; ++sg)
+        if (g.rows[sg] % C::BN) return false;
+    return true;
+}
+
+template <typename C>
 hipError_t gemm_launch(const GemmArgs& g, hipStream_t stream) {
     gemm_kernel<C><<<gemm_tiles<C>(g), C::THREADS, 0, stream>>>(g);
     return hipGetLastError();
@@ -404,6 +412,12 @@ hipError_t launch_gemm(const GemmArgs& g, hipStream_t stream) {
     // The largest tile whose tiles alone fill every CU once; 64 x 64 below that.
     const uint32_t cus = (uint32_t)gemm_cus();
     if (gemm_tiles<GmLarge>(g) >= cus) return gemm_launch<GmLarge>(g, stream);
+    // 128 x 128 tiles that overflow the two resident workgroups per CU leave
+    // a second, mostly idle round: 128 x 192 tiles, when they fit one round
+    // (and every segment is whole tiles of 192), take it in one.
+    if (gemm_tiles<GmSmall>(g) > 2 * cus && gemm_tiles<GmMid>(g) <= 2 * cus &&
+        gemm_whole<GmMid>(g))
+        return gemm_launch<GmMid>(g, stream);
     if (gemm_tiles<GmSmall>(g) >= cus) return gemm_launch<GmSmall>(g, stream);
     if (g.N % GmMini::BK == 0) return gemm_launch<GmMini>(g, stream);
     return gemm_launch<GmMini64>(g, stream);

@@ -59,6 +59,35 @@ __global__ __launch_bounds__(256) void row_norm_rope_kernel(const uint16_t* in, 
                      threadIdx.x % LPR, mode);
 }
 
+// Rows [0, T*hq) are Q's (q -> q_out), rows [T*hq, T*(hq + hkv)) K's
+// (k -> k_out); each row normalised with its tensor's weight and rotated at
+// position = its token index.
+struct QkRows {
+    const uint16_t* q;
+    uint16_t* q_out;
+    const uint16_t* q_weight;
+    const uint16_t* k;
+    uint16_t* k_out;
+    const uint16_t* k_weight;
+    const float2* table;
+    float eps;
+    uint32_t q_rows, rows, hq, hkv;
+};
+
+template <int D>
+__global__ __launch_bounds__(256) void qk_rows_norm_rope_kernel(QkRows a) {
+    constexpr int LPR = D / 16;
+    constexpr int RPB = 256 / LPR;
+    const uint32_t row = blockIdx.x * RPB + threadIdx.x / LPR;
+    if (row >= a.rows) return;  // the LPR lanes of a row exit together
+    const bool is_q = row < a.q_rows;
+    const uint32_t r = is_q ? row : row - a.q_rows;
+    const int64_t off = (int64_t)r * D;
+    norm_rope_row<D>((is_q ? a.q : a.k) + off, (is_q ? a.q_out : a.k_out) + off,
+                     is_q ? a.q_weight : a.k_weight, nullptr, a.table, a.eps,
+                     r / (is_q ? a.hq : a.hkv), threadIdx.x % LPR, kRowNorm | kRowRope);
+}
+
 // One decoded token at position pos = min(*pos_d or pos_host, pos_cap - 1):
 // rows [0, hq) are its query heads (q -> q_out, q_mode), rows
 // [hq, hq + hkv) its key heads (k -> row pos of k_cache, k_mode), rows
@@ -162,6 +191,32 @@ hipError_t launch_kv_row_copy(const uint16_t* src, uint16_t* cache, const uint32
     const uint32_t lanes = vec16 ? kv_dim / 8 : kv_dim / 2;
     hipLaunchKernelGGL(kv_row_copy_kernel, dim3((lanes + 255) / 256), dim3(256), 0, stream, src,
                        cache, pos_d, kv_dim, vec16 ? 1 : 0);
+    return hipGetLastError();
+}
+
+hipError_t launch_qk_norm_rope_rows(const uint16_t* q, uint16_t* q_out, const uint16_t* q_weight,
+                                    const uint16_t* k, uint16_t* k_out, const uint16_t* k_weight,
+                                    const float* table, float eps, uint32_t num_tokens,
+                                    uint32_t hq, uint32_t hkv, uint32_t d, hipStream_t stream) {
+    QkRows a;
+    a.q = q;
+    a.q_out = q_out;
+    a.q_weight = q_weight;
+    a.k = k;
+    a.k_out = k_out;
+    a.k_weight = k_weight;
+    a.table = reinterpret_cast<const float2*>(table);
+    a.eps = eps;
+    a.hq = hq;
+    a.hkv = hkv;
+    a.q_rows = num_tokens * hq;
+    a.rows = num_tokens * (hq + hkv);
+    const uint32_t rows_per_block = 256 / (d / 16);
+    const dim3 grid((a.rows + rows_per_block - 1) / rows_per_block);
+    if (d == 64)
+        hipLaunchKernelGGL(qk_rows_norm_rope_kernel<64>, grid, dim3(256), 0, stream, a);
+    else
+        hipLaunchKernelGGL(qk_rows_norm_rope_kernel<128>, grid, dim3(256), 0, stream, a);
     return hipGetLastError();
 }
 

@@ -351,6 +351,14 @@ int toyinfer_qwen3_prefill(toyinfer_qwen3* m, const uint32_t* token_ids_d, uint3
     const bool gemm = proj_uses_gemm(T, H, m->layers[0].q_proj, m->p_xn) &&
                       proj_uses_gemm(T, qd, m->layers[0].o_proj, m->p_o) &&
                       proj_uses_gemm(T, F, m->layers[0].down_proj, m->p_inter);
+    PrefillProblem attn{};
+    attn.q = m->p_q;
+    attn.o = m->p_o;
+    attn.s = T;
+    attn.hq = hq;
+    attn.hkv = hkv;
+    attn.d = d;
+    const bool split_attn = prefill_uses_split(attn);
     for (uint32_t l = 0; l < c.num_layers; ++l) {
         const toyinfer_qwen3_layer& L = m->layers[l];
         uint16_t* kc = m->k_cache + (size_t)l * msl * kv;
@@ -378,9 +386,21 @@ int toyinfer_qwen3_prefill(toyinfer_qwen3* m, const uint32_t* token_ids_d, uint3
             TRY(toyinfer_batch_gemv_proj_bf16(L.k_proj, m->p_xn, m->p_k, T, kv, H, s0));
             TRY(toyinfer_batch_gemv_proj_bf16(L.v_proj, m->p_xn, vc, T, kv, H, s0));
         }
-        TRY(toyinfer_prefill_qknorm_rope_attention_bf16(m->p_q, m->p_k, vc, m->p_o, kc, L.q_norm,
-                                                        L.k_norm, m->rope, eps, hq, hkv, d, T,
-                                                        s0));
+        if (split_attn) {
+            // Q normalised and rotated in place, K into the cache rows, one
+            // launch; then the split kernel on the prepared Q (its fused-Q
+            // form cannot keep the next item's Q in flight).
+            TRYH(launch_qk_norm_rope_rows(m->p_q, m->p_q, u16(L.q_norm), m->p_k, kc,
+                                          u16(L.k_norm), m->rope, eps, T, hq, hkv, d, st));
+            PrefillProblem pp = attn;
+            pp.k = kc;
+            pp.v = vc;
+            TRYH(launch_prefill(pp, st));
+        } else {
+            TRY(toyinfer_prefill_qknorm_rope_attention_bf16(m->p_q, m->p_k, vc, m->p_o, kc,
+                                                            L.q_norm, L.k_norm, m->rope, eps, hq,
+                                                            hkv, d, T, s0));
+        }
         if (gemm) {
             GemmArgs g;
             g.x = m->p_o;

@@ -262,6 +262,16 @@ int toyinfer_batch_gemv_proj_bf16(const void* W, const void* hidden_states, void
 int toyinfer_gemm_segments_bf16(const void* hidden_states, uint32_t num_tokens, uint32_t N,
                                 uint32_t num_segments, const void* const* W, void* const* y,
                                 const uint32_t* rows, int residual, void* stream);
+/* Extension: the gate and up projections of one layer with SwiGLU in the
+ * GEMM epilogue: out[t][m] = bf16(bf16(up) * silu(bf16(gate))), gate =
+ * hidden_states * W_gate^T, up = hidden_states * W_up^T ([M][N] each), i.e.
+ * two toyinfer_batch_gemv_proj_bf16 calls followed by
+ * toyinfer_batch_swiglu_bf16x2 (the sequence at src/transformer.cpp:434-444,
+ * include/kernel_warpper.h:59-64 and :121-126) in one launch, bit for bit.
+ * Needs num_tokens > 4, N % 64 == 0 and 16-byte aligned operands. */
+int toyinfer_gemm_swiglu_bf16(const void* hidden_states, uint32_t num_tokens, uint32_t N,
+                              const void* W_gate, const void* W_up, uint32_t M, void* out,
+                              void* stream);
 
 /* ---- The rest of a Qwen3 decoder layer (for the model harness) ----
  * bf16 tensors need 4-byte alignment (16 bytes and sizes % 8 == 0 take the

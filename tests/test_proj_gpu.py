@@ -251,3 +251,26 @@ def test_gemm_residual_epilogue_equals_projection_then_add(dev):
     torch.cuda.synchronize()
     assert torch.equal(fused.view(torch.int16), ref.view(torch.int16))
 
+
+
+@pytest.mark.parametrize("T,hid,M", [(1371, 1024, 3072), (4096, 1024, 3072), (300, 512, 3072),
+                                     (17, 256, 200)])
+def test_gemm_swiglu_equals_projections_then_swiglu(dev, T, hid, M):
+    """Gate/up with SwiGLU in the GEMM epilogue (192 x 128, 256 x 256 and
+    128 x 128 tiles by grid size; a ragged last tile at M = 200) equals the
+    two projections followed by batch_swiglu_bf16x2, bit for bit."""
+    print(f"[step] gemm swiglu T={T} hid={hid} M={M}", flush=True)
+    g = torch.Generator(device=dev).manual_seed(39)
+    x = torch.randn((T, hid), generator=g, device=dev).to(torch.bfloat16)
+    wg = (torch.randn((M, hid), generator=g, device=dev) * 0.05).to(torch.bfloat16)
+    wu = (torch.randn((M, hid), generator=g, device=dev) * 0.05).to(torch.bfloat16)
+    out = torch.full((T, M), -7.0, dtype=torch.bfloat16, device=dev)
+    attn.gemm_swiglu_bf16(x, T, hid, wg, wu, M, out)
+    gate = torch.empty((T, M), dtype=torch.bfloat16, device=dev)
+    up = torch.empty_like(gate)
+    attn.batch_gemv_proj_bf16(wg, x, gate, T, M, hid)
+    attn.batch_gemv_proj_bf16(wu, x, up, T, M, hid)
+    ref = torch.empty_like(gate)
+    attn.batch_swiglu_bf16x2(gate, up, ref, T, M)
+    torch.cuda.synchronize()
+    assert torch.equal(out.view(torch.int16), ref.view(torch.int16))

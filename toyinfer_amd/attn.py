@@ -63,6 +63,7 @@ SIGNATURES = {
     "toyinfer_gemv_proj_bf162float": (_i32, [_vp, _vp, _vp, _u32, _u32, _vp]),
     "toyinfer_batch_gemv_proj_bf16": (_i32, [_vp, _vp, _vp, _u32, _u32, _u32, _vp]),
     "toyinfer_gemm_segments_bf16": (_i32, [_vp, _u32, _u32, _u32, _vp, _vp, _vp, _i32, _vp]),
+    "toyinfer_gemm_swiglu_bf16": (_i32, [_vp, _u32, _u32, _vp, _vp, _u32, _vp, _vp]),
     "toyinfer_rmsnorm_bf16": (_i32, [_vp, _vp, _vp, _vp, _f32, _u32, _vp]),
     "toyinfer_batch_rmsnorm_bf16": (_i32, [_vp, _vp, _vp, _vp, _f32, _u32, _u32, _vp]),
     "toyinfer_residual_add_bf16": (_i32, [_vp, _vp, _u32, _vp]),
@@ -363,6 +364,15 @@ def gemm_segments_bf16(hidden_states, num_tokens: int, N: int, Ws, ys, rows, res
     _check("gemm_segments_bf16",
            LIB.toyinfer_gemm_segments_bf16(_ptr(hidden_states), num_tokens, N, n, w_arr, y_arr,
                                            r_arr, int(bool(residual)), _stream(stream)))
+
+
+def gemm_swiglu_bf16(hidden_states, num_tokens: int, N: int, W_gate, W_up, M: int, out,
+                     stream=None) -> None:
+    """Gate/up projections with SwiGLU in the epilogue (extension):
+    out = bf16(bf16(up) * silu(bf16(gate)))."""
+    _check("gemm_swiglu_bf16",
+           LIB.toyinfer_gemm_swiglu_bf16(_ptr(hidden_states), num_tokens, N, _ptr(W_gate),
+                                         _ptr(W_up), M, _ptr(out), _stream(stream)))
 
 
 # ------------------------------------------------- rest of a decoder layer

@@ -611,6 +611,29 @@ int toyinfer_gemm_segments_bf16(const void* hidden_states, uint32_t num_tokens, 
     return from_hip(launch_gemm(g, as_stream(stream)));
 }
 
+int toyinfer_gemm_swiglu_bf16(const void* hidden_states, uint32_t num_tokens, uint32_t N,
+                              const void* W_gate, const void* W_up, uint32_t M, void* out,
+                              void* stream) {
+    if (N > kProjMaxN) return TOYINFER_ERR_INVALID_ARGUMENT;
+    for (const void* w : {W_gate, W_up}) {
+        const int st = proj_args(w, hidden_states, out, 2, num_tokens, M, N);
+        if (st != TOYINFER_OK) return st;
+        if (!proj_uses_gemm(num_tokens, N, w, hidden_states)) return TOYINFER_ERR_UNSUPPORTED;
+    }
+    GemmArgs g;
+    g.x = static_cast<const uint16_t*>(hidden_states);
+    g.T = num_tokens;
+    g.N = N;
+    g.nseg = 2;
+    g.w[0] = static_cast<const uint16_t*>(W_gate);
+    g.w[1] = static_cast<const uint16_t*>(W_up);
+    g.y[0] = static_cast<uint16_t*>(out);
+    g.rows[0] = M;
+    g.rows[1] = M;
+    g.swiglu = true;
+    return from_hip(launch_gemm(g, as_stream(stream)));
+}
+
 static bool bf16_ok(const void* p) { return p && aligned(p, 4); }
 
 int toyinfer_rmsnorm_bf16(const void* input, const void* weight, void* output, float* sum,

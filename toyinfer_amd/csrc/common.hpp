@@ -101,6 +101,13 @@ __device__ __forceinline__ uint4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t v
     return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, 0, 0));
 }
 
+// up * silu(gate) on bf16 values (as floats), silu(g) = g / (1 + exp(-g)),
+// written as the reference's SwiGLU kernel computes it.
+__device__ __forceinline__ float swiglu1(float g, float u) {
+    const float silu = g * (1.0f / (1.0f + expf(-g)));
+    return u * silu;
+}
+
 // 16 bytes from global memory into LDS at `lds` (buffer-load DMA: the 64
 // lanes' 16-byte chunks land contiguously in lane order from the wave's
 // first lane's address).

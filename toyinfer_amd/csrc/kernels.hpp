@@ -181,6 +181,9 @@ struct GemmArgs {
     uint16_t* y[3] = {nullptr, nullptr, nullptr};
     uint32_t rows[3] = {0, 0, 0};
     bool residual = false;
+    // SwiGLU epilogue: nseg = 2, w[0] gate and w[1] up (rows[0] == rows[1]),
+    // y[0][t][m] = bf16(bf16(up) * silu(bf16(gate))).
+    bool swiglu = false;
 };
 hipError_t launch_gemm(const GemmArgs& g, hipStream_t stream);
 

@@ -101,10 +101,6 @@ __global__ void residual_add_kernel(const uint16_t* __restrict__ residual,
     }
 }
 
-__device__ __forceinline__ float swiglu1(float g, float u) {
-    const float silu = g * (1.0f / (1.0f + expf(-g)));
-    return u * silu;
-}
 
 // out[i] = bf16(up[i] * silu(gate[i])), silu(g) = g / (1 + exp(-g)).
 template <int VEC>

@@ -182,6 +182,7 @@ using GmMini = GmCfg<64, 64, 2, 2, 4, 128>;  // 4 waves of 32 x 32
 using GmMini64 = GmCfg<64, 64, 2, 2, 4, 64>;
 using GmSmall = GmCfg<128, 128, 2, 2, 2>;  // 4 waves of 64 x 64, 2 workgroups per CU
 using GmMid = GmCfg<128, 192, 2, 2, 2>;    // 4 waves of 64 x 96, 2 workgroups per CU (80 KB LDS each)
+using GmTall = GmCfg<192, 128, 2, 2, 2>;   // 4 waves of 96 x 64, 2 workgroups per CU (80 KB LDS each)
 using GmLarge = GmCfg<256, 256, 2, 4, 1>;  // 8 waves of 128 x 64
 
 // LDS rows of BK bf16 (CPR 16-byte chunks); chunk c of row r sits at
@@ -220,9 +221,24 @@ __device__ __forceinline__ GmTile gm_tile(uint32_t b, uint32_t n_tt, uint32_t n_
     return {in / gsize, first_tm + in % gsize};
 }
 
-template <typename C>
+// Output tiles of one launch: BN columns of the stacked segments, or with
+// the SwiGLU epilogue BN / 2 columns of the gate/up pair.
+template <typename C, bool SW>
+__device__ __host__ __forceinline__ uint32_t gm_out_tiles(const GemmArgs& g) {
+    if (SW) return (g.rows[0] + C::BN / 2 - 1) / (C::BN / 2);
+    uint32_t n = 0;
+    for (int sg = 0; sg < g.nseg; ++sg) n += (g.rows[sg] + C::BN - 1) / C::BN;
+    return n;
+}
+
+// SW (SwiGLU epilogue): B tile row r belongs to 32-row block b = r / 32;
+// even blocks are gate rows, odd blocks up rows, both of output columns
+// m0 + 32 (b / 2) + r % 32, so a wave's two column blocks (JN = 2) hold
+// gate and up of the same 32 columns and the epilogue pairs them in-lane.
+template <typename C, bool SW>
 __global__ __launch_bounds__(C::THREADS, C::MINB) void gemm_kernel(GemmArgs g) {
     constexpr int IM = C::IM, JN = C::JN;
+    static_assert(!SW || JN == 2, "the SwiGLU pairing needs two column blocks per wave");
     const uint32_t T = g.T, N = g.N;
     const uint16_t* __restrict__ x = g.x;
     // One array per stage (A rows, then B rows), so that the compiler can
@@ -231,22 +247,26 @@ __global__ __launch_bounds__(C::THREADS, C::MINB) void gemm_kernel(GemmArgs g) {
     __shared__ __align__(1024) uint16_t s_1[C::A_ELEMS + C::B_ELEMS];
     // Output tiles run over the segments' rows stacked, each segment
     // starting on a tile boundary.
-    uint32_t n_tm = 0;
-    for (int sg = 0; sg < g.nseg; ++sg) n_tm += (g.rows[sg] + C::BN - 1) / C::BN;
+    const uint32_t n_tm = gm_out_tiles<C, SW>(g);
     const uint32_t n_tt = (T + C::BM - 1) / C::BM;
     const GmTile tile = gm_tile(blockIdx.x, n_tt, n_tm);
     uint32_t tm = tile.tm;
     int seg = 0;
-    while (seg + 1 < g.nseg && tm >= (g.rows[seg] + C::BN - 1) / C::BN) {
-        tm -= (g.rows[seg] + C::BN - 1) / C::BN;
-        ++seg;
+    if (!SW) {
+        while (seg + 1 < g.nseg && tm >= (g.rows[seg] + C::BN - 1) / C::BN) {
+            tm -= (g.rows[seg] + C::BN - 1) / C::BN;
+            ++seg;
+        }
     }
+    constexpr uint32_t TILE_N = SW ? C::BN / 2 : C::BN;  // output columns per tile
     const uint32_t M = g.rows[seg];
     uint16_t* __restrict__ y = g.y[seg];
-    const uint32_t t0 = tile.tt * C::BM, m0 = tm * C::BN;
+    const uint32_t t0 = tile.tt * C::BM, m0 = tm * TILE_N;
     const uint32_t row_bytes = 2 * N;
     const auto ra = make_rsrc(x + (size_t)t0 * N, min((uint32_t)C::BM, T - t0) * row_bytes);
-    const auto rb = make_rsrc(g.w[seg] + (size_t)m0 * N, min((uint32_t)C::BN, M - m0) * row_bytes);
+    const uint32_t b_rows = min(TILE_N, M - m0);
+    const auto rb = make_rsrc(g.w[seg] + (size_t)m0 * N, b_rows * row_bytes);
+    const auto rb_up = make_rsrc(g.w[SW ? 1 : seg] + (size_t)m0 * N, b_rows * row_bytes);
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int wr = wave / C::WGN, wc = wave % C::WGN;
 
@@ -272,7 +292,22 @@ __global__ __launch_bounds__(C::THREADS, C::MINB) void gemm_kernel(GemmArgs g) {
     const uint32_t nk = N / BK;
     auto dma_slice = [&](uint32_t kt, uint16_t* st) __attribute__((always_inline)) {
         gm_dma<C::WAVES, C::A_DMA, C::CPR>(ra, row_bytes, kt * BK * 2, st);
-        gm_dma<C::WAVES, C::B_DMA, C::CPR>(rb, row_bytes, kt * BK * 2, st + C::A_ELEMS);
+        if constexpr (!SW) {
+            gm_dma<C::WAVES, C::B_DMA, C::CPR>(rb, row_bytes, kt * BK * 2, st + C::A_ELEMS);
+        } else {
+            // One DMA instruction fills 64 / CPR rows inside one 32-row block.
+            const int wave_s = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+#pragma unroll
+            for (int j = 0; j < C::B_DMA; ++j) {
+                const int blk = wave_s + C::WAVES * j;
+                const uint32_t r = (64 / C::CPR) * blk + lane / C::CPR;  // tile row
+                const uint32_t b32 = ((64 / C::CPR) * blk) / 32;         // its 32-row block
+                const uint32_t src = 32 * (b32 / 2) + r % 32;            // row of gate / up
+                const uint32_t logical = (lane % C::CPR) ^ (r & 7);
+                dma16(b32 & 1 ? rb_up : rb, st + C::A_ELEMS + 512 * blk,
+                      src * row_bytes + kt * BK * 2 + 16 * logical);
+            }
+        }
     };
     // Step kt: wait for slice kt, barrier, start slice kt + 1 into the stage
     // step kt - 1 read, then KS k-steps of MFMAs from stage kt % 2.
@@ -320,6 +355,22 @@ __global__ __launch_bounds__(C::THREADS, C::MINB) void gemm_kernel(GemmArgs g) {
 
     // C block (i, j): lane l value v is token row 8 (v / 4) + 4 (l / 32) + v % 4,
     // output column l % 32.
+    if constexpr (SW) {
+        // Blocks (i, 0) and (i, 1): gate and up of columns m0 + 32 wc + l % 32.
+        const uint32_t m = m0 + 32 * wc + (lane & 31);
+#pragma unroll
+        for (int i = 0; i < IM; ++i)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                const uint32_t t = t0 + 32 * (IM * wr + i) + 8 * (v / 4) + 4 * (lane >> 5) + (v % 4);
+                if (t < T && m < M) {
+                    const float gt = bf16_to_f32(f32_to_bf16(acc[i][0][v]));
+                    const float up = bf16_to_f32(f32_to_bf16(acc[i][1][v]));
+                    y[(size_t)t * M + m] = f32_to_bf16(swiglu1(gt, up));
+                }
+            }
+        return;
+    }
 #pragma unroll
     for (int i = 0; i < IM; ++i)
 #pragma unroll
@@ -347,11 +398,9 @@ __global__ __launch_bounds__(C::THREADS, C::MINB) void gemm_kernel(GemmArgs g) {
         }
 }
 
-template <typename C>
+template <typename C, bool SW = false>
 uint32_t gemm_tiles(const GemmArgs& g) {
-    uint32_t n_tm = 0;
-    for (int sg = 0; sg < g.nseg; ++sg) n_tm += (g.rows[sg] + C::BN - 1) / C::BN;
-    return ((g.T + C::BM - 1) / C::BM) * n_tm;
+    return ((g.T + C::BM - 1) / C::BM) * gm_out_tiles<C, SW>(g);
 }
 
 template <typename C>
@@ -361,9 +410,9 @@ bool gemm_whole(const GemmArgs& g) {
     return true;
 }
 
-template <typename C>
+template <typename C, bool SW = false>
 hipError_t gemm_launch(const GemmArgs& g, hipStream_t stream) {
-    gemm_kernel<C><<<gemm_tiles<C>(g), C::THREADS, 0, stream>>>(g);
+    gemm_kernel<C, SW><<<gemm_tiles<C, SW>(g), C::THREADS, 0, stream>>>(g);
     return hipGetLastError();
 }
 
@@ -411,6 +460,15 @@ hipError_t launch_batch_proj_bf16(const uint16_t* W, const uint16_t* x, uint16_t
 hipError_t launch_gemm(const GemmArgs& g, hipStream_t stream) {
     // The largest tile whose tiles alone fill every CU once; 64 x 64 below that.
     const uint32_t cus = (uint32_t)gemm_cus();
+    if (g.swiglu) {
+        // Tiles with two column blocks per wave: 256 x 256 when they fill the
+        // CUs; 192 x 128 when 128 x 128 would need a second round and these do
+        // not; else 128 x 128.
+        if (gemm_tiles<GmLarge, true>(g) >= cus) return gemm_launch<GmLarge, true>(g, stream);
+        if (gemm_tiles<GmSmall, true>(g) > 2 * cus && gemm_tiles<GmTall, true>(g) <= 2 * cus)
+            return gemm_launch<GmTall, true>(g, stream);
+        return gemm_launch<GmSmall, true>(g, stream);
+    }
     if (gemm_tiles<GmLarge>(g) >= cus) return gemm_launch<GmLarge>(g, stream);
     // 128 x 128 tiles that overflow the two resident workgroups per CU leave
     // a second, mostly idle round: 128 x 192 tiles, when they fit one round

@@ -425,16 +425,16 @@ int toyinfer_qwen3_prefill(toyinfer_qwen3* m, const uint32_t* token_ids_d, uint3
             g.nseg = 2;
             g.w[0] = u16(L.gate_proj);
             g.w[1] = u16(L.up_proj);
-            g.y[0] = m->p_gate;
-            g.y[1] = m->p_up;
+            g.y[0] = m->p_inter;  // SwiGLU in the epilogue
             g.rows[0] = F;
             g.rows[1] = F;
+            g.swiglu = true;
             TRYH(launch_gemm(g, st));
         } else {
             TRY(toyinfer_batch_gemv_proj_bf16(L.gate_proj, m->p_xn, m->p_gate, T, F, H, s0));
             TRY(toyinfer_batch_gemv_proj_bf16(L.up_proj, m->p_xn, m->p_up, T, F, H, s0));
+            TRY(toyinfer_batch_swiglu_bf16x2(m->p_gate, m->p_up, m->p_inter, T, F, s0));
         }
-        TRY(toyinfer_batch_swiglu_bf16x2(m->p_gate, m->p_up, m->p_inter, T, F, s0));
         if (gemm) {
             GemmArgs g;
             g.x = m->p_inter;

@@ -321,8 +321,9 @@ def bench_decode_contract(dev, stream, steps, warmup, hq=32, hkv=8, d=128, msl=4
             "entry": "toyinfer_attention_bf16_graph", "steps": steps,
             "ms_per_step": round(ms, 5), "value": round(gbs, 1), "unit": "GB/s",
             "note": "KV bytes attended per call / call time; the call also writes the "
-                    f"{hq}x{msl} fp32 probability rows the contract requires (re-reading K "
-                    "for them), O_buffer and O",
+                    f"{hq}x{msl} fp32 probability rows the contract requires (from raw "
+                    "scores the split pass stores when the rows past pos hold its partials, "
+                    "else re-reading K), O_buffer and O",
             "roofline": roofline("hbm", gbs, PEAK_HBM_GBS, "GB/s")}
 
 

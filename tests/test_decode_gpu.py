@@ -47,6 +47,10 @@ REF_CASES = [
     # Long caches: the split partials then live in score rows (several splits).
     ("long msl", 32, 8, 128, 777, 1000, 0.03, 0.017),
     ("long msl d64", 16, 4, 64, 2999, 3001, 0.021, 0.013),
+    # Room past the length for the partials: the split pass also stores the
+    # raw scores, and the score pass rescales them.
+    ("long msl raw scores", 32, 8, 128, 1200, 4096, 0.03, 0.017),
+    ("long msl raw scores d64", 16, 4, 64, 700, 2200, 0.021, 0.013),
 ]
 
 

@@ -237,7 +237,8 @@ static int decode_compat(const void* Q, const void* Ks, const void* Vs, float* s
     const uint32_t sizing = len_mode == kLenHost ? pos + 1 : msl;
     compat_partials(hq, hkv, d, sizing, msl, score, O_buffer, O, &p.splits, &part);
     hipStream_t st = as_stream(stream);
-    hipError_t e = launch_decode_split(p, part, st);
+    hipError_t e = p.splits >= 2 ? launch_decode_split_compat(p, part, st)
+                                 : launch_decode_split(p, part, st);
     if (e != hipSuccess) return from_hip(e);
     return from_hip(launch_decode_finalize_compat(p, part, score, msl, O_buffer,
                                                   static_cast<uint16_t*>(O), st));

@@ -84,13 +84,50 @@ __device__ __forceinline__ v4i16_t ds_read_tr16(const uint16_t* p) {
 constexpr int kMaxSplits = 1024;
 
 
+// Reference-contract decode with the partials in the score rows
+// ([Hq][msl] fp32, part.ml = score, row stride msl).  When the rows past
+// the length L have room for the partials of at least half of the splits,
+// the split pass also stores every raw score (q.k times
+// log2(e)/sqrt(D)) at its position and puts the partials after them: the
+// probabilities are then a rescale of the stored scores, with no second
+// pass over K.  Otherwise (a position near msl) the partials start at the
+// row head and the score pass recomputes q.k.  Every kernel of the
+// contract path derives the same layout from L on the device, so a graph
+// captured once serves every position.
+struct CompatLayout {
+    bool raw;
+    uint32_t splits;       // splits that carry a slice (raw: fewer than the grid holds)
+    DecodePartials part;
+};
+
+__device__ __forceinline__ CompatLayout compat_layout(const DecodeProblem& p,
+                                                      const DecodePartials& part, uint32_t L) {
+    const uint32_t room = p.len_cap - L;
+    uint32_t fit = room / (p.d + 2);
+    if (fit > p.splits) fit = p.splits;
+    CompatLayout c;
+    // Fewer splits stream more slowly (B=1, 32/8 heads, pos 32767 of 40960:
+    // 63 of 96 splits take 29.4 us where 96 take 23); at half the splits
+    // that loss is about what the skipped pass over K would cost.
+    c.raw = fit >= 2 && 2 * fit >= p.splits;
+    c.splits = c.raw ? fit : p.splits;
+    c.part = part;
+    if (c.raw) {
+        c.part.ml = part.ml + L;
+        c.part.o = part.ml + L + 2 * (size_t)fit;
+    }
+    return c;
+}
+
 // Workgroup blockIdx.x takes a fixed slice [t_begin, t_end) of the positions
 // (split_range), its wave w the 32-row chunks w, w+4, ... of that slice.
 // PRO: the engine's form with the token's q/k norm + RoPE and cache-row
 // writes folded in (DecodePrologue).
-template <int D, bool PRO>
+// COMPAT: the reference-contract pass (B = 1, partials in the score rows,
+// raw scores stored when compat_layout says so).
+template <int D, bool PRO, bool COMPAT = false>
 __device__ __forceinline__ void decode_split_body(const DecodeProblem& p,
-                                                  const DecodePartials& part, float scale_log2,
+                                                  const DecodePartials& part_in, float scale_log2,
                                                   const DecodePrologue& pro) {
     constexpr int NLD = D / 32;  // 16-byte loads per row and lane == QK k-steps
     constexpr int NDB = D / 16;  // PV output blocks of 16 dims
@@ -115,8 +152,18 @@ __device__ __forceinline__ void decode_split_body(const DecodeProblem& p,
     const int64_t bh0 = (int64_t)b * p.hq + h0;
 
     const uint32_t L = seq_length(p, b);
+    DecodePartials part = part_in;
+    uint32_t nsplits = p.splits;
+    bool raw = false;
+    if constexpr (COMPAT) {
+        const CompatLayout cl = compat_layout(p, part_in, L);
+        if (blockIdx.x >= cl.splits) return;  // raw layout: this split carries no slice
+        part = cl.part;
+        nsplits = cl.splits;
+        raw = cl.raw;
+    }
     uint32_t t_begin, t_end;
-    split_range(L, p.splits, blockIdx.x, &t_begin, &t_end);
+    split_range(L, nsplits, blockIdx.x, &t_begin, &t_end);
     if (t_begin >= t_end) {
         if (threadIdx.x < nh) {
             float* ml = part.ml + (bh0 + threadIdx.x) * part.ml_head + blockIdx.x * 2;
@@ -285,6 +332,16 @@ __device__ __forceinline__ void decode_split_body(const DecodeProblem& p,
 #pragma unroll
             for (int i = 0; i < NLD; ++i) st[tt] = mfma16x16x32(ka[tt][i], qb[i], st[tt]);
         }
+        if (COMPAT && raw && (uint32_t)n < nh) {
+            float* srow = part_in.ml + (int64_t)(h0 + n) * part_in.ml_head;
+#pragma unroll
+            for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const uint32_t t = t0 + 16 * tt + 4 * g + r;
+                    if (t < t_end) srow[t] = st[tt][r] * scale_log2;
+                }
+        }
         // The load registers are free: the next chunk's loads overlap this
         // chunk's softmax and P.V.
         const uint32_t nxt = cur + kDecWaves;
@@ -378,6 +435,14 @@ template <int D>
 __global__ __launch_bounds__(256, 3) void decode_split_kernel(DecodeProblem p, DecodePartials part,
                                                               float scale_log2) {
     decode_split_body<D, false>(p, part, scale_log2, DecodePrologue{});
+}
+
+// Reference-contract split pass (compat_layout).
+template <int D>
+__global__ __launch_bounds__(256, 3) void decode_split_compat_kernel(DecodeProblem p,
+                                                                     DecodePartials part,
+                                                                     float scale_log2) {
+    decode_split_body<D, false, true>(p, part, scale_log2, DecodePrologue{});
 }
 
 // The engine's single-sequence grid (splits x Hkv workgroups) is far below
@@ -724,8 +789,9 @@ template <int D>
 __global__ __launch_bounds__(kCombineThreads) void decode_compat_merge_kernel(
     DecodeProblem p, DecodePartials part, float* o_buffer, uint16_t* o) {
     const uint32_t h = blockIdx.x;
+    const CompatLayout cl = compat_layout(p, part, seq_length(p, 0));
     float M, den;
-    const float my_o = merge_splits<D>(part, h, p.splits, &M, &den);
+    const float my_o = merge_splits<D>(cl.part, h, cl.splits, &M, &den);
     if (threadIdx.x < D) o_buffer[(int64_t)h * D + threadIdx.x] = my_o;
     if (threadIdx.x == 0)
         stash_put(o + (int64_t)h * D, M == -INFINITY ? 0.0f : M, den > 0.0f ? 1.0f / den : 0.0f);
@@ -752,6 +818,25 @@ __global__ __launch_bounds__(256) void decode_compat_score_kernel(
     const uint32_t h0 = kvh * group + hgi * kDecMaxHeads;
     const uint32_t nh = min((uint32_t)kDecMaxHeads, group - hgi * kDecMaxHeads);
     const uint32_t L = seq_length(p, 0);
+    // Raw layout: the split pass stored q.k * log2(e)/sqrt(D) at every
+    // position below L; the probability is a rescale of it.  Wave w takes
+    // heads w, w+4, ... of the group, lane l positions 2l, 2l+1 of the
+    // wave's 128 (whole lines per instruction).
+    DecodePartials sp{};
+    sp.ml = score;
+    if (compat_layout(p, sp, L).raw) {
+        const uint32_t tb = blockIdx.x * kDecIterRows + 2 * lane;
+        for (uint32_t hs = wave; hs < nh; hs += kDecWaves) {
+            float* row = score + (int64_t)(h0 + hs) * msl;
+            const float2 sv = stash_get(o + (int64_t)(h0 + hs) * D);
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+                const uint32_t t = tb + e;
+                if (t < msl) row[t] = t < L ? __builtin_amdgcn_exp2f(row[t] - sv.x) * sv.y : 0.0f;
+            }
+        }
+        return;
+    }
     const uint32_t t0 = blockIdx.x * kDecIterRows + wave * kDecWaveRows;
     if (t0 >= msl) return;
     const bool has = (uint32_t)n < nh;
@@ -853,6 +938,17 @@ hipError_t launch_decode_split(const DecodeProblem& p, const DecodePartials& par
                                hipStream_t stream) {
     if (p.d == 64) return launch_split_t<64>(p, part, stream);
     return launch_split_t<128>(p, part, stream);
+}
+
+hipError_t launch_decode_split_compat(const DecodeProblem& p, const DecodePartials& part,
+                                      hipStream_t stream) {
+    const dim3 grid(p.splits, p.hkv * decode_head_groups(p.hq / p.hkv), 1);
+    const float sl2 = kLog2e / sqrtf((float)p.d);
+    if (p.d == 64)
+        hipLaunchKernelGGL((decode_split_compat_kernel<64>), grid, dim3(256), 0, stream, p, part, sl2);
+    else
+        hipLaunchKernelGGL((decode_split_compat_kernel<128>), grid, dim3(256), 0, stream, p, part, sl2);
+    return hipGetLastError();
 }
 
 hipError_t launch_decode_split_prologue(const DecodeProblem& p, const DecodePartials& part,

@@ -59,6 +59,12 @@ struct DecodeProblem {
 // Split pass: grid (splits, Hkv * head groups, B).
 hipError_t launch_decode_split(const DecodeProblem& p, const DecodePartials& part,
                                hipStream_t stream);
+// The reference contract's split pass (B = 1, two or more splits, partials in
+// the score rows: part.ml = score, ml_head = o_head = len_cap = msl): where
+// the rows past the length have room, it also stores the raw scores and
+// moves the partials behind them; launch_decode_finalize_compat follows it.
+hipError_t launch_decode_split_compat(const DecodeProblem& p, const DecodePartials& part,
+                                      hipStream_t stream);
 
 // The engine's decode step (one sequence, the token at position L - 1 with
 // L from len_dev) folds its pre-attention row work into the split pass:

@@ -54,14 +54,18 @@ def check_logits(got, exp, label):
         f"{label}: max {d.max():.3g} mean {d.mean():.3g}"
 
 
+# max_seq_len 64: the attention pass gives each split a fixed 128-row slice of
+# the cache and requests it before the device length arrives; 16384 (more
+# rows than 96 splits x 128): slices follow the length instead.
+@pytest.mark.parametrize("msl", [64, 16384])
 @pytest.mark.parametrize("graph", [False, True])
-def test_wide_prefill_and_decode_vs_oracle(dev, weights_wide, graph):
-    print(f"[step] wide prefill 24 + 3 decode steps, graph={graph}", flush=True)
+def test_wide_prefill_and_decode_vs_oracle(dev, weights_wide, graph, msl):
+    print(f"[step] wide prefill 24 + 3 decode steps, graph={graph}, max_seq_len={msl}", flush=True)
     host, dw = weights_wide
     T, steps = 24, 3
     ids = np.random.default_rng(SEED + int(graph)).integers(0, WIDE["vocab_size"], T)
     ids = ids.astype(np.uint32)
-    m = qwen3.Qwen3(qwen3.Config(**WIDE), dw)
+    m = qwen3.Qwen3(qwen3.Config(**dict(WIDE, max_seq_len=msl)), dw)
     id_t = torch.from_numpy(ids.view(np.int32)).to(dev)
     m.prefill(id_t, T)
     got = m.logits_host()

@@ -151,6 +151,37 @@ __device__ __forceinline__ void decode_split_body(const DecodeProblem& p,
     const uint32_t nh = min((uint32_t)kDecMaxHeads, group - hgi * kDecMaxHeads);
     const int64_t bh0 = (int64_t)b * p.hq + h0;
 
+    // Global loads: instruction j of lane l reads row (l>>3) + 8*(j / CPL) of the
+    // wave's 32, 16-byte chunk (l&7) + 8*(j % CPL): each instruction covers 8
+    // whole 128-byte lines, the shape the memory pipeline streams fastest.
+    // The cache is read exactly once, so the loads carry the non-temporal hint
+    // (6.4-6.6 TB/s for this pattern where plain loads reach 5.6-5.9).
+    constexpr int CPR = D / 8;        // 16-byte chunks per row
+    constexpr int CPL = CPR / 8;      // 128-byte lines per row
+    constexpr int NJ = kDecWaveRows * CPR / 64;
+    const int lrow = lane >> 3, lchunk = lane & 7;
+    const int64_t row_stride = (int64_t)p.hkv * D;
+    const uint16_t* kbase = p.k + (int64_t)b * p.kv_stride + (int64_t)kvh * D;
+    const uint16_t* vbase = p.v + (int64_t)b * p.kv_stride + (int64_t)kvh * D;
+    uint4 kr[NJ], vr[NJ];
+    auto load_rows = [&](uint32_t tb, uint32_t lim) {  // rows tb .. tb+31, clamped below lim
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) {
+            const uint32_t t = tb + lrow + 8 * (j / CPL);
+            const uint32_t tc = t < lim ? t : lim - 1;
+            const int64_t off = (int64_t)tc * row_stride + 8 * (lchunk + 8 * (j % CPL));
+            kr[j] = ldg16_nt(kbase + off);
+            vr[j] = ldg16_nt(vbase + off);
+        }
+    };
+    // PRO with fixed slices (p.slice_rows == 128: split s owns rows
+    // [128 s, 128 s + 128), one 32-row chunk per wave): the slice does not
+    // depend on the length, so the chunk is requested before the device
+    // length arrives, its rows clamped to the cache (len_cap); rows at or past
+    // the length are masked and their V zeroed below.
+    const bool fixed = PRO && p.slice_rows != 0;
+    if (fixed) load_rows(blockIdx.x * kDecIterRows + wave * kDecWaveRows, p.len_cap);
+
     const uint32_t L = seq_length(p, b);
     DecodePartials part = part_in;
     uint32_t nsplits = p.splits;
@@ -163,7 +194,12 @@ __device__ __forceinline__ void decode_split_body(const DecodeProblem& p,
         raw = cl.raw;
     }
     uint32_t t_begin, t_end;
-    split_range(L, nsplits, blockIdx.x, &t_begin, &t_end);
+    if (fixed) {
+        t_begin = blockIdx.x * kDecIterRows;
+        t_end = min(t_begin + kDecIterRows, L);
+    } else {
+        split_range(L, nsplits, blockIdx.x, &t_begin, &t_end);
+    }
     if (t_begin >= t_end) {
         if (threadIdx.x < nh) {
             float* ml = part.ml + (bh0 + threadIdx.x) * part.ml_head + blockIdx.x * 2;
@@ -214,9 +250,6 @@ __device__ __forceinline__ void decode_split_body(const DecodeProblem& p,
         }
     }
 
-    const int64_t row_stride = (int64_t)p.hkv * D;
-    const uint16_t* kbase = p.k + (int64_t)b * p.kv_stride + (int64_t)kvh * D;
-    const uint16_t* vbase = p.v + (int64_t)b * p.kv_stride + (int64_t)kvh * D;
     uint16_t* vs = reinterpret_cast<uint16_t*>(s_raw) + wave * V_ELEMS;
 
     f32x4_t acc[NDB];
@@ -236,39 +269,32 @@ __device__ __forceinline__ void decode_split_body(const DecodeProblem& p,
         }
     }
 
-    // Global loads: instruction j of lane l reads row (l>>3) + 8*(j / CPL) of the
-    // wave's 32, 16-byte chunk (l&7) + 8*(j % CPL): each instruction covers 8
-    // whole 128-byte lines, the shape the memory pipeline streams fastest.
-    // The cache is read exactly once, so the loads carry the non-temporal hint
-    // (6.4-6.6 TB/s for this pattern where plain loads reach 5.6-5.9).
-    constexpr int CPR = D / 8;        // 16-byte chunks per row
-    constexpr int CPL = CPR / 8;      // 128-byte lines per row
-    constexpr int NJ = kDecWaveRows * CPR / 64;
-    const int lrow = lane >> 3, lchunk = lane & 7;
     int st_off[NJ];  // LDS element offset of instruction j's chunk
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {
         const int row = lrow + 8 * (j / CPL), chunk = lchunk + 8 * (j % CPL);
         st_off[j] = row * D + 8 * (chunk ^ vt_swz<D>(row));
     }
-    uint4 kr[NJ], vr[NJ];
-    auto load_kv = [&](uint32_t tb) {  // rows tb .. tb+31, clamped below t_end
+    // PRO: row t_end - 1 is not written yet and rows past it hold older or
+    // no data, so V of rows at or past t_end is zeroed (their scores are
+    // masked, but 0 * NaN is NaN).
+    auto zero_v_past_end = [&](uint32_t tb) {
 #pragma unroll
-        for (int j = 0; j < NJ; ++j) {
-            const uint32_t t = tb + lrow + 8 * (j / CPL);
-            const uint32_t tc = t < t_end ? t : t_end - 1;
-            const int64_t off = (int64_t)tc * row_stride + 8 * (lchunk + 8 * (j % CPL));
-            kr[j] = ldg16_nt(kbase + off);
-            vr[j] = ldg16_nt(vbase + off);
-            // PRO: row t_end - 1 is not written yet, so the rows clamped to it
-            // get zero V (their scores are masked, but 0 * NaN is NaN).
-            if (PRO && t >= t_end) vr[j] = make_uint4(0, 0, 0, 0);
-        }
+        for (int j = 0; j < NJ; ++j)
+            if (tb + lrow + 8 * (j / CPL) >= t_end) vr[j] = make_uint4(0, 0, 0, 0);
+    };
+    auto load_kv = [&](uint32_t tb) {
+        load_rows(tb, t_end);
+        if (PRO) zero_v_past_end(tb);
     };
     // Chunk c = rows [t_begin + 32c, t_begin + 32c + 32) (masked at t_end).
     const uint32_t nchunks = (t_end - t_begin + kDecWaveRows - 1) / kDecWaveRows;
     uint32_t cur = wave;
-    if (cur < nchunks) load_kv(t_begin + cur * kDecWaveRows);
+    if (fixed) {
+        if (cur < nchunks) zero_v_past_end(t_begin + cur * kDecWaveRows);
+    } else if (cur < nchunks) {
+        load_kv(t_begin + cur * kDecWaveRows);
+    }
 
     // PRO: normalise + rotate the rows into LDS (row kNewV is a copy), the
     // token's k/v rows also to cache row pos (one head group writes them),

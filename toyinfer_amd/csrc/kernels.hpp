@@ -54,6 +54,10 @@ struct DecodeProblem {
     uint32_t len_host;   // kLenHost: the length; otherwise unused
     uint32_t len_cap;    // upper bound for device lengths (grid sizing, clamping)
     uint32_t splits;
+    // Prologue pass only: 0, or 128 when splits * 128 >= len_cap, so that
+    // split s owns cache rows [128 s, 128 s + 128) whatever the length and
+    // loads them before the device length arrives.
+    uint32_t slice_rows;
 };
 
 // Split pass: grid (splits, Hkv * head groups, B).

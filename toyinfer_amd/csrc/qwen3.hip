@@ -206,6 +206,7 @@ int decode_body(toyinfer_qwen3* m) {
         ap.len_dev = m->seq_len;
         ap.len_cap = msl;
         ap.splits = m->splits;
+        ap.slice_rows = (uint64_t)m->splits * 128 >= msl ? 128 : 0;
         DecodePrologue pro;
         pro.q_w = u16(L.q_norm);
         pro.k_raw = m->d_k;

@@ -1,8 +1,9 @@
 """Build the gfx950 attention library in-tree.
 
 ``python -m toyinfer_amd.build`` (or ``__graft_entry__.build()``) compiles
-every HIP and host C++ source under ``toyinfer_amd/csrc`` with hipcc into
-``toyinfer_amd/lib/libtoyinfer_attn.so``.  Packed-FP32 VALU forms are
+every HIP and host C++ source under ``toyinfer_amd/csrc`` with hipcc (one
+object per source, compiled in parallel under ``toyinfer_amd/lib/obj``) and
+links them into ``toyinfer_amd/lib/libtoyinfer_attn.so``.  Packed-FP32 VALU forms are
 disabled on purpose: some of their encodings have produced silently wrong
 results on the target machines, and the kernels do not depend on them.
 """
@@ -59,16 +60,30 @@ def build_synth(verbose: bool = False) -> str:
     return SYNTH_PATH
 
 
-def build_library(verbose: bool = False) -> str:
-    os.makedirs(LIB_DIR, exist_ok=True)
-    tmp = LIB_PATH + ".tmp"
-    cmd = [hipcc(), *HIP_FLAGS, "-shared", "-o", tmp, *sources()]
+def _run(cmd, verbose):
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         sys.stderr.write(res.stdout + res.stderr)
         raise RuntimeError("hipcc failed building libtoyinfer_attn.so")
+
+
+def build_library(verbose: bool = False) -> str:
+    """One object per source (in parallel), then one shared library."""
+    from concurrent.futures import ThreadPoolExecutor
+
+    os.makedirs(LIB_DIR, exist_ok=True)
+    obj_dir = os.path.join(LIB_DIR, "obj")
+    os.makedirs(obj_dir, exist_ok=True)
+    srcs = sources()
+    objs = [os.path.join(obj_dir, os.path.basename(src) + ".o") for src in srcs]
+    cmds = [[hipcc(), *HIP_FLAGS, "-c", "-o", obj, src] for src, obj in zip(srcs, objs)]
+    workers = min(len(cmds), max(1, min(8, os.cpu_count() or 1)))
+    with ThreadPoolExecutor(max_workers=workers) as pool:
+        list(pool.map(lambda c: _run(c, verbose), cmds))
+    tmp = LIB_PATH + ".tmp"
+    _run([hipcc(), *HIP_FLAGS, "-shared", "-o", tmp, *objs], verbose)
     os.replace(tmp, LIB_PATH)
     return LIB_PATH
 

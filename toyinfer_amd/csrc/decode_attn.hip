@@ -125,7 +125,9 @@ __device__ __forceinline__ CompatLayout compat_layout(const DecodeProblem& p,
 // writes folded in (DecodePrologue).
 // COMPAT: the reference-contract pass (B = 1, partials in the score rows,
 // raw scores stored when compat_layout says so).
-template <int D, bool PRO, bool COMPAT = false>
+// FIXED (PRO only): p.slice_rows == 128, split s owns rows [128 s, 128 s +
+// 128) whatever the length.
+template <int D, bool PRO, bool COMPAT = false, bool FIXED = false>
 __device__ __forceinline__ void decode_split_body(const DecodeProblem& p,
                                                   const DecodePartials& part_in, float scale_log2,
                                                   const DecodePrologue& pro) {
@@ -174,15 +176,66 @@ __device__ __forceinline__ void decode_split_body(const DecodeProblem& p,
             vr[j] = ldg16_nt(vbase + off);
         }
     };
-    // PRO with fixed slices (p.slice_rows == 128: split s owns rows
-    // [128 s, 128 s + 128), one 32-row chunk per wave): the slice does not
-    // depend on the length, so the chunk is requested before the device
-    // length arrives, its rows clamped to the cache (len_cap); rows at or past
-    // the length are masked and their V zeroed below.
-    const bool fixed = PRO && p.slice_rows != 0;
-    if (fixed) load_rows(blockIdx.x * kDecIterRows + wave * kDecWaveRows, p.len_cap);
+    // PRO: rows of LPR lanes each (lane group prow) load the q heads (rows
+    // 0 .. nh-1) and the token's raw k and v rows (rows kDecMaxHeads,
+    // kDecMaxHeads + 1; every workgroup loads them, the one whose slice holds
+    // the token uses them).  Nothing here depends on the device length (the
+    // rotary row of the position is pro.rope), so these loads go out first
+    // and the arithmetic waits for them alone.
+    constexpr int LPR = D / 16;
+    constexpr int kNewK = kDecMaxHeads, kNewV = kDecMaxHeads + 1;
+    __shared__ __align__(16) uint16_t s_pro[PRO ? (kDecMaxHeads + 2) * D : 8];
+    const int prow = threadIdx.x / LPR, pc = threadIdx.x % LPR;
+    int pmode = -1;  // -1: no prologue row in this lane
+    NormRopeIn pin;
+    uint4 pro_a, pro_b;  // the lane's two output chunks of its prologue row
+    if constexpr (PRO) {
+        // Every lane runs one unconditional load sequence (per-lane sources;
+        // lanes without a row re-read q row 0, the v row loads weights and
+        // angles it does not use): loads under a branch would make the
+        // compiler wait for every load in flight, the K/V chunk's included,
+        // before the arithmetic.
+        const bool is_q = (uint32_t)prow < nh, is_k = prow == kNewK, is_v = prow == kNewV;
+        pmode = is_q || is_k ? (kRowNorm | kRowRope) : (is_v ? 0 : -1);
+        const uint16_t* src = is_k   ? pro.k_raw + (int64_t)kvh * D
+                              : is_v ? pro.v_raw + (int64_t)kvh * D
+                                     : p.q + (bh0 + (is_q ? prow : 0)) * D;
+        const uint16_t* wsrc = is_k ? pro.k_w : pro.q_w;
+        pin = norm_rope_load<D>(src, wsrc, nullptr, pro.rope, 0, pc, kRowNorm | kRowRope);
+        // Keep these loads ahead of the K/V chunk's in the instruction
+        // stream: loads complete in order, so the prologue's wait then leaves
+        // the chunk in flight.
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    // Normalise + rotate the rows (row kNewV is a copy) into LDS; needs no
+    // length.
+    auto pro_compute = [&]() {
+        if (pmode >= 0) {
+            norm_rope_compute<D>(pin, true, pro.eps, 0, pmode, &pro_a, &pro_b);
+            *reinterpret_cast<uint4*>(s_pro + prow * D + 8 * pc) = pro_a;
+            *reinterpret_cast<uint4*>(s_pro + prow * D + 8 * pc + D / 2) = pro_b;
+        }
+    };
 
-    const uint32_t L = seq_length(p, b);
+    // FIXED: the slice does not depend on the length, so its chunk (one
+    // 32-row chunk per wave) is requested before the device length arrives,
+    // its rows clamped to the cache (len_cap); rows at or past the length are
+    // masked and their V zeroed in the loop.  The prologue rows are computed
+    // meanwhile.
+    // PRO takes its length from len_dev (kLenDevice); FIXED requests it
+    // behind the chunk (a scalar load: its wait leaves the vector loads in
+    // flight) and uses it after the prologue arithmetic.
+    uint32_t len_pro = 0;
+    if constexpr (FIXED) {
+        load_rows(blockIdx.x * kDecIterRows + wave * kDecWaveRows, p.len_cap);
+        __builtin_amdgcn_sched_barrier(0);
+        len_pro = p.len_dev[b];
+        pro_compute();
+    } else if constexpr (PRO) {
+        len_pro = p.len_dev[b];
+    }
+
+    const uint32_t L = PRO ? min(len_pro, p.len_cap) : seq_length(p, b);
     DecodePartials part = part_in;
     uint32_t nsplits = p.splits;
     bool raw = false;
@@ -194,7 +247,7 @@ __device__ __forceinline__ void decode_split_body(const DecodeProblem& p,
         raw = cl.raw;
     }
     uint32_t t_begin, t_end;
-    if (fixed) {
+    if (FIXED) {
         t_begin = blockIdx.x * kDecIterRows;
         t_end = min(t_begin + kDecIterRows, L);
     } else {
@@ -209,33 +262,8 @@ __device__ __forceinline__ void decode_split_body(const DecodeProblem& p,
         return;
     }
 
-    // PRO: rows of LPR lanes each (lane group prow) load the q heads (rows
-    // 0 .. nh-1) and, in the workgroup whose slice holds the token, its raw
-    // k and v rows (rows kDecMaxHeads, kDecMaxHeads + 1); these loads go out
-    // before the first K/V chunk's, the arithmetic waits for them alone.
-    constexpr int LPR = D / 16;
-    constexpr int kNewK = kDecMaxHeads, kNewV = kDecMaxHeads + 1;
-    __shared__ __align__(16) uint16_t s_pro[PRO ? (kDecMaxHeads + 2) * D : 8];
     const uint32_t pos = L - 1;
     const bool has_new = PRO && t_end == L;
-    const int prow = threadIdx.x / LPR, pc = threadIdx.x % LPR;
-    int pmode = -1;  // -1: no prologue row in this lane
-    NormRopeIn pin;
-    if constexpr (PRO) {
-        if ((uint32_t)prow < nh) {
-            pmode = kRowNorm | kRowRope;
-            pin = norm_rope_load<D>(p.q + (bh0 + prow) * D, pro.q_w, nullptr, pro.rope, pos, pc,
-                                    pmode);
-        } else if (has_new && prow == kNewK) {
-            pmode = kRowNorm | kRowRope;
-            pin = norm_rope_load<D>(pro.k_raw + (int64_t)kvh * D, pro.k_w, nullptr, pro.rope, pos,
-                                    pc, pmode);
-        } else if (has_new && prow == kNewV) {
-            pmode = 0;
-            pin = norm_rope_load<D>(pro.v_raw + (int64_t)kvh * D, nullptr, nullptr, nullptr, pos,
-                                    pc, pmode);
-        }
-    }
 
     // B operand Q^T: column n = head h0 + n (zero beyond the group).
     bf16x8_t qb[NLD];
@@ -283,34 +311,24 @@ __device__ __forceinline__ void decode_split_body(const DecodeProblem& p,
         for (int j = 0; j < NJ; ++j)
             if (tb + lrow + 8 * (j / CPL) >= t_end) vr[j] = make_uint4(0, 0, 0, 0);
     };
-    auto load_kv = [&](uint32_t tb) {
-        load_rows(tb, t_end);
-        if (PRO) zero_v_past_end(tb);
-    };
+    auto load_kv = [&](uint32_t tb) { load_rows(tb, t_end); };
     // Chunk c = rows [t_begin + 32c, t_begin + 32c + 32) (masked at t_end).
     const uint32_t nchunks = (t_end - t_begin + kDecWaveRows - 1) / kDecWaveRows;
     uint32_t cur = wave;
-    if (fixed) {
-        if (cur < nchunks) zero_v_past_end(t_begin + cur * kDecWaveRows);
-    } else if (cur < nchunks) {
-        load_kv(t_begin + cur * kDecWaveRows);
-    }
+    // PRO: a wave without a chunk still loads one (rows clamped to t_end - 1,
+    // never used), so that no branch separates these loads from the
+    // prologue's.
+    if (!FIXED && (PRO || cur < nchunks)) load_kv(t_begin + cur * kDecWaveRows);
 
-    // PRO: normalise + rotate the rows into LDS (row kNewV is a copy), the
-    // token's k/v rows also to cache row pos (one head group writes them),
-    // then Q^T from LDS.
+    // PRO: the token's k/v rows also to cache row pos (one head group writes
+    // them), then Q^T from LDS.
     if constexpr (PRO) {
-        if (pmode >= 0) {
-            uint4 a, b;
-            norm_rope_compute<D>(pin, true, pro.eps, pos, pmode, &a, &b);
-            *reinterpret_cast<uint4*>(s_pro + prow * D + 8 * pc) = a;
-            *reinterpret_cast<uint4*>(s_pro + prow * D + 8 * pc + D / 2) = b;
-            if (prow >= kNewK && hgi == 0) {
-                uint16_t* crow = (prow == kNewK ? pro.k_cache : pro.v_cache) +
-                                 ((int64_t)pos * p.hkv + kvh) * D;
-                *reinterpret_cast<uint4*>(crow + 8 * pc) = a;
-                *reinterpret_cast<uint4*>(crow + 8 * pc + D / 2) = b;
-            }
+        if constexpr (!FIXED) pro_compute();
+        if (pmode >= 0 && prow >= kNewK && has_new && hgi == 0) {
+            uint16_t* crow = (prow == kNewK ? pro.k_cache : pro.v_cache) +
+                             ((int64_t)pos * p.hkv + kvh) * D;
+            *reinterpret_cast<uint4*>(crow + 8 * pc) = pro_a;
+            *reinterpret_cast<uint4*>(crow + 8 * pc + D / 2) = pro_b;
         }
         lds_barrier();
         const bool has = (uint32_t)n < nh;
@@ -345,6 +363,7 @@ __device__ __forceinline__ void decode_split_body(const DecodeProblem& p,
         }
         // V -> the same tile (LDS operations of a wave complete in order, so
         // the K reads above see K).
+        if (PRO) zero_v_past_end(t0);
 #pragma unroll
         for (int j = 0; j < NJ; ++j) *reinterpret_cast<uint4*>(vs + st_off[j]) = vr[j];
         if (PRO && put_new)
@@ -473,12 +492,12 @@ __global__ __launch_bounds__(256, 3) void decode_split_compat_kernel(DecodeProbl
 
 // The engine's single-sequence grid (splits x Hkv workgroups) is far below
 // one per CU, so the register budget is not cut for occupancy.
-template <int D>
+template <int D, bool FIXED>
 __global__ __launch_bounds__(256, 1) void decode_split_pro_kernel(DecodeProblem p,
                                                                   DecodePartials part,
                                                                   float scale_log2,
                                                                   DecodePrologue pro) {
-    decode_split_body<D, true>(p, part, scale_log2, pro);
+    decode_split_body<D, true, false, FIXED>(p, part, scale_log2, pro);
 }
 
 // Merge the splits of one (sequence, q-head) in a 256-thread block.  The
@@ -758,7 +777,12 @@ hipError_t launch_split_pro_t(const DecodeProblem& p, const DecodePartials& part
     const uint32_t group = p.hq / p.hkv;
     const dim3 grid(p.splits, p.hkv * decode_head_groups(group), 1);
     const float sl2 = kLog2e / sqrtf((float)D);
-    hipLaunchKernelGGL((decode_split_pro_kernel<D>), grid, dim3(256), 0, st, p, part, sl2, pro);
+    if (p.slice_rows != 0)
+        hipLaunchKernelGGL((decode_split_pro_kernel<D, true>), grid, dim3(256), 0, st, p, part, sl2,
+                           pro);
+    else
+        hipLaunchKernelGGL((decode_split_pro_kernel<D, false>), grid, dim3(256), 0, st, p, part,
+                           sl2, pro);
     return hipGetLastError();
 }
 

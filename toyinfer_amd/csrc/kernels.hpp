@@ -81,7 +81,7 @@ struct DecodePrologue {
     const uint16_t* k_raw;  // the token's raw k projection [Hkv][D]
     const uint16_t* k_w;    // k RMSNorm weight [D]
     const uint16_t* v_raw;  // [Hkv][D]
-    const float2* rope;     // rotary table [positions][D/2] (cos, sin)
+    const float2* rope;     // the token position's rotary row [D/2] (cos, sin)
     uint16_t* k_cache;      // p.k and p.v, writable
     uint16_t* v_cache;
     float eps;
@@ -269,10 +269,12 @@ hipError_t launch_argmax(const float* logits, uint32_t n, uint32_t* out, uint32_
                          uint32_t out_cap, hipStream_t stream);
 // *p = value, as a one-lane kernel (stream-ordered, capturable).
 hipError_t launch_set_u32(uint32_t* p, uint32_t value, hipStream_t stream);
-// hidden = table[ids[p]], seq_len_d[0] = p + 1, p = min(*pos_d, cap - 1).
+// hidden = table[ids[p]], seq_len_d[0] = p + 1, p = min(*pos_d, cap - 1);
+// with rope_row: rope_row[0..rope_floats) = rope_table row p.
 hipError_t launch_decode_step_setup(const uint16_t* table, const uint32_t* ids,
                                     const uint32_t* pos_d, uint16_t* hidden, uint32_t* seq_len_d,
                                     uint32_t size, uint32_t vocab, uint32_t cap,
-                                    hipStream_t stream);
+                                    hipStream_t stream, const float* rope_table = nullptr,
+                                    float* rope_row = nullptr, uint32_t rope_floats = 0);
 
 }  // namespace tiattn

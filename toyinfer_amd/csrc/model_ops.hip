@@ -202,16 +202,25 @@ __global__ __launch_bounds__(kArgmaxThreads) void argmax_kernel(const float* __r
 }
 
 // The decode step's first kernel: hidden = table[ids[*pos_d]] (the token
-// at the current position) and seq_len_d[0] = min(*pos_d, cap - 1) + 1.
+// at the current position), seq_len_d[0] = min(*pos_d, cap - 1) + 1 and,
+// when rope_row is given, rope_row = row pos of the rotary table
+// (rope_floats floats), so that later kernels of the step read the
+// position's angles without waiting for the position first.
 template <int VEC>
 __global__ void decode_step_setup_kernel(const uint16_t* __restrict__ table,
                                          const uint32_t* __restrict__ ids,
                                          const uint32_t* __restrict__ pos_d,
                                          uint16_t* __restrict__ hidden, uint32_t* seq_len_d,
-                                         uint32_t size, uint32_t vocab, uint32_t cap) {
+                                         uint32_t size, uint32_t vocab, uint32_t cap,
+                                         const float* __restrict__ rope_table,
+                                         float* __restrict__ rope_row, uint32_t rope_floats) {
     const uint32_t pos = min(*pos_d, cap - 1);
     const uint32_t c = (blockIdx.x * blockDim.x + threadIdx.x) * VEC;
     if (blockIdx.x == 0 && threadIdx.x == 0) seq_len_d[0] = pos + 1;
+    if (blockIdx.x == 0 && rope_row) {
+        for (uint32_t i = threadIdx.x; i < rope_floats; i += blockDim.x)
+            rope_row[i] = rope_table[(size_t)pos * rope_floats + i];
+    }
     if (c >= size) return;
     const uint32_t id = ids[pos];
     const uint16_t* row = table + (size_t)min(id, vocab - 1) * size;
@@ -285,14 +294,17 @@ hipError_t launch_argmax(const float* logits, uint32_t n, uint32_t* out, uint32_
 hipError_t launch_decode_step_setup(const uint16_t* table, const uint32_t* ids,
                                     const uint32_t* pos_d, uint16_t* hidden, uint32_t* seq_len_d,
                                     uint32_t size, uint32_t vocab, uint32_t cap,
-                                    hipStream_t stream) {
+                                    hipStream_t stream, const float* rope_table, float* rope_row,
+                                    uint32_t rope_floats) {
     constexpr int kT = 128;
     if (vec8_ok(size, {table, hidden}))
         decode_step_setup_kernel<8><<<(size / 8 + kT - 1) / kT, kT, 0, stream>>>(
-            table, ids, pos_d, hidden, seq_len_d, size, vocab, cap);
+            table, ids, pos_d, hidden, seq_len_d, size, vocab, cap, rope_table, rope_row,
+            rope_floats);
     else
         decode_step_setup_kernel<2><<<(size / 2 + kT - 1) / kT, kT, 0, stream>>>(
-            table, ids, pos_d, hidden, seq_len_d, size, vocab, cap);
+            table, ids, pos_d, hidden, seq_len_d, size, vocab, cap, rope_table, rope_row,
+            rope_floats);
     return hipGetLastError();
 }
 

@@ -46,6 +46,7 @@ struct toyinfer_qwen3 {
     SampleArgs sample;          // the pick after the lm-head (greedy by default)
     float* inv_freq = nullptr;
     float* rope = nullptr;
+    float* rope_cur = nullptr;  // the decode position's row of `rope`, [D/2] (cos, sin)
     float* logits = nullptr;
     uint16_t* k_cache = nullptr;
     uint16_t* v_cache = nullptr;
@@ -90,6 +91,7 @@ size_t carve(const toyinfer_qwen3_config& c, uint32_t splits, toyinfer_qwen3* m)
     const size_t o_pos = take(4), o_len = take(4), o_sws = take(sample_workspace_bytes());
     const size_t o_inv = take(4ull * c.head_dim / 2);
     const size_t o_rope = take(4ull * c.max_seq_len * c.head_dim);
+    const size_t o_rope_cur = take(4ull * c.head_dim);
     const size_t o_logits = take(4ull * c.vocab_size);
     const size_t o_kc = take(2ull * c.num_layers * c.max_seq_len * kv);
     const size_t o_vc = take(2ull * c.num_layers * c.max_seq_len * kv);
@@ -108,6 +110,7 @@ size_t carve(const toyinfer_qwen3_config& c, uint32_t splits, toyinfer_qwen3* m)
         m->sample_ws = b + o_sws;
         m->inv_freq = reinterpret_cast<float*>(b + o_inv);
         m->rope = reinterpret_cast<float*>(b + o_rope);
+        m->rope_cur = reinterpret_cast<float*>(b + o_rope_cur);
         m->logits = reinterpret_cast<float*>(b + o_logits);
         m->k_cache = reinterpret_cast<uint16_t*>(b + o_kc);
         m->v_cache = reinterpret_cast<uint16_t*>(b + o_vc);
@@ -173,7 +176,7 @@ int decode_body(toyinfer_qwen3* m) {
     void* s0 = st;
     auto u16 = [](const void* p) { return static_cast<const uint16_t*>(p); };
     TRYH(launch_decode_step_setup(u16(m->embed), m->tokens, m->pos, m->d_hidden, m->seq_len, H, V,
-                                  msl, st));
+                                  msl, st, m->rope, m->rope_cur, d));
     for (uint32_t l = 0; l < c.num_layers; ++l) {
         const toyinfer_qwen3_layer& L = m->layers[l];
         uint16_t* kc = m->k_cache + (size_t)l * msl * kv;
@@ -212,7 +215,7 @@ int decode_body(toyinfer_qwen3* m) {
         pro.k_raw = m->d_k;
         pro.k_w = u16(L.k_norm);
         pro.v_raw = m->d_v;
-        pro.rope = reinterpret_cast<const float2*>(m->rope);
+        pro.rope = reinterpret_cast<const float2*>(m->rope_cur);
         pro.k_cache = kc;
         pro.v_cache = vc;
         pro.eps = eps;

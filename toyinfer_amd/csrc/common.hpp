@@ -127,6 +127,28 @@ __device__ __forceinline__ float sum_bf16x8(uint4 v, float acc) {
     return acc;
 }
 
+// Slot i (< 3) of a three-slot kernel-argument array, by selects: an indexed
+// access with a run-time i becomes a vector load from the argument block,
+// whose wait then holds back every load that depends on the result.
+template <typename T>
+__device__ __forceinline__ T pick3(const T (&v)[3], int i) {
+    return i == 0 ? v[0] : (i == 1 ? v[1] : v[2]);
+}
+
+// Segment of unit u among up to three stacked segments of span[s] units
+// each; u is made relative to its segment.
+__device__ __forceinline__ int segment_of(const uint32_t (&span)[3], int nseg, uint32_t& u) {
+    int seg = 0;
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+        if (seg == s && s + 1 < nseg && u >= span[s]) {
+            u -= span[s];
+            seg = s + 1;
+        }
+    }
+    return seg;
+}
+
 __device__ __forceinline__ uint32_t word_of(const uint4& v, int i) {
     return i == 0 ? v.x : (i == 1 ? v.y : (i == 2 ? v.z : v.w));
 }

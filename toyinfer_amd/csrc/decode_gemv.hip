@@ -54,18 +54,19 @@ __global__ __launch_bounds__(kDgThreads) void decode_gemv_kernel(DecodeGemvArgs 
     // Which segment and rows this workgroup owns.
     // (each segment spans whole groups of RB rows).
     uint32_t r0 = blockIdx.x * RB;
-    int seg = 0;
-    while (seg + 1 < a.nseg && r0 >= (a.rows[seg] + RB - 1) / RB * RB) {
-        r0 -= (a.rows[seg] + RB - 1) / RB * RB;
-        ++seg;
-    }
-    const uint32_t nrows = min((uint32_t)RB, a.rows[seg] - r0);
+    const uint32_t spans[3] = {(a.rows[0] + RB - 1) / RB * RB, (a.rows[1] + RB - 1) / RB * RB,
+                               (a.rows[2] + RB - 1) / RB * RB};
+    const int seg = segment_of(spans, a.nseg, r0);
+    const uint32_t seg_rows = pick3(a.rows, seg);
+    const uint16_t* const seg_w = pick3(a.w, seg);
+    uint16_t* const seg_y = pick3(a.y, seg);
+    const uint32_t nrows = min((uint32_t)RB, seg_rows - r0);
     const uint32_t row_bytes = 2 * N;
 
     // The weight rows do not depend on the input: the first trip's chunks
     // are requested before the input is staged (and normalised).
     __amdgpu_buffer_rsrc_t rw[EPI == kDgSwiglu ? 2 : 1];
-    rw[0] = make_rsrc(a.w[seg] + (size_t)r0 * N, nrows * row_bytes);
+    rw[0] = make_rsrc(seg_w + (size_t)r0 * N, nrows * row_bytes);
     if constexpr (EPI == kDgSwiglu) rw[1] = make_rsrc(a.w[1] + (size_t)r0 * N, nrows * row_bytes);
     uint4 wv[2][NR];
     auto load_trip = [&](uint32_t off0, uint32_t off1) __attribute__((always_inline)) {
@@ -175,9 +176,9 @@ __global__ __launch_bounds__(kDgThreads) void decode_gemv_kernel(DecodeGemvArgs 
         for (int w = 0; w < kDgThreads / 64; ++w) v += s_acc[w][r];
         const uint32_t m = r0 + r;
         if constexpr (EPI == kDgPlain) {
-            a.y[seg][m] = f32_to_bf16(v);
+            seg_y[m] = f32_to_bf16(v);
         } else if constexpr (EPI == kDgResidual) {
-            a.y[seg][m] = f32_to_bf16(bf16_to_f32(a.y[seg][m]) + bf16_round(v));
+            seg_y[m] = f32_to_bf16(bf16_to_f32(seg_y[m]) + bf16_round(v));
         } else {
             float u = 0.0f;
 #pragma unroll
@@ -206,19 +207,21 @@ template <int RPW, int NCH, bool NORM, int EPI>
 __global__ __launch_bounds__(64 * kDwWaves) void decode_gemv_wave_kernel(DecodeGemvArgs a) {
     constexpr int NR = EPI == kDgSwiglu ? 2 * RPW : RPW;
     const int lane = threadIdx.x & 63;
-    const uint32_t wave = blockIdx.x * kDwWaves + (threadIdx.x >> 6);
+    const uint32_t wave =
+        __builtin_amdgcn_readfirstlane(blockIdx.x * kDwWaves + (threadIdx.x >> 6));
     const uint32_t N = a.n;
     uint32_t r0 = wave * RPW;
-    int seg = 0;
-    while (seg + 1 < a.nseg && r0 >= (a.rows[seg] + RPW - 1) / RPW * RPW) {
-        r0 -= (a.rows[seg] + RPW - 1) / RPW * RPW;
-        ++seg;
-    }
-    if (r0 >= a.rows[seg]) return;  // a grid's last waves may have no rows
-    const uint32_t nrows = min((uint32_t)RPW, a.rows[seg] - r0);
+    const uint32_t spans[3] = {(a.rows[0] + RPW - 1) / RPW * RPW, (a.rows[1] + RPW - 1) / RPW * RPW,
+                               (a.rows[2] + RPW - 1) / RPW * RPW};
+    const int seg = segment_of(spans, a.nseg, r0);
+    const uint32_t seg_rows = pick3(a.rows, seg);
+    const uint16_t* const seg_w = pick3(a.w, seg);
+    uint16_t* const seg_y = pick3(a.y, seg);
+    if (r0 >= seg_rows) return;  // a grid's last waves may have no rows
+    const uint32_t nrows = min((uint32_t)RPW, seg_rows - r0);
     const uint32_t row_bytes = 2 * N;
     __amdgpu_buffer_rsrc_t rw[EPI == kDgSwiglu ? 2 : 1];
-    rw[0] = make_rsrc(a.w[seg] + (size_t)r0 * N, nrows * row_bytes);
+    rw[0] = make_rsrc(seg_w + (size_t)r0 * N, nrows * row_bytes);
     if constexpr (EPI == kDgSwiglu) rw[1] = make_rsrc(a.w[1] + (size_t)r0 * N, nrows * row_bytes);
     const __amdgpu_buffer_rsrc_t rx = make_rsrc(a.x, row_bytes);
     uint4 wv[NR][NCH], xv[NCH], gv[NCH];
@@ -235,7 +238,7 @@ __global__ __launch_bounds__(64 * kDwWaves) void decode_gemv_wave_kernel(DecodeG
         if constexpr (NORM) gv[k] = buf_load16(make_rsrc(a.norm_w, row_bytes), off);
     }
     uint16_t res = 0;
-    if (EPI == kDgResidual && (uint32_t)lane < nrows) res = a.y[seg][r0 + lane];
+    if (EPI == kDgResidual && (uint32_t)lane < nrows) res = seg_y[r0 + lane];
 
     if constexpr (NORM) {
         float ss = 0.0f;
@@ -277,9 +280,9 @@ __global__ __launch_bounds__(64 * kDwWaves) void decode_gemv_wave_kernel(DecodeG
     if ((uint32_t)lane < nrows) {
         const uint32_t m = r0 + lane;
         if constexpr (EPI == kDgPlain) {
-            a.y[seg][m] = f32_to_bf16(v);
+            seg_y[m] = f32_to_bf16(v);
         } else if constexpr (EPI == kDgResidual) {
-            a.y[seg][m] = f32_to_bf16(bf16_to_f32(res) + bf16_round(v));
+            seg_y[m] = f32_to_bf16(bf16_to_f32(res) + bf16_round(v));
         } else {
             const float g = bf16_round(v), up = bf16_round(u);
             a.y[0][m] = f32_to_bf16(up * (g * (1.0f / (1.0f + expf(-g)))));

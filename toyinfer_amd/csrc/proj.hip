@@ -253,20 +253,19 @@ __global__ __launch_bounds__(C::THREADS, C::MINB) void gemm_kernel(GemmArgs g) {
     uint32_t tm = tile.tm;
     int seg = 0;
     if (!SW) {
-        while (seg + 1 < g.nseg && tm >= (g.rows[seg] + C::BN - 1) / C::BN) {
-            tm -= (g.rows[seg] + C::BN - 1) / C::BN;
-            ++seg;
-        }
+        const uint32_t spans[3] = {(g.rows[0] + C::BN - 1) / C::BN, (g.rows[1] + C::BN - 1) / C::BN,
+                                   (g.rows[2] + C::BN - 1) / C::BN};
+        seg = segment_of(spans, g.nseg, tm);
     }
     constexpr uint32_t TILE_N = SW ? C::BN / 2 : C::BN;  // output columns per tile
-    const uint32_t M = g.rows[seg];
-    uint16_t* __restrict__ y = g.y[seg];
+    const uint32_t M = pick3(g.rows, seg);
+    uint16_t* __restrict__ y = pick3(g.y, seg);
     const uint32_t t0 = tile.tt * C::BM, m0 = tm * TILE_N;
     const uint32_t row_bytes = 2 * N;
     const auto ra = make_rsrc(x + (size_t)t0 * N, min((uint32_t)C::BM, T - t0) * row_bytes);
     const uint32_t b_rows = min(TILE_N, M - m0);
-    const auto rb = make_rsrc(g.w[seg] + (size_t)m0 * N, b_rows * row_bytes);
-    const auto rb_up = make_rsrc(g.w[SW ? 1 : seg] + (size_t)m0 * N, b_rows * row_bytes);
+    const auto rb = make_rsrc(pick3(g.w, seg) + (size_t)m0 * N, b_rows * row_bytes);
+    const auto rb_up = make_rsrc(pick3(g.w, SW ? 1 : seg) + (size_t)m0 * N, b_rows * row_bytes);
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int wr = wave / C::WGN, wc = wave % C::WGN;
 

@@ -693,6 +693,8 @@ __global__ __launch_bounds__(kSliceDims * kSliceGroups) void decode_combine_slic
             l[u] = ml[2 * sp + 1];
             v[u] = po[(int64_t)sp * part.o_split];
         }
+        // Every load above in flight before the first use.
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int u = 0; u < U; ++u)
             merge_partial(M, den, &acc, 1, s0 + u * kSliceGroups < splits ? m[u] : -INFINITY, l[u],

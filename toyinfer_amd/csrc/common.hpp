@@ -101,6 +101,12 @@ __device__ __forceinline__ uint4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t v
     return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, 0, 0));
 }
 
+// Same with the non-temporal hint (cache-policy bit nt), for data a launch
+// streams exactly once (weights of a one-token projection).
+__device__ __forceinline__ uint4 buf_load16_nt(__amdgpu_buffer_rsrc_t r, uint32_t voff) {
+    return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, 0, 2));
+}
+
 // up * silu(gate) on bf16 values (as floats), silu(g) = g / (1 + exp(-g)),
 // written as the reference's SwiGLU kernel computes it.
 __device__ __forceinline__ float swiglu1(float g, float u) {

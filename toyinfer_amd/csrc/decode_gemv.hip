@@ -233,7 +233,7 @@ __global__ __launch_bounds__(64 * kDwWaves) void decode_gemv_wave_kernel(DecodeG
         const bool in = off < row_bytes;
 #pragma unroll
         for (int r = 0; r < NR; ++r)
-            wv[r][k] = buf_load16(rw[r / RPW], in ? (r % RPW) * row_bytes + off : 0x80000000u);
+            wv[r][k] = buf_load16_nt(rw[r / RPW], in ? (r % RPW) * row_bytes + off : 0x80000000u);
         xv[k] = buf_load16(rx, off);
         if constexpr (NORM) gv[k] = buf_load16(make_rsrc(a.norm_w, row_bytes), off);
     }

@@ -37,16 +37,20 @@ struct GvChunk {
     uint32_t w[WORDS];
 };
 
-template <int E>
+// POL: the loads' cache-policy bits (kGvStream for the weight rows, which
+// one call reads exactly once).
+constexpr int kGvStream = 2;  // nt
+
+template <int E, int POL = 0>
 __device__ __forceinline__ GvChunk<E> gv_load(__amdgpu_buffer_rsrc_t r, uint32_t off) {
     GvChunk<E> c;
     if constexpr (E == 8) {
-        const uint4 v = buf_load16(r, off);
+        const uint4 v = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, POL));
         c.w[0] = v.x; c.w[1] = v.y; c.w[2] = v.z; c.w[3] = v.w;
     } else if constexpr (E == 2) {
-        c.w[0] = __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
+        c.w[0] = __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, POL);
     } else {
-        c.w[0] = __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0);
+        c.w[0] = __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, POL);
     }
     return c;
 }
@@ -96,7 +100,7 @@ __global__ __launch_bounds__(kGvThreads) void gemv_kernel(const uint16_t* __rest
 #pragma unroll
             for (int t = 0; t < TB; ++t) xv[u][t] = gv_load<E>(rx, t * row_bytes + off[u]);
 #pragma unroll
-            for (int r = 0; r < RB; ++r) wv[u][r] = gv_load<E>(rw, r * row_bytes + off[u]);
+            for (int r = 0; r < RB; ++r) wv[u][r] = gv_load<E, kGvStream>(rw, r * row_bytes + off[u]);
         }
 #pragma unroll
         for (int u = 0; u < 2; ++u)

@@ -200,7 +200,9 @@ __global__ __launch_bounds__(kDgThreads) void decode_gemv_kernel(DecodeGemvArgs 
 // (4-12 MB of weights): 3.4-4.9 us per projection, against 4-6 us for the
 // block-cooperative kernel below; 16-wave workgroups on 32-48 CUs stream the
 // same matrices from HBM at under half the rate (8.5 us for 4 MB).  The
-// residual row is read at the start, with the weights.
+// residual row is read at the start, with the weights; the weight rows carry
+// the non-temporal hint (read once per step: 0.729 -> 0.666 ms per
+// Qwen3-0.6B decode step together with the lm-head's).
 constexpr int kDwWaves = 4;
 
 template <int RPW, int NCH, bool NORM, int EPI>

@@ -354,7 +354,8 @@ hipError_t dg_rows(const DecodeGemvArgs& a, hipStream_t stream) {
 // the last workgroup to arrive (ticket) writes the index, advances the
 // position as the one-workgroup argmax does, and rearms key and ticket for
 // the next launch.
-constexpr int kAmBlocks = 256, kAmThreads = 256;
+constexpr int kAmBlocks = 64, kAmThreads = 512;
+constexpr int kAmUnroll = 8;  // loads per lane in flight (one round for V <= 262144)
 
 __device__ __forceinline__ uint64_t am_key(float v, uint32_t i) {
     // Values not above -FLT_MAX (and NaN) never win: key 0.
@@ -371,9 +372,20 @@ __global__ __launch_bounds__(kAmThreads) void argmax_wide_kernel(const float* __
     __shared__ uint64_t s_k[kAmThreads / 64];
     __shared__ bool s_last;
     uint64_t best = 0;
-    for (uint32_t i = blockIdx.x * kAmThreads + threadIdx.x; i < n; i += kAmBlocks * kAmThreads) {
-        const uint64_t k = am_key(logits[i], i);
-        best = k > best ? k : best;
+    constexpr uint32_t kStride = kAmBlocks * kAmThreads;
+    for (uint32_t i0 = blockIdx.x * kAmThreads + threadIdx.x; i0 < n; i0 += kAmUnroll * kStride) {
+        float v[kAmUnroll];
+#pragma unroll
+        for (int u = 0; u < kAmUnroll; ++u) {
+            const uint32_t i = i0 + u * kStride;
+            v[u] = i < n ? logits[i] : -INFINITY;
+        }
+#pragma unroll
+        for (int u = 0; u < kAmUnroll; ++u) {
+            const uint32_t i = i0 + u * kStride;
+            const uint64_t k = i < n ? am_key(v[u], i) : 0;
+            best = k > best ? k : best;
+        }
     }
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) {

@@ -8,7 +8,9 @@ per-head QK-RMSNorm (eps 1e-6, gamma ~ U(0.9, 1.1)) and RoPE (theta 1e6,
 positions 0..8191) fused in front; bf16 ~ N(0,1) seeded; metric TFLOP/s with
 the causal FLOP count 4*S^2*Hq*D/2 (attention only; the K pre-pass time is
 inside the step).  A step is one toyinfer_prefill_qknorm_rope_attention_bf16
-call over that input; W untimed steps, then exactly K timed steps between two
+call over that input.  The step first runs untimed for --settle seconds (the
+GPU's power controller cuts the clock for ~10-15 ms after an idle-to-MFMA
+load step), then W untimed steps, then exactly K timed steps between two
 device synchronisations, timed with HIP events recorded on the stream the
 kernels run on.
 
@@ -50,6 +52,9 @@ METRIC = "prefill attn TFLOP/s + decode attn HBM GB/s (% MI355X roofline), Qwen3
 PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
 PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
 SEED = 2026
+# Untimed run of the headline step before its warm-up steps, in seconds (see
+# settle()): long enough for the power controller's transient to pass.
+SETTLE_S = 0.3
 # HBM bytes per launch of each workload's dominant kernel: rocprofv3 --pmc
 # FETCH_SIZE and WRITE_SIZE passes (KiB per dispatch) over
 # `bench.py --workload <name>`, scaled by what the same counters read for a
@@ -79,13 +84,14 @@ def causal_flops(s, hq, d):
 def parse():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
-    # The headline step is ~0.6 ms; the defaults give the MFMA clock ~12 ms of
-    # sustained launches to settle before the timed region.
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-components", action="store_true",
                     help="only the headline workload")
     ap.add_argument("--no-cpu", action="store_true", help="skip the cpu_baseline leg")
+    ap.add_argument("--settle", type=float, default=SETTLE_S,
+                    help="seconds the headline step runs untimed before its warm-up steps "
+                         "(0: none)")
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="target CPU time of the cpu_baseline sample")
     ap.add_argument("--workload", default="all", choices=WORKLOADS,
@@ -106,6 +112,27 @@ def to_host(t):
     import torch
 
     return t.detach().cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
+
+
+def settle(fn, stream, seconds):
+    """Run `fn(i)` untimed for `seconds` of wall time, in bursts of 16 launches
+    each followed by a device synchronisation; returns the launch count.
+
+    After an idle-to-MFMA load step the GPU's power controller cuts the clock
+    for about 10-15 ms (per-launch kernel traces of the headline show the
+    prefill kernel at a constant ~7.5 M GRBM_GUI_ACTIVE cycles while its
+    duration climbs from 520 to 670 us and back), so MFMA-bound steps timed
+    straight after a short warm-up measure that transient, not the kernel."""
+    import torch
+
+    n, t0 = 0, time.perf_counter()
+    with torch.cuda.stream(stream):
+        while time.perf_counter() - t0 < seconds:
+            for _ in range(16):
+                fn(n)
+                n += 1
+            torch.cuda.synchronize()
+    return n
 
 
 def time_steps(fn, steps, warmup, stream):
@@ -183,9 +210,11 @@ def fused_inputs(dev, s, hq, hkv, d, theta):
     return host + (gqb, gkb), (q, k, v, to_dev(gqb, dev), to_dev(gkb, dev), table)
 
 
-def bench_prefill_fused(dev, stream, steps, warmup):
+def bench_prefill_fused(dev, stream, steps, warmup, settle_s=SETTLE_S):
     """the headline step (K norm+RoPE pre-pass, then attention
-    with Q normalised and rotated on load)."""
+    with Q normalised and rotated on load).  The step first runs untimed for
+    `settle_s` seconds (see settle()), then `warmup` untimed and `steps` timed
+    steps.  Returns (ms, TFLOP/s, settle launches, host inputs, output bits)."""
     import torch
 
     from toyinfer_amd import attn
@@ -194,11 +223,15 @@ def bench_prefill_fused(dev, stream, steps, warmup):
     host, (q, k, v, gq, gk, table) = fused_inputs(dev, s, hq, hkv, d, FUSED["theta"])
     o = torch.empty((s, hq, d), dtype=torch.bfloat16, device=dev)
     k_out = torch.empty_like(k)
-    ms = time_steps(lambda i: attn.prefill_qknorm_rope_attention_bf16(
-        q, k, v, o, k_out, gq, gk, table, FUSED["eps"], hq, hkv, d, s, stream), steps, warmup,
-        stream)
+
+    def step(i):
+        attn.prefill_qknorm_rope_attention_bf16(q, k, v, o, k_out, gq, gk, table, FUSED["eps"],
+                                                hq, hkv, d, s, stream)
+
+    n_settle = settle(step, stream, settle_s) if settle_s > 0 else 0
+    ms = time_steps(step, steps, warmup, stream)
     tflops = causal_flops(s, hq, d) / (ms * 1e-3) / 1e12
-    return ms, tflops, host, to_host(o)
+    return ms, tflops, n_settle, host, to_host(o)
 
 
 # ------------------------------------------------------------------- decode
@@ -617,16 +650,19 @@ def main():
     }
     if args.workload != "all":
         if args.workload == "prefill_fused":
-            ms, tf, _, _ = bench_prefill_fused(dev, stream, args.steps, args.warmup)
+            ms, tf, n_settle, _, _ = bench_prefill_fused(dev, stream, args.steps, args.warmup,
+                                                         args.settle)
             out = {"workload": "prefill_fused_qknorm_rope_s8192_hq32_hkv8_d128",
-                   "ms_per_step": round(ms, 5), "value": round(tf, 2), "unit": "TFLOP/s"}
+                   "ms_per_step": round(ms, 5), "value": round(tf, 2), "unit": "TFLOP/s",
+                   "settle_launches": n_settle}
         else:
             out = comp[args.workload]()
         print(json.dumps(out), flush=True)
         return
 
     s, hq, hkv, d = FUSED["s"], FUSED["hq"], FUSED["hkv"], FUSED["d"]
-    ms, tflops, host, gpu_out = bench_prefill_fused(dev, stream, args.steps, args.warmup)
+    ms, tflops, n_settle, host, gpu_out = bench_prefill_fused(dev, stream, args.steps,
+                                                              args.warmup, args.settle)
     line = {
         "metric": METRIC, "value": round(tflops, 2), "unit": "TFLOP/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 5),
@@ -638,7 +674,11 @@ def main():
                    "qk_norm_eps": FUSED["eps"], "rope_theta": FUSED["theta"],
                    "flops_per_step": causal_flops(s, hq, d), "accumulate": "fp32",
                    "entry": "toyinfer_prefill_qknorm_rope_attention_bf16",
-                   "note": "step = K norm+RoPE pre-pass + attention; FLOPs count attention only",
+                   "note": "step = K norm+RoPE pre-pass + attention; FLOPs count attention only; "
+                           f"before the {args.warmup} warm-up and {args.steps} timed steps the "
+                           f"same step ran untimed for {args.settle:g} s ({n_settle} launches, "
+                           "the GPU's power-controller transient after an idle-to-MFMA load "
+                           "step); nothing else ran before it",
                    "parallelism": "single GPU"},
         "roofline": roofline("mfma", tflops, PEAK_BF16_TFLOPS, "TFLOP/s",
                              traffic_bytes("prefill_fused")),

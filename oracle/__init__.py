@@ -413,9 +413,12 @@ class Qwen3Reference:
     logits fp32.  Weights are float32 arrays holding bf16 values (dict as in
     toyinfer_amd.qwen3, plus "inv_freq").  Caches [layers][max_seq_len][Hkv][D]."""
 
-    def __init__(self, cfg: dict, weights: dict):
+    def __init__(self, cfg: dict, weights: dict, nthreads: int = 0):
         self.cfg = cfg
         self.w = weights
+        # OpenMP threads of the projections and the prefill attention (0: this
+        # process's CPUs, at most 16); the results do not depend on it.
+        self.nt = nthreads if nthreads > 0 else max(1, min(16, len(os.sched_getaffinity(0))))
         L, msl = cfg["num_layers"], cfg["max_seq_len"]
         shape = (L, msl, cfg["num_kv_heads"], cfg["head_dim"])
         self.kc = np.zeros(shape, np.float32)
@@ -426,9 +429,9 @@ class Qwen3Reference:
         T = x.shape[0]
         hq, hkv, d, eps = c["num_q_heads"], c["num_kv_heads"], c["head_dim"], c["rms_norm_eps"]
         xn = rmsnorm_rows(x, W["input_layernorm"], eps)
-        q = round_bf16(gemv(W["q_proj"], xn))
-        k = round_bf16(gemv(W["k_proj"], xn))
-        v = round_bf16(gemv(W["v_proj"], xn))
+        q = round_bf16(gemv(W["q_proj"], xn, self.nt))
+        k = round_bf16(gemv(W["k_proj"], xn, self.nt))
+        v = round_bf16(gemv(W["v_proj"], xn, self.nt))
         q = rope(multi_rmsnorm(q, W["q_norm"], d, eps), self.w["inv_freq"], T, hq, d, pos0)
         k = rope(multi_rmsnorm(k, W["k_norm"], d, eps), self.w["inv_freq"], T, hkv, d, pos0)
         self.kc[l, pos0:pos0 + T] = k.reshape(T, hkv, d)
@@ -436,22 +439,22 @@ class Qwen3Reference:
         if T > 1:
             assert pos0 == 0
             o = round_bf16(flash_reference(q.reshape(T, hq, d), k.reshape(T, hkv, d),
-                                           v.reshape(T, hkv, d), nthreads=8))
+                                           v.reshape(T, hkv, d), nthreads=self.nt))
         else:
             _, _, ob = decode_attention(q.reshape(hq, d), self.kc[l], self.vc[l], pos0,
                                         c["max_seq_len"])
             o = bf16_to_f32(ob)
-        a = round_bf16(gemv(W["o_proj"], o.reshape(T, hq * d)))
+        a = round_bf16(gemv(W["o_proj"], o.reshape(T, hq * d), self.nt))
         x = residual_add(x, a)
         xn = rmsnorm_rows(x, W["post_attention_layernorm"], eps)
-        g = round_bf16(gemv(W["gate_proj"], xn))
-        u = round_bf16(gemv(W["up_proj"], xn))
-        dn = round_bf16(gemv(W["down_proj"], swiglu(g, u)))
+        g = round_bf16(gemv(W["gate_proj"], xn, self.nt))
+        u = round_bf16(gemv(W["up_proj"], xn, self.nt))
+        dn = round_bf16(gemv(W["down_proj"], swiglu(g, u), self.nt))
         return residual_add(x, dn)
 
     def _logits(self, x_last):
         xn = rmsnorm_rows(x_last[None, :], self.w["norm"], self.cfg["rms_norm_eps"])
-        return gemv(self.w["lm_head"], xn)[0]
+        return gemv(self.w["lm_head"], xn, self.nt)[0]
 
     def forward(self, token_ids, pos0):
         """Tokens at positions pos0.. (a prompt from 0, or one decode token)

@@ -519,19 +519,78 @@ void or_make_batch_gemv_case(uint32_t batch, uint32_t M, uint32_t N, float hidde
 /* tests/gemv_test_common.h:52-65 and tests/test_batch_gemv_proj_bf16.cu:52-66:
  * y[t][r] = sum over c in order of w[r][c] * x[t][c], float accumulation
  * (the caller rounds to bf16 where the projection outputs bf16).  Tokens are
- * independent; `nthreads` > 0 spreads them and the rows over OpenMP threads. */
+ * independent; `nthreads` > 0 spreads them and the rows over OpenMP threads.
+ *
+ * With 16 or more tokens the same sums run 16 tokens wide: each vector lane
+ * holds one token's running sum and performs exactly the scalar sequence
+ * (sum = 0; sum = sum + rounded(w * x) for c in order; -ffp-contract=off
+ * keeps the product and the sum separately rounded), so the results are
+ * bit-identical to the scalar loop; tests/test_oracle.py checks that. */
+typedef float or_v8f __attribute__((vector_size(32)));
+
+enum { OR_GT = 64, OR_GR = 64 }; /* token and row tile of one task */
+
+static void gemv_tile(const float* w, const float* xt, float* y, uint32_t t0, uint32_t nt,
+                      uint32_t r0, uint32_t nr, uint32_t M, uint32_t N) {
+    /* xt: the tile's tokens transposed, [N][OR_GT], zero past nt. */
+    for (uint32_t rb = 0; rb < nr; rb += 4) {
+        const float* wr[4];
+        for (int i = 0; i < 4; ++i) wr[i] = w + (size_t)(r0 + (rb + i < nr ? rb + i : nr - 1)) * N;
+        for (uint32_t tb = 0; tb < nt; tb += 16) {
+            or_v8f acc[4][2];
+            for (int i = 0; i < 4; ++i) acc[i][0] = acc[i][1] = (or_v8f){0, 0, 0, 0, 0, 0, 0, 0};
+            const float* xc = xt + tb;
+            for (uint32_t c = 0; c < N; ++c, xc += OR_GT) {
+                or_v8f x0, x1;
+                memcpy(&x0, xc, 32);
+                memcpy(&x1, xc + 8, 32);
+                for (int i = 0; i < 4; ++i) {
+                    const float wv = wr[i][c];
+                    acc[i][0] = acc[i][0] + wv * x0;
+                    acc[i][1] = acc[i][1] + wv * x1;
+                }
+            }
+            for (int i = 0; i < 4 && rb + i < nr; ++i)
+                for (int j = 0; j < 16 && tb + j < nt; ++j)
+                    y[(size_t)(t0 + tb + j) * M + r0 + rb + i] = acc[i][j >> 3][j & 7];
+        }
+    }
+}
+
 void or_gemv(const float* w, const float* x, float* y, uint32_t tokens, uint32_t M, uint32_t N,
              int nthreads) {
-    const int64_t total = (int64_t)tokens * M;
+    if (tokens < 16) {
+        const int64_t total = (int64_t)tokens * M;
 #pragma omp parallel for schedule(static) num_threads(nthreads > 0 ? nthreads : 1) if (nthreads > 1)
-    for (int64_t i = 0; i < total; ++i) {
-        const uint32_t t = (uint32_t)(i / M), r = (uint32_t)(i % M);
-        const float* wr = w + (size_t)r * N;
-        const float* xt = x + (size_t)t * N;
-        float sum = 0.0f;
-        for (uint32_t c = 0; c < N; ++c) sum += wr[c] * xt[c];
-        y[i] = sum;
+        for (int64_t i = 0; i < total; ++i) {
+            const uint32_t t = (uint32_t)(i / M), r = (uint32_t)(i % M);
+            const float* wr = w + (size_t)r * N;
+            const float* xr = x + (size_t)t * N;
+            float sum = 0.0f;
+            for (uint32_t c = 0; c < N; ++c) sum += wr[c] * xr[c];
+            y[i] = sum;
+        }
+        return;
     }
+    const uint32_t ntb = (tokens + OR_GT - 1) / OR_GT, nrb = (M + OR_GR - 1) / OR_GR;
+    float* xt = (float*)malloc((size_t)ntb * N * OR_GT * sizeof(float));
+    if (!xt) abort();
+    for (uint32_t b = 0; b < ntb; ++b)
+        for (uint32_t c = 0; c < N; ++c)
+            for (uint32_t j = 0; j < OR_GT; ++j) {
+                const uint32_t t = b * OR_GT + j;
+                xt[((size_t)b * N + c) * OR_GT + j] = t < tokens ? x[(size_t)t * N + c] : 0.0f;
+            }
+    const int64_t tasks = (int64_t)ntb * nrb;
+#pragma omp parallel for schedule(dynamic) num_threads(nthreads > 0 ? nthreads : 1) if (nthreads > 1)
+    for (int64_t k = 0; k < tasks; ++k) {
+        const uint32_t b = (uint32_t)(k / nrb), rb = (uint32_t)(k % nrb);
+        const uint32_t t0 = b * OR_GT, r0 = rb * OR_GR;
+        const uint32_t nt = tokens - t0 < OR_GT ? tokens - t0 : OR_GT;
+        const uint32_t nr = M - r0 < OR_GR ? M - r0 : OR_GR;
+        gemv_tile(w, xt + (size_t)b * N * OR_GT, y, t0, nt, r0, nr, M, N);
+    }
+    free(xt);
 }
 
 /* ------------------------------------------------- rest of a decoder layer */

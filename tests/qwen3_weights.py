@@ -29,8 +29,7 @@ def bits_to_f32(b: np.ndarray) -> np.ndarray:
 
 def scaled_bits(seed: int, name: str, shape, std: float) -> np.ndarray:
     """bf16 bits of std * N(0, 1) (the N(0, 1) draw rounded to bf16 first)."""
-    x = bits_to_f32(synth.normal_bf16(seed, name, shape)) * np.float32(std)
-    return synth.f32_to_bf16_bits(x)
+    return synth.scale_bf16(synth.normal_bf16(seed, name, shape), std)
 
 
 def weight_bits(cfg: dict, seed: int, proj_std: float, embed_std: float, norm_range,

@@ -273,6 +273,9 @@ def test_generator_c_matches_numpy_specification():
                               synth.normal_bf16(seed, name, (n,), use_c=False))
         assert np.array_equal(synth.uniform_bf16(seed, name, (n,), 0.9, 1.1, use_c=True),
                               synth.uniform_bf16(seed, name, (n,), 0.9, 1.1, use_c=False))
+        b = synth.normal_bf16(seed, name, (n,))
+        assert np.array_equal(synth.scale_bf16(b, 0.02, use_c=True),
+                              synth.scale_bf16(b, 0.02, use_c=False))
 
 
 def test_generator_pinned_values_and_statistics():

@@ -367,6 +367,23 @@ def test_gemv_vs_float64_and_closed_forms():
     assert np.array_equal(oracle.gemv(w, xs, nthreads=4), ys)
 
 
+@pytest.mark.parametrize("T,M,N", [(16, 5, 1), (37, 67, 129), (130, 9, 514), (64, 64, 3072)])
+def test_gemv_token_vector_path_equals_scalar_sums(T, M, N):
+    """16+ tokens run 16 tokens per vector lane-set; each lane must repeat the
+    scalar in-order float sum exactly: compare with one-token calls (the
+    scalar loop) bit for bit, across ragged token and row tails, and with a
+    float64 bound."""
+    rng = np.random.default_rng(T * 1000 + M)
+    w = oracle.round_bf16(rng.standard_normal((M, N)).astype(np.float32))
+    x = oracle.round_bf16(rng.standard_normal((T, N)).astype(np.float32))
+    y = oracle.gemv(w, x, nthreads=3)
+    ys = np.stack([oracle.gemv(w, x[t]) for t in range(T)])
+    assert np.array_equal(y.view(np.uint32), ys.view(np.uint32))
+    ref = x.astype(np.float64) @ w.astype(np.float64).T
+    bound = N * 2.0 ** -23 * (np.abs(x).astype(np.float64) @ np.abs(w).astype(np.float64).T)
+    assert (np.abs(y - ref) <= bound + 1e-30).all()
+
+
 # ------------------------------------------------- rest of a decoder layer
 
 def test_layer_op_case_generators_literal_values():

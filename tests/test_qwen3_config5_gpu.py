@@ -7,8 +7,10 @@ Qwen3-0.6B (28 layers, hidden 1024, 16/8 heads, D=128, SwiGLU 3072, vocab
   float64 forward that matches transformers' Qwen3): each step's logits
   within LOGIT_MAX_ABS / LOGIT_MEAN_ABS, the device pick = argmax of the
   device logits, the oracle fed the tokens the device chose.
-* After a 1371-token prefill (config 5's prompt), 12 decode steps from a
-  captured graph and 12 direct steps give identical tokens and logits.
+* The 1371-token prompt of config 5 and 2 graph decode steps against the
+  same oracle forward.
+* After a 1371-token prefill, 12 decode steps from a captured graph and 12
+  direct steps give identical tokens and logits.
 
 Bars: the oracle and the float64 forward with the same bf16 rounding points
 differ by max 0.041, mean 0.0069 on these logits (std 0.64; fp32 vs fp64
@@ -79,6 +81,36 @@ def test_config5_prefill_and_decode_vs_oracle(dev, weights5, graph):
     assert toks[T] == oracle.argmax(got), "prefill pick"
     for s in range(steps):
         m.decode(1, graph)
+        got = m.logits_host()
+        toks = m.tokens_host(T + s + 2)
+        check_logits(got, ref.forward([toks[T + s]], T + s), f"step {s}")
+        assert toks[T + s + 1] == oracle.argmax(got), f"step {s} pick"
+    assert m.position_host() == T + steps
+    m.close()
+
+
+def test_config5_full_prompt_and_decode_vs_oracle(dev, weights5):
+    """Configuration 5's own prompt length (src/transformer.cpp:327-481 runs
+    the 1371-token prompt): every layer's attention goes through the
+    persistent split-over-keys prefill kernel in more than one round, and the
+    prefill projections through the 128 x 192 / 64 x 64 GEMM tiles; then two
+    graph-replayed decode steps over the 1371-row cache."""
+    print("[step] config-5 1371-token prefill + 2 graph decode steps vs oracle", flush=True)
+    host, dw = weights5
+    T, steps = 1371, 2
+    ids = np.random.default_rng(SEED + 11).integers(0, CFG5["vocab_size"], T).astype(np.uint32)
+    m = qwen3.Qwen3(qwen3.Config(**CFG5), dw)
+    id_t = ids_dev(ids, dev)
+    m.prefill(id_t, T)
+    got = m.logits_host()
+    print("[step] oracle forward of 1371 tokens", flush=True)
+    ref = oracle.Qwen3Reference(dict(CFG5, max_seq_len=T + steps + 1), host)
+    check_logits(got, ref.forward(ids, 0), "prefill 1371")
+    toks = m.tokens_host(T + 1)
+    assert np.array_equal(toks[:T], ids)
+    assert toks[T] == oracle.argmax(got), "prefill pick"
+    for s in range(steps):
+        m.decode(1, True)
         got = m.logits_host()
         toks = m.tokens_host(T + s + 2)
         check_logits(got, ref.forward([toks[T + s]], T + s), f"step {s}")

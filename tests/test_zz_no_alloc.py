@@ -68,3 +68,44 @@ def test_noalloc_rejects_sizes_beyond_the_array(dev):
     with pytest.raises(attn.ToyInferError) as e:
         attn.decode_attention_bf16_noalloc(t, t, t, t, b, hq, hkv, d, None, L, L * hkv * d, 1)
     assert e.value.status == attn.ERR_WORKSPACE
+
+
+def test_noalloc_captured_in_a_graph_replays_bit_identically(dev):
+    """The callers this entry point is for capture it: a torch CUDAGraph holds
+    one call (device lengths, so each replay reads the lengths then current);
+    three replays, with eager work and synchronisations between them, each
+    match the workspace entry point bit for bit.  The array's address is
+    taken on the entry point's first call on the device, which the capture
+    does not contain (the calls of the tests above, or the direct call here)."""
+    print("[no-alloc] graph capture and replays, B=4 L=2048 32/8 D=128", flush=True)
+    b, L, hq, hkv, d = 4, 2048, 32, 8, 128
+    qb, kb, vb = inputs(305, b, L, hq, hkv, d)
+    q, k, v = H.to_dev_bf16(qb, dev), H.to_dev_bf16(kb, dev), H.to_dev_bf16(vb, dev)
+    lens_d = torch.tensor([L, L, L, L], dtype=torch.int32, device=dev)
+    o_na = torch.zeros((b, hq, d), dtype=torch.bfloat16, device=dev)
+    side = torch.cuda.Stream(device=dev)
+    with torch.cuda.stream(side):
+        attn.decode_attention_bf16_noalloc(q, k, v, o_na, b, hq, hkv, d, lens_d, L, L * hkv * d,
+                                           0, side)
+    H.sync()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=side):
+        attn.decode_attention_bf16_noalloc(q, k, v, o_na, b, hq, hkv, d, lens_d, L, L * hkv * d,
+                                           0, side)
+    H.sync()
+    splits = attn.decode_default_splits(b, hq, hkv, d, L)
+    ws = attn.decode_workspace(b, hq, d, splits, dev)
+    o_ws = torch.empty_like(o_na)
+    for r, lens in enumerate(([2048, 1, 700, 2048], [5, 2047, 64, 1000], [2048] * 4)):
+        lens_d.copy_(torch.tensor(lens, dtype=torch.int32))
+        o_na.fill_(3.0)
+        H.sync()
+        g.replay()
+        H.sync()
+        attn.decode_attention_bf16(q, k, v, o_ws, b, hq, hkv, d, lens_d, L, L * hkv * d, splits,
+                                   ws)
+        H.sync()
+        got = H.from_dev_bf16(o_na)
+        assert np.array_equal(got, H.from_dev_bf16(o_ws)), f"replay {r} differs"
+        exp = oracle.round_bf16(oracle.decode_batched(qb, kb, vb, lens))
+        H.check_bar(H.bf16_bits_to_f32(got), exp, f"replay {r} vs oracle")

@@ -115,3 +115,16 @@ void ti_synth_uniform_bf16(uint64_t key, int64_t n, double lo, double hi, uint16
         out[i] = f32_to_bf16((float)(lo + span * u));
     }
 }
+
+static inline float bf16_to_f32(uint16_t h) {
+    const uint32_t u = (uint32_t)h << 16;
+    float f;
+    memcpy(&f, &u, 4);
+    return f;
+}
+
+/* bf16(float(in[i]) * scale): one float32 product, rounded to nearest even. */
+void ti_synth_scale_bf16(const uint16_t* in, int64_t n, float scale, uint16_t* out) {
+#pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < n; ++i) out[i] = f32_to_bf16(bf16_to_f32(in[i]) * scale);
+}

@@ -147,6 +147,7 @@ class Qwen3:
     def __init__(self, cfg: Config, weights: Dict):
         self.cfg = cfg
         self._keep = weights
+        self._held = []  # device ids whose copy may still be queued (prefill)
         layers = (Layer * cfg.num_layers)()
         for i, lw in enumerate(weights["layers"]):
             for n in LAYER_FIELDS:
@@ -185,7 +186,11 @@ class Qwen3:
         return attn.LIB.toyinfer_qwen3_state_bytes(ctypes.byref(cfg))
 
     def prefill(self, ids_dev, n: int) -> None:
+        """The ids are copied on the model's stream after this returns, so
+        the tensor is held here until the next synchronize(): a caller's
+        temporary is not handed back to torch's allocator before the copy."""
         attn._check("qwen3_prefill", attn.LIB.toyinfer_qwen3_prefill(self.h, ids_dev.data_ptr(), n))
+        self._held.append(ids_dev)
 
     def decode(self, steps: int, graph: bool) -> None:
         attn._check("qwen3_decode", attn.LIB.toyinfer_qwen3_decode(self.h, steps, int(graph)))
@@ -196,6 +201,7 @@ class Qwen3:
 
     def synchronize(self) -> None:
         attn._check("qwen3_synchronize", attn.LIB.toyinfer_qwen3_synchronize(self.h))
+        self._held.clear()
 
     def logits_host(self) -> np.ndarray:
         self.synchronize()

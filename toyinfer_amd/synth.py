@@ -41,6 +41,9 @@ def _c():
         lib.ti_synth_uniform_bf16.argtypes = [ctypes.c_uint64, ctypes.c_int64, ctypes.c_double,
                                               ctypes.c_double, ctypes.c_void_p]
         lib.ti_synth_uniform_bf16.restype = None
+        lib.ti_synth_scale_bf16.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_float,
+                                            ctypes.c_void_p]
+        lib.ti_synth_scale_bf16.restype = None
         _clib = lib
     return _clib
 
@@ -174,6 +177,17 @@ def normal_bf16(seed: int, name: str, shape, use_c: bool = True) -> np.ndarray:
         return out.reshape(shape)
     z = normal_f64(key, n).astype(np.float32)
     return f32_to_bf16_bits(z).reshape(shape)
+
+
+def scale_bf16(bits: np.ndarray, scale: float, use_c: bool = True) -> np.ndarray:
+    """bf16 bits of float32(bits) * float32(scale), rounded to nearest even."""
+    b = np.ascontiguousarray(bits, dtype=np.uint16)
+    lib = _c() if use_c else None
+    if lib is not None:
+        out = np.empty_like(b)
+        lib.ti_synth_scale_bf16(b.ctypes.data, b.size, float(np.float32(scale)), out.ctypes.data)
+        return out
+    return f32_to_bf16_bits(bf16_bits_to_f32(b) * np.float32(scale))
 
 
 def uniform_bf16(seed: int, name: str, shape, lo: float, hi: float,

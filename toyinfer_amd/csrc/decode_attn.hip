@@ -414,12 +414,14 @@ __device__ __forceinline__ void decode_split_body(const DecodeProblem& p,
 #pragma unroll
         for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
+            for (int r = 0; r < 4; ++r)
                 pr[4 * tt + r] = __builtin_amdgcn_exp2f(fmaf(st[tt][r], scale_log2, -mref));
-                l_run += pr[4 * tt + r];
-            }
-        const bf16x8_t pb = as_bf16x8(make_uint4(pack_bf16x2(pr[0], pr[1]), pack_bf16x2(pr[2], pr[3]),
-                                                 pack_bf16x2(pr[4], pr[5]), pack_bf16x2(pr[6], pr[7])));
+        // P.V multiplies the bf16-rounded probabilities, so the denominator
+        // sums exactly those values: numerator and denominator see the same P.
+        const uint4 pw = make_uint4(pack_bf16x2(pr[0], pr[1]), pack_bf16x2(pr[2], pr[3]),
+                                    pack_bf16x2(pr[4], pr[5]), pack_bf16x2(pr[6], pr[7]));
+        l_run = sum_bf16x8(pw, l_run);
+        const bf16x8_t pb = as_bf16x8(pw);
 #pragma unroll
         for (int db = 0; db < NDB; ++db) {
             const v4i16_t lo = ds_read_tr16(vs + tr_off[0][db]);

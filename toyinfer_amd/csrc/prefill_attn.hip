@@ -73,8 +73,9 @@ struct PfShape {
 //   K rows (A operand reads): chunk c at c ^ (row mod D/8).
 //   V rows (transposing reads, 4 rows x 64 bytes per half-wave at D = 128):
 //   chunk c at c ^ 4*(row & 3) (D = 128), c ^ 2*(row & 3) (D = 64).
-// SQ_LDS_BANK_CONFLICT reads 0 for this kernel with these maps (the earlier
-// c ^ (row & 7) / c ^ 2*(row & 3) gave 6.8e7 conflict cycles per launch).
+// With these maps SQ_LDS_BANK_CONFLICT reads 524288 cycles per launch at
+// S=8192, 32/8 heads (256 per workgroup, about 2 % of the LDS-active
+// cycles; the earlier c ^ (row & 7) / c ^ 2*(row & 3) gave 6.8e7).
 template <int D>
 struct DmaShape {
     static constexpr int CPR = D / 8;

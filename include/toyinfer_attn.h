@@ -50,7 +50,10 @@ int toyinfer_flash_attention_v1_bf16(const void* Qs, const void* Ks, const void*
 /* Same, with the kernel chosen explicitly (extension, for tuning and tests):
  * algo 0 = pick by shape (what toyinfer_flash_attention_v1_bf16 does),
  * 1 = 32-row workgroups whose waves split the keys (short sequences),
- * 2 = 128-row workgroups sharing each K/V tile (long sequences). */
+ * 2 = 128-row workgroups sharing each K/V tile (long sequences),
+ * 3 = as 1 with both query heads of a GQA pair in one workgroup sharing
+ *     each K/V tile (what algo 0 runs for short sequences when Hq/Hkv is
+ *     even; as 1 when it is odd). */
 int toyinfer_flash_attention_algo_bf16(const void* Qs, const void* Ks, const void* Vs, void* Os,
                                        uint32_t num_q_heads, uint32_t num_kv_heads,
                                        uint32_t heads_dim, uint32_t seq_len, int algo,

@@ -16,7 +16,7 @@ from toyinfer_amd import attn, synth
 pytestmark = pytest.mark.gpu
 
 
-ALGOS = [attn.ALGO_SPLIT_KEYS, attn.ALGO_ROW_TILES]
+ALGOS = [attn.ALGO_SPLIT_KEYS, attn.ALGO_ROW_TILES, attn.ALGO_SPLIT_PAIRS]
 
 
 def run_prefill(q_bits, k_bits, v_bits, dev, algo=attn.ALGO_AUTO):
@@ -172,7 +172,9 @@ def test_algos_agree_at_long_s(dev, s, hq, hkv, d):
     qb, kb, vb = seeded(3, s, hq, hkv, d)
     a = H.bf16_bits_to_f32(run_prefill(qb, kb, vb, dev, attn.ALGO_SPLIT_KEYS))
     b = H.bf16_bits_to_f32(run_prefill(qb, kb, vb, dev, attn.ALGO_ROW_TILES))
+    c = H.bf16_bits_to_f32(run_prefill(qb, kb, vb, dev, attn.ALGO_SPLIT_PAIRS))
     H.check_bar(a, b, "split vs rows", max_abs=1.6e-2, mean_abs=3e-4)
+    H.check_bar(c, b, "split pairs vs rows", max_abs=1.6e-2, mean_abs=3e-4)
 
 
 @pytest.mark.parametrize("algo", ALGOS)
@@ -185,10 +187,13 @@ def test_deterministic(dev, algo):
 
 @pytest.mark.parametrize("algo", ALGOS)
 def test_gqa_equals_mha_with_repeated_kv(dev, algo):
-    """GQA output == MHA output on K/V heads repeated G times (bitwise)."""
+    """GQA output == the output on K/V heads repeated (bitwise): G times (MHA)
+    for the kernels that run each head alone, twice (G = 2) for the pair
+    kernel, whose workgroups hold a head pair."""
     qb, kb, vb = seeded(6, 300, 8, 2, 128)
+    rep = 2 if algo == attn.ALGO_SPLIT_PAIRS else 4
     gqa = run_prefill(qb, kb, vb, dev, algo)
-    mha = run_prefill(qb, np.repeat(kb, 4, axis=1), np.repeat(vb, 4, axis=1), dev, algo)
+    mha = run_prefill(qb, np.repeat(kb, rep, axis=1), np.repeat(vb, rep, axis=1), dev, algo)
     assert np.array_equal(gqa, mha)
 
 

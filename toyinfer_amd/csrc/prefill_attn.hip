@@ -778,34 +778,342 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_splitkv_kernel(PrefillP
     }
 }
 
+// ---------------------------------------------------------------------------
+// Split over keys with both query heads of a GQA pair in one workgroup.
+//
+// Eight waves take 32 query rows of the two heads 2j, 2j + 1 of pair j of a
+// KV head: waves w and w + 4 (which share a SIMD) run heads 2j and 2j + 1
+// over the same key tiles, stream w % 4 taking tiles w % 4, w % 4 + 4, ....
+// A stream's 32-key K and V tiles reach LDS by buffer loads that write LDS
+// (each of its two waves fills half), double-buffered, so one fetch serves
+// both heads, no registers stage a tile and no ds_write is issued; one
+// barrier per step of four tiles.  After the last step the partials merge in
+// LDS in two rounds (streams 2, 3 into 0, 1, then 1 into 0) while the next
+// item's first tiles and Q are already in flight.
+constexpr int kSpThreads = 512;
+
+template <int D>
+struct SpShape {
+    static constexpr int CPR = D / 8;
+    static constexpr int TILE = kSkBN * D;          // elements of one K or V tile
+    static constexpr int BLOCKS = TILE * 2 / 1024;  // 1 KiB DMA blocks per tile
+    static constexpr int BPW = BLOCKS / 2;          // per wave (two waves per stream)
+    static constexpr int STREAM = 2 * TILE;         // K then V
+    static constexpr int STAGE = 4 * STREAM;        // the four streams of one buffer
+    static constexpr int KSTEPS = D / 16;
+    static constexpr int DBLK = D / 32;
+};
+
+// Work item i = (KV head i % Hkv, head pair, 32-row block), heaviest (last)
+// row blocks first, as sk_item orders them.
+struct SpItem {
+    uint32_t h0, kvh, q0, n_tiles;
+};
+
+__device__ __forceinline__ SpItem sp_item(const PrefillProblem& p, uint32_t i, uint32_t group,
+                                          uint32_t n_qt) {
+    SpItem it;
+    const uint32_t pairs = group / 2;
+    it.kvh = i % p.hkv;
+    const uint32_t r = i / p.hkv;
+    it.h0 = it.kvh * group + 2 * (r % pairs);
+    it.q0 = (n_qt - 1 - r / pairs) * kSkBM;
+    it.n_tiles = (min(p.s, it.q0 + kSkBM) + kSkBN - 1) / kSkBN;
+    return it;
+}
+
+// One stream's tile at byte `off` of the KV head's K and V into LDS at sk
+// (K) and sk + TILE (V): this wave's blocks sub, sub + 2, ....
+template <int D>
+__device__ __forceinline__ void sp_dma_tile(const uint16_t* k_head, const uint16_t* v_head,
+                                            uint32_t kv_bytes, uint32_t off, const uint32_t* offk,
+                                            const uint32_t* offv, int sub, uint16_t* sk) {
+    using P = SpShape<D>;
+    const __amdgpu_buffer_rsrc_t rk = make_rsrc(reinterpret_cast<const char*>(k_head) + off, kv_bytes - off);
+    const __amdgpu_buffer_rsrc_t rv = make_rsrc(reinterpret_cast<const char*>(v_head) + off, kv_bytes - off);
+#pragma unroll
+    for (int j = 0; j < P::BPW; ++j) {
+        const int blk = sub + 2 * j;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (__attribute__((address_space(3))) void*)(sk + 512 * blk), 16, offk[j], 0, 0, 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (__attribute__((address_space(3))) void*)(sk + P::TILE + 512 * blk), 16, offv[j], 0, 0, 0);
+    }
+}
+
+// Workgroup barrier that waits for this wave's LDS operations only, leaving
+// its global loads (also those that write LDS) in flight; the memory clobber
+// keeps the compiler from moving memory accesses across it.
+__device__ __forceinline__ void lds_ops_barrier() {
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+template <int D, bool FUSED>
+__global__ __launch_bounds__(kSpThreads, 1) void prefill_splitkv_pair_kernel(PrefillProblem p,
+                                                                             float scale_log2,
+                                                                             uint32_t n_items) {
+    using P = SpShape<D>;
+    // Two buffers as separate arrays, so that the compiler can tell the one
+    // being read from the one the loads are filling.  The merge reuses the
+    // second (s_b): 4 waves x 64 lanes x D/2 floats = one buffer exactly.
+    __shared__ __align__(1024) uint16_t s_a[P::STAGE];
+    __shared__ __align__(1024) uint16_t s_b[P::STAGE];
+    __shared__ float2 s_ml[4][64];
+    static_assert(4 * 64 * (D / 2) * 4 == P::STAGE * 2, "merge area is one buffer");
+
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int ql = lane & 31, kg = lane >> 5;
+    const int sw = __builtin_amdgcn_readfirstlane(wave);
+    const int stream = sw & 3, sub = sw >> 2;
+    const uint32_t group = p.hq / p.hkv;
+    const uint32_t n_qt = (p.s + kSkBM - 1) / kSkBM;
+    const uint32_t row_bytes = p.hkv * D * 2;
+    const uint32_t kv_bytes = (p.s - 1) * row_bytes + D * 2;
+
+    // This lane's global chunk for each of its blocks of a tile (blocks
+    // sub, sub + 2, ...), laid out as the 128-row kernel's tiles.
+    uint32_t offk[P::BPW], offv[P::BPW];
+#pragma unroll
+    for (int j = 0; j < P::BPW; ++j) {
+        const int slot = 64 * (sub + 2 * j) + lane;
+        const int row = slot / P::CPR, phys = slot % P::CPR;
+        offk[j] = row * row_bytes + 16 * (phys ^ k_swz<D>(row));
+        offv[j] = row * row_bytes + 16 * (phys ^ v_swz<D>(row));
+    }
+    // Operand read offsets within a stream's tiles (elements).
+    int k_off[P::KSTEPS], v_off[P::DBLK];
+#pragma unroll
+    for (int ks = 0; ks < P::KSTEPS; ++ks) k_off[ks] = ql * D + 8 * ((2 * ks + kg) ^ k_swz<D>(ql));
+    {
+        const int s16 = lane & 15, g16 = lane >> 4;
+        const int vrow = 4 * kg + (s16 >> 2);
+#pragma unroll
+        for (int db = 0; db < P::DBLK; ++db) {
+            const int c = 4 * db + 2 * (g16 & 1) + ((s16 & 3) >> 1);
+            v_off[db] = vrow * D + 8 * (c ^ v_swz<D>(vrow)) + 4 * (s16 & 1);
+        }
+    }
+
+    uint32_t round = 0;
+    SpItem it = sp_item(p, blockIdx.x, group, n_qt);
+    const uint16_t* k_head = p.k + (int64_t)it.kvh * D;
+    const uint16_t* v_head = p.v + (int64_t)it.kvh * D;
+    // Tile t of the current item into buffer `buf` (this stream's part).
+    auto dma = [&](uint32_t t, uint16_t* buf) __attribute__((always_inline)) {
+        sp_dma_tile<D>(k_head, v_head, kv_bytes, t * kSkBN * row_bytes, offk, offv, sub,
+                       buf + stream * P::STREAM);
+    };
+    bf16x8_t qf[P::KSTEPS];
+    if ((uint32_t)stream < it.n_tiles) dma(stream, s_a);
+    load_q<D, FUSED>(qf, p, it.q0 + ql, it.h0 + sub, kg);
+
+    while (true) {
+        const uint32_t q0 = it.q0, qq = q0 + ql, n_tiles = it.n_tiles;
+        const uint32_t n_steps = (n_tiles + 3) / 4;
+        f32x16_t oacc[P::DBLK];
+#pragma unroll
+        for (int db = 0; db < P::DBLK; ++db)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) oacc[db][i] = 0.0f;
+        float m_run = -INFINITY, l_run = 0.0f;
+
+        // This stream's key tile t, from buffer `cur`.
+        auto tile = [&](uint32_t t, const uint16_t* cur) __attribute__((always_inline)) {
+            const uint16_t* kb = cur + stream * P::STREAM;
+            const uint16_t* vb = kb + P::TILE;
+            const uint32_t n0 = t * kSkBN;
+            f32x16_t st;
+#pragma unroll
+            for (int i = 0; i < 16; ++i) st[i] = 0.0f;
+            uint4 ka[P::KSTEPS];
+#pragma unroll
+            for (int ks = 0; ks < P::KSTEPS; ++ks) ka[ks] = *reinterpret_cast<const uint4*>(kb + k_off[ks]);
+#pragma unroll
+            for (int ks = 0; ks < P::KSTEPS; ++ks) st = mfma32x32x16(as_bf16x8(ka[ks]), qf[ks], st);
+            __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+#pragma unroll
+            for (int ks = 0; ks + 2 < P::KSTEPS; ++ks) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+            }
+            __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+            if (n0 + kSkBN - 1 > q0) {
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    const uint32_t key = n0 + 8 * (i / 4) + 4 * kg + (i % 4);
+                    if (key > qq) st[i] = -INFINITY;
+                }
+            }
+            float ma = fmaxf(st[0], st[1]), mb = fmaxf(st[8], st[9]);
+#pragma unroll
+            for (int i = 2; i < 8; i += 2) {
+                ma = fmaxf(fmaxf(ma, st[i]), st[i + 1]);
+                mb = fmaxf(fmaxf(mb, st[i + 8]), st[i + 9]);
+            }
+            const float mt = xor32_max(fmaxf(ma, mb)) * scale_log2;
+            const bool need = mt > m_run + kRescaleThreshold;
+            if (__any(need)) {
+                float alpha = 1.0f;
+                if (need) {
+                    alpha = __builtin_amdgcn_exp2f(m_run - mt);
+                    m_run = mt;
+                }
+                l_run *= alpha;
+#pragma unroll
+                for (int db = 0; db < P::DBLK; ++db)
+#pragma unroll
+                    for (int i = 0; i < 16; ++i) oacc[db][i] *= alpha;
+            }
+#pragma unroll
+            for (int i = 0; i < 16; ++i) st[i] = __builtin_amdgcn_exp2f(fmaf(st[i], scale_log2, -m_run));
+            bf16x8_t pf[2];
+#pragma unroll
+            for (int tt = 0; tt < 2; ++tt) {
+                const int o8 = 8 * tt;
+                pf[tt] = as_bf16x8(make_uint4(pack_bf16x2(st[o8 + 0], st[o8 + 1]),
+                                              pack_bf16x2(st[o8 + 2], st[o8 + 3]),
+                                              pack_bf16x2(st[o8 + 4], st[o8 + 5]),
+                                              pack_bf16x2(st[o8 + 6], st[o8 + 7])));
+            }
+            l_run += sum_bf16x8(__builtin_bit_cast(uint4, pf[0]),
+                                sum_bf16x8(__builtin_bit_cast(uint4, pf[1]), 0.0f));
+#pragma unroll
+            for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+                for (int db = 0; db < P::DBLK; ++db) {
+                    const v4i16_t lo = ds_read_tr16(vb + v_off[db] + 16 * tt * D);
+                    const v4i16_t hi = ds_read_tr16(vb + v_off[db] + (16 * tt + 8) * D);
+                    const uint4 a = make_uint4(__builtin_bit_cast(uint2, lo).x, __builtin_bit_cast(uint2, lo).y,
+                                               __builtin_bit_cast(uint2, hi).x, __builtin_bit_cast(uint2, hi).y);
+                    oacc[db] = mfma32x32x16(as_bf16x8(a), pf[tt], oacc[db]);
+                }
+        };
+        // Step s: step s + 1's tiles go to the other buffer (every wave was
+        // done with it at the previous step's barrier) and this stream's tile
+        // of step s is computed; then every wave waits for its loads and for
+        // the other waves.  The waits for the loads are explicit: the
+        // compiler does not track loads that write LDS across the loop's
+        // back edge.
+        auto step = [&](uint32_t s, const uint16_t* cur, uint16_t* nxt) __attribute__((always_inline)) {
+            const uint32_t tn = stream + 4 * (s + 1);
+            if (tn < n_tiles) dma(tn, nxt);
+            const uint32_t t = stream + 4 * s;
+            if (t < n_tiles) tile(t, cur);
+            __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+            __syncthreads();
+        };
+        __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);  // step 0's tiles and Q
+        __syncthreads();
+        for (uint32_t s = 0; s < n_steps; s += 2) {
+            step(s, s_a, s_b);
+            if (s + 1 < n_steps) step(s + 1, s_b, s_a);
+        }
+        // Every wave is done with both buffers (the last step's barrier): the
+        // next item's first tiles go to s_a and its Q to registers, landing
+        // while this item merges in s_b.  (With FUSED the grid holds every
+        // item: its Q prologue would not fit beside the merge's registers.)
+        ++round;
+        const uint32_t nxt = sk_item_index(round, blockIdx.x, gridDim.x);
+        const bool more = !FUSED && nxt < n_items;
+        const uint32_t h = it.h0 + sub;
+        if (more) {
+            it = sp_item(p, nxt, group, n_qt);
+            k_head = p.k + (int64_t)it.kvh * D;
+            v_head = p.v + (int64_t)it.kvh * D;
+            if ((uint32_t)stream < it.n_tiles) dma(stream, s_a);
+            load_q<D, FUSED>(qf, p, it.q0 + ql, it.h0 + sub, kg);
+        }
+
+        // Merge: (m, l, O) of this wave's rows with a partner wave's, element
+        // by element (lanes hold the same rows and dims in every wave).
+        float l_tot = xor32_sum(l_run);
+        float4* const s_mrg = reinterpret_cast<float4*>(s_b);
+        auto put = [&](int slot) __attribute__((always_inline)) {
+#pragma unroll
+            for (int db = 0; db < P::DBLK; ++db)
+#pragma unroll
+                for (int g = 0; g < 4; ++g)
+                    s_mrg[(slot * P::DBLK * 4 + db * 4 + g) * 64 + lane] =
+                        make_float4(oacc[db][4 * g], oacc[db][4 * g + 1], oacc[db][4 * g + 2], oacc[db][4 * g + 3]);
+            s_ml[slot][lane] = make_float2(m_run, l_tot);
+        };
+        auto take = [&](int slot) __attribute__((always_inline)) {
+            const float2 ml = s_ml[slot][lane];
+            const float M = fmaxf(m_run, ml.x);
+            const float wa = m_run == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m_run - M);
+            const float wb = ml.x == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(ml.x - M);
+#pragma unroll
+            for (int db = 0; db < P::DBLK; ++db)
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    const float4 x = s_mrg[(slot * P::DBLK * 4 + db * 4 + g) * 64 + lane];
+                    oacc[db][4 * g] = fmaf(wb, x.x, wa * oacc[db][4 * g]);
+                    oacc[db][4 * g + 1] = fmaf(wb, x.y, wa * oacc[db][4 * g + 1]);
+                    oacc[db][4 * g + 2] = fmaf(wb, x.z, wa * oacc[db][4 * g + 2]);
+                    oacc[db][4 * g + 3] = fmaf(wb, x.w, wa * oacc[db][4 * g + 3]);
+                }
+            l_tot = fmaf(wb, ml.y, wa * l_tot);
+            m_run = M;
+        };
+        // The merge's barriers wait for LDS operations only (a release fence
+        // on LDS would also wait for the next item's tile loads into s_a).
+        if (stream >= 2) put(2 * sub + (stream & 1));
+        lds_ops_barrier();
+        if (stream < 2) take(2 * sub + stream);
+        lds_ops_barrier();
+        if (stream == 1) put(sub);
+        lds_ops_barrier();
+        if (stream == 0) {
+            take(sub);
+            if (qq < p.s) {
+                const float inv = 1.0f / l_tot;
+                uint16_t* orow = p.o + ((int64_t)qq * p.hq + h) * D + 4 * kg;
+#pragma unroll
+                for (int db = 0; db < P::DBLK; ++db)
+#pragma unroll
+                    for (int g = 0; g < 4; ++g)
+                        *reinterpret_cast<uint2*>(orow + 32 * db + 8 * g) =
+                            make_uint2(pack_bf16x2(oacc[db][4 * g] * inv, oacc[db][4 * g + 1] * inv),
+                                       pack_bf16x2(oacc[db][4 * g + 2] * inv, oacc[db][4 * g + 3] * inv));
+            }
+        }
+        if (!more) break;
+    }
+}
+
 // Below this many 128-row workgroups the split-over-keys variant wins: the
 // 128-row kernel would leave CUs idle and be bound by its longest tile walk.
 constexpr uint32_t kSplitKvBelowWgs = 257;
 
-// Workgroups of the split kernel the device holds at once (CUs x resident
-// blocks per CU), queried once per device and variant; 256 CUs x 2 when no
-// device is visible.
-template <int D, bool FUSED>
-uint32_t splitkv_slots() {
-    static int cache[64];
+// Workgroups of a persistent split kernel the device holds at once (CUs x
+// resident blocks per CU), queried once per device into the caller's
+// per-kernel `cache`; `fallback` per CU when no device is visible.
+template <typename Kern>
+uint32_t resident_slots(Kern kern, int threads, int fallback, int (&cache)[64]) {
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
         (void)hipGetLastError();
-        return 256 * 2;
+        return 256 * fallback;
     }
     int v = __atomic_load_n(&cache[dev], __ATOMIC_RELAXED);
     if (v > 0) return (uint32_t)v;
     int cus = 0, per = 0;
     const hipError_t e1 = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
-    const hipError_t e2 = hipOccupancyMaxActiveBlocksPerMultiprocessor(
-        &per, prefill_splitkv_kernel<D, FUSED>, kPfThreads, 0);
+    const hipError_t e2 = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, kern, threads, 0);
     if (e1 != hipSuccess || e2 != hipSuccess || cus <= 0 || per <= 0) {
         (void)hipGetLastError();
-        return 256 * 2;
+        return 256 * fallback;
     }
     v = cus * per;
     __atomic_store_n(&cache[dev], v, __ATOMIC_RELAXED);
     return (uint32_t)v;
+}
+
+template <int D>
+hipError_t launch_pairs(const PrefillProblem& p, float sl2, uint32_t items, uint32_t slots,
+                        hipStream_t st) {
+    const dim3 grid(min(items, slots));
+    hipLaunchKernelGGL((prefill_splitkv_pair_kernel<D, false>), grid, dim3(kSpThreads), 0, st, p,
+                       sl2, items);
+    return hipGetLastError();
 }
 
 template <int D, bool FUSED>
@@ -813,9 +1121,23 @@ hipError_t launch_t(const PrefillProblem& p, hipStream_t st) {
     const uint32_t n_qtiles = (p.s + kPfBM - 1) / kPfBM;
     const float sl2 = kLog2e / sqrtf((float)D);
     const bool split = prefill_uses_split(p);
+    // Short sequences with an even GQA group take the pair kernel when asked
+    // (variant 3), or by shape when it has more items than the device holds
+    // workgroups of it at D = 128: with fewer it leaves CUs idle, and at
+    // D = 64 a tile's work is too small for its per-step barrier and merge
+    // (measured on MI355X: S = 1371, 16/8 heads, 21.3 -> 18.7 us at D = 128,
+    // 12.1 -> 12.5 us at D = 64; S = 512: 9.1 -> 10.8 us).  The fused Q
+    // prologue stays with the single-head kernel.
+    if (!FUSED && split && (p.hq / p.hkv) % 2 == 0 && p.variant != 1) {
+        static int cache[64];
+        const uint32_t items = ((p.s + kSkBM - 1) / kSkBM) * p.hkv * (p.hq / p.hkv / 2);
+        const uint32_t slots = resident_slots(prefill_splitkv_pair_kernel<D, false>, kSpThreads, 1, cache);
+        if (p.variant == 3 || (D == 128 && items > slots)) return launch_pairs<D>(p, sl2, items, slots, st);
+    }
     if (split) {
         const uint32_t items = ((p.s + kSkBM - 1) / kSkBM) * p.hq;
-        const dim3 grid(FUSED ? items : min(items, splitkv_slots<D, FUSED>()));
+        static int cache[64];
+        const dim3 grid(FUSED ? items : min(items, resident_slots(prefill_splitkv_kernel<D, FUSED>, kPfThreads, 2, cache)));
         hipLaunchKernelGGL((prefill_splitkv_kernel<D, FUSED>), grid, dim3(kPfThreads), 0, st, p,
                            sl2, items);
     } else {
@@ -829,7 +1151,7 @@ hipError_t launch_t(const PrefillProblem& p, hipStream_t st) {
 
 bool prefill_uses_split(const PrefillProblem& p) {
     const uint32_t n_qtiles = (p.s + kPfBM - 1) / kPfBM;
-    return p.variant == 1 || (p.variant == 0 && n_qtiles * p.hq < kSplitKvBelowWgs);
+    return p.variant == 1 || p.variant == 3 || (p.variant == 0 && n_qtiles * p.hq < kSplitKvBelowWgs);
 }
 
 hipError_t launch_prefill(const PrefillProblem& p, hipStream_t stream) {

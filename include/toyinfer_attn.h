@@ -50,10 +50,11 @@ int toyinfer_flash_attention_v1_bf16(const void* Qs, const void* Ks, const void*
 /* Same, with the kernel chosen explicitly (extension, for tuning and tests):
  * algo 0 = pick by shape (what toyinfer_flash_attention_v1_bf16 does),
  * 1 = 32-row workgroups whose waves split the keys (short sequences),
- * 2 = 128-row workgroups sharing each K/V tile (long sequences),
+ * 2 = 128-row workgroups of one head (long sequences),
  * 3 = as 1 with both query heads of a GQA pair in one workgroup sharing
- *     each K/V tile (what algo 0 runs for short sequences when Hq/Hkv is
- *     even; as 1 when it is odd). */
+ *     each K/V tile (as 1 when Hq/Hkv is odd),
+ * 4 = as 2 with both query heads of a GQA pair in one workgroup (as 2 when
+ *     Hq/Hkv is odd).  Algo 0 picks among them by shape. */
 int toyinfer_flash_attention_algo_bf16(const void* Qs, const void* Ks, const void* Vs, void* Os,
                                        uint32_t num_q_heads, uint32_t num_kv_heads,
                                        uint32_t heads_dim, uint32_t seq_len, int algo,

@@ -34,7 +34,7 @@ def prefill(qb, kb, vb, dev, algo):
     return H.bf16_bits_to_f32(H.from_dev_bf16(o))
 
 
-@pytest.mark.parametrize("algo", [attn.ALGO_SPLIT_KEYS, attn.ALGO_ROW_TILES, attn.ALGO_SPLIT_PAIRS])
+@pytest.mark.parametrize("algo", [attn.ALGO_SPLIT_KEYS, attn.ALGO_ROW_TILES, attn.ALGO_SPLIT_PAIRS, attn.ALGO_ROW_PAIRS])
 @pytest.mark.parametrize("name", ["seq1_gqa", "exact_kv_tile", "gqa_tail_tiles", "multi_kv_tile",
                                   "large_magnitude", "causal_focus"])
 def test_prefill_reference_cases_vs_golden(dev, name, algo):
@@ -43,7 +43,7 @@ def test_prefill_reference_cases_vs_golden(dev, name, algo):
     H.check_bar(got, H.bf16_bits_to_f32(g["o_bf16"]), name)
 
 
-@pytest.mark.parametrize("algo", [attn.ALGO_SPLIT_KEYS, attn.ALGO_ROW_TILES, attn.ALGO_SPLIT_PAIRS])
+@pytest.mark.parametrize("algo", [attn.ALGO_SPLIT_KEYS, attn.ALGO_ROW_TILES, attn.ALGO_SPLIT_PAIRS, attn.ALGO_ROW_PAIRS])
 def test_prefill_config1_vs_golden(dev, algo):
     g = gold("prefill_config1")
     sd = int(g["seed"])

@@ -141,7 +141,7 @@ def test_prefill_argument_validation():
     assert flash(s=0) == INVALID
     assert flash(q=None) == INVALID
     assert flash(k=P + 2) == INVALID               # 16-byte alignment
-    assert flash(algo=4) == INVALID
+    assert flash(algo=5) == INVALID
     assert flash(s=1 << 30) == UNSUPPORTED         # K/V rows beyond 32-bit byte offsets
     assert L.toyinfer_flash_attention_v1_bf16(P, P, P, P, 8, 3, 128, 4, None) == INVALID
 

@@ -16,7 +16,7 @@ from toyinfer_amd import attn, synth
 pytestmark = pytest.mark.gpu
 
 
-ALGOS = [attn.ALGO_SPLIT_KEYS, attn.ALGO_ROW_TILES, attn.ALGO_SPLIT_PAIRS]
+ALGOS = [attn.ALGO_SPLIT_KEYS, attn.ALGO_ROW_TILES, attn.ALGO_SPLIT_PAIRS, attn.ALGO_ROW_PAIRS]
 
 
 def run_prefill(q_bits, k_bits, v_bits, dev, algo=attn.ALGO_AUTO):
@@ -177,6 +177,19 @@ def test_algos_agree_at_long_s(dev, s, hq, hkv, d):
     H.check_bar(c, b, "split pairs vs rows", max_abs=1.6e-2, mean_abs=3e-4)
 
 
+@pytest.mark.parametrize("s,hq,hkv,d", [(700, 8, 2, 128), (1000, 32, 8, 128), (333, 16, 4, 64),
+                                         (129, 4, 2, 128), (4096, 32, 8, 128)])
+def test_row_pairs_equal_row_tiles_bitwise(dev, s, hq, hkv, d):
+    """The 128-row kernel with a GQA head pair per workgroup computes every
+    row as the single-head kernel does (same tiles in the same order): the
+    outputs are equal bit for bit."""
+    print(f"[prefill] row pairs vs row tiles S={s} {hq}/{hkv} D={d}", flush=True)
+    qb, kb, vb = seeded(9, s, hq, hkv, d)
+    a = run_prefill(qb, kb, vb, dev, attn.ALGO_ROW_TILES)
+    b = run_prefill(qb, kb, vb, dev, attn.ALGO_ROW_PAIRS)
+    assert np.array_equal(a, b)
+
+
 @pytest.mark.parametrize("algo", ALGOS)
 def test_deterministic(dev, algo):
     qb, kb, vb = seeded(5, 700, 8, 2, 128)
@@ -189,9 +202,9 @@ def test_deterministic(dev, algo):
 def test_gqa_equals_mha_with_repeated_kv(dev, algo):
     """GQA output == the output on K/V heads repeated (bitwise): G times (MHA)
     for the kernels that run each head alone, twice (G = 2) for the pair
-    kernel, whose workgroups hold a head pair."""
+    kernels, whose workgroups hold a head pair."""
     qb, kb, vb = seeded(6, 300, 8, 2, 128)
-    rep = 2 if algo == attn.ALGO_SPLIT_PAIRS else 4
+    rep = 2 if algo in (attn.ALGO_SPLIT_PAIRS, attn.ALGO_ROW_PAIRS) else 4
     gqa = run_prefill(qb, kb, vb, dev, algo)
     mha = run_prefill(qb, np.repeat(kb, rep, axis=1), np.repeat(vb, rep, axis=1), dev, algo)
     assert np.array_equal(gqa, mha)

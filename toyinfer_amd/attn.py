@@ -148,13 +148,13 @@ def flash_attention_v1_bf16(Qs, Ks, Vs, Os, num_q_heads: int, num_kv_heads: int,
                                                 _stream(stream)))
 
 
-ALGO_AUTO, ALGO_SPLIT_KEYS, ALGO_ROW_TILES, ALGO_SPLIT_PAIRS = 0, 1, 2, 3
+ALGO_AUTO, ALGO_SPLIT_KEYS, ALGO_ROW_TILES, ALGO_SPLIT_PAIRS, ALGO_ROW_PAIRS = 0, 1, 2, 3, 4
 
 
 def flash_attention_algo_bf16(Qs, Ks, Vs, Os, num_q_heads: int, num_kv_heads: int,
                               heads_dim: int, seq_len: int, algo: int, stream=None) -> None:
     """Prefill with an explicit kernel choice (0 auto, 1 split keys, 2 row tiles,
-    3 split keys with GQA head pairs)."""
+    3 split keys with GQA head pairs, 4 row tiles with GQA head pairs)."""
     _check("flash_attention_algo_bf16",
            LIB.toyinfer_flash_attention_algo_bf16(_ptr(Qs), _ptr(Ks), _ptr(Vs), _ptr(Os),
                                                   num_q_heads, num_kv_heads, heads_dim, seq_len,

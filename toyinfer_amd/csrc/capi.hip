@@ -141,7 +141,7 @@ int toyinfer_flash_attention_algo_bf16(const void* Qs, const void* Ks, const voi
                                        uint32_t heads_dim, uint32_t seq_len, int algo,
                                        void* stream) {
     if (int st = check_heads(num_q_heads, num_kv_heads, heads_dim)) return st;
-    if (algo < 0 || algo > 3) return TOYINFER_ERR_INVALID_ARGUMENT;
+    if (algo < 0 || algo > 4) return TOYINFER_ERR_INVALID_ARGUMENT;
     if (!kv_fits_32bit(seq_len, num_kv_heads, heads_dim)) return TOYINFER_ERR_UNSUPPORTED;
     if (seq_len == 0) return TOYINFER_ERR_INVALID_ARGUMENT;
     if (!Qs || !Ks || !Vs || !Os) return TOYINFER_ERR_INVALID_ARGUMENT;

@@ -118,7 +118,8 @@ struct PrefillProblem {
     const float* rope;        // [S][D/2] (cos, sin) pairs (fused_q)
     float eps;
     int variant;              // 0: pick by shape, 1: split over keys, 2: 128-row tiles,
-                              // 3: split over keys, GQA head pairs per workgroup (1 for odd groups)
+                              // 3: split over keys, GQA head pairs per workgroup (1 for odd groups),
+                              // 4: 128-row tiles, GQA head pairs per workgroup (2 for odd groups)
 };
 hipError_t launch_prefill(const PrefillProblem& p, hipStream_t stream);
 // Whether launch_prefill takes the split-over-keys kernel for this problem.

@@ -76,12 +76,12 @@ struct PfShape {
 // With these maps SQ_LDS_BANK_CONFLICT reads 524288 cycles per launch at
 // S=8192, 32/8 heads (256 per workgroup, about 2 % of the LDS-active
 // cycles; the earlier c ^ (row & 7) / c ^ 2*(row & 3) gave 6.8e7).
-template <int D>
+template <int D, int NW = kPfThreads / 64>
 struct DmaShape {
     static constexpr int CPR = D / 8;
     static constexpr int TILE_ELEMS = kPfBN * D;
     static constexpr int BLOCKS = kPfBN * D * 2 / 1024;        // 1 KiB blocks per tile and tensor
-    static constexpr int BLOCKS_PER_WAVE = BLOCKS / (kPfThreads / 64);
+    static constexpr int BLOCKS_PER_WAVE = BLOCKS / NW;        // NW waves fill a tile
     static constexpr int KSTEPS = D / 16;
     static constexpr int DBLK = D / 32;
 };
@@ -91,20 +91,21 @@ template <int D>
 __device__ __forceinline__ int v_swz(int row) { return D == 128 ? 4 * (row & 3) : 2 * (row & 3); }
 
 // This lane's byte offsets, within a tile, of the global chunks it loads
-// into its LDS slots (K and V maps), for each of the wave's 1 KiB blocks.
-template <int D>
+// into its LDS slots (K and V maps), for each of the wave's 1 KiB blocks
+// (blocks wave, wave + NW, ... of a tile filled by NW waves).
+template <int D, int NW>
 struct DmaOffsets {
-    uint32_t k[DmaShape<D>::BLOCKS_PER_WAVE];
-    uint32_t v[DmaShape<D>::BLOCKS_PER_WAVE];
+    uint32_t k[DmaShape<D, NW>::BLOCKS_PER_WAVE];
+    uint32_t v[DmaShape<D, NW>::BLOCKS_PER_WAVE];
 };
 
-template <int D>
-__device__ __forceinline__ DmaOffsets<D> dma_offsets(uint32_t row_bytes, int wave, int lane) {
-    using P = DmaShape<D>;
-    DmaOffsets<D> r;
+template <int D, int NW>
+__device__ __forceinline__ DmaOffsets<D, NW> dma_offsets(uint32_t row_bytes, int wave, int lane) {
+    using P = DmaShape<D, NW>;
+    DmaOffsets<D, NW> r;
 #pragma unroll
     for (int j = 0; j < P::BLOCKS_PER_WAVE; ++j) {
-        const int slot = 64 * (wave + (kPfThreads / 64) * j) + lane;  // 16-byte slot within the tile
+        const int slot = 64 * (wave + NW * j) + lane;  // 16-byte slot within the tile
         const int row = slot / P::CPR, phys = slot % P::CPR;
         r.k[j] = row * row_bytes + 16 * (phys ^ k_swz<D>(row));
         r.v[j] = row * row_bytes + 16 * (phys ^ v_swz<D>(row));
@@ -118,16 +119,16 @@ __device__ __forceinline__ DmaOffsets<D> dma_offsets(uint32_t row_bytes, int wav
 // which the scalar offset operand would escape), `wave` is a scalar (the
 // LDS destination, M0, is then a scalar sum), and the per-lane offsets are
 // loop invariants: a tile's issue costs no vector instructions.
-template <int D>
+template <int D, int NW>
 __device__ __forceinline__ void dma_tile(const uint16_t* k_head, const uint16_t* v_head, uint32_t kv_bytes,
                                          const uint32_t* offk, const uint32_t* offv, int wave, uint32_t tile_off,
                                          uint16_t* sk, uint16_t* sv) {
-    using P = DmaShape<D>;
+    using P = DmaShape<D, NW>;
     const __amdgpu_buffer_rsrc_t rk = make_rsrc(reinterpret_cast<const char*>(k_head) + tile_off, kv_bytes - tile_off);
     const __amdgpu_buffer_rsrc_t rv = make_rsrc(reinterpret_cast<const char*>(v_head) + tile_off, kv_bytes - tile_off);
 #pragma unroll
     for (int j = 0; j < P::BLOCKS_PER_WAVE; ++j) {
-        const int blk = wave + (kPfThreads / 64) * j;
+        const int blk = wave + NW * j;
         __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (__attribute__((address_space(3))) void*)(sk + 512 * blk), 16, offk[j], 0, 0, 0);
         __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (__attribute__((address_space(3))) void*)(sv + 512 * blk), 16, offv[j], 0, 0, 0);
     }
@@ -254,9 +255,14 @@ __device__ __forceinline__ void load_q(bf16x8_t (&qf)[PfShape<D>::KSTEPS], const
     }
 }
 
-template <int D, bool FUSED>
-__global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(PrefillProblem p, float scale_log2) {
-    using P = DmaShape<D>;
+// PAIR: eight waves, the two query heads of a GQA pair over the same 128
+// rows (waves w and w + 4, which share a SIMD, take head 2j and 2j + 1 of
+// pair j), so that one K/V tile in LDS serves both: half the DMA and L2
+// reads per head; one workgroup per CU instead of two.
+template <int D, bool FUSED, bool PAIR>
+__global__ __launch_bounds__(PAIR ? 512 : kPfThreads, PAIR ? 1 : 2) void prefill_kernel(PrefillProblem p, float scale_log2) {
+    constexpr int NW = PAIR ? 8 : kPfThreads / 64;
+    using P = DmaShape<D, NW>;
     // Four separate arrays (not one indexed by buffer): the compiler can then
     // tell the tile being computed from the one the LDS DMA is filling, and
     // does not make the operand reads wait for the in-flight loads.
@@ -272,12 +278,13 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(PrefillProblem p
     const uint32_t bid = blockIdx.x;
     const uint32_t kvh = bid % p.hkv;
     const uint32_t r = bid / p.hkv;
-    const uint32_t h = kvh * group + r % group;
-    const uint32_t qt = n_qtiles - 1 - r / group;
+    const uint32_t hpw = PAIR ? 2 : 1;  // heads per workgroup
+    const uint32_t h = kvh * group + hpw * (r % (group / hpw)) + (PAIR ? wave >> 2 : 0);
+    const uint32_t qt = n_qtiles - 1 - r / (group / hpw);
 
     const uint32_t q_end = min(p.s, (qt + 1) * kPfBM);
     const uint32_t n_tiles = (q_end + kPfBN - 1) / kPfBN;
-    const uint32_t q0 = qt * kPfBM + wave * 32;
+    const uint32_t q0 = qt * kPfBM + (wave & 3) * 32;
     const uint32_t qq = q0 + ql;
     const uint32_t wave_tiles = q0 < p.s ? (min(q0 + 31, p.s - 1) / kPfBN + 1) : 0;
     // K/V rows of this KV head: row t at byte t*row_bytes from the head's
@@ -288,8 +295,8 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(PrefillProblem p
     const uint16_t* v_head = p.v + (int64_t)kvh * D;
 
     const int swave = __builtin_amdgcn_readfirstlane(wave);
-    const DmaOffsets<D> doff = dma_offsets<D>(row_bytes, swave, lane);
-    dma_tile<D>(k_head, v_head, kv_bytes, doff.k, doff.v, swave, 0, s_k0, s_v0);
+    const DmaOffsets<D, NW> doff = dma_offsets<D, NW>(row_bytes, swave, lane);
+    dma_tile<D, NW>(k_head, v_head, kv_bytes, doff.k, doff.v, swave, 0, s_k0, s_v0);
     bf16x8_t qf[P::KSTEPS];
     load_q<D, FUSED>(qf, p, qq, h, kg);
 
@@ -315,13 +322,14 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(PrefillProblem p
             v_off[db] = vrow * D + 8 * (c ^ v_swz<D>(vrow)) + 4 * (s16 & 1);
         }
     }
+    __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);  // the first tile (and Q)
     __syncthreads();
 
     // Tile t computes from (kb, vb) while tile t+1 streams into (kn, vn),
     // whose last readers passed the previous barrier.
     auto step = [&](uint32_t t, const uint16_t* kb, const uint16_t* vb, uint16_t* kn,
                     uint16_t* vn) __attribute__((always_inline)) {
-        if (t + 1 < n_tiles) dma_tile<D>(k_head, v_head, kv_bytes, doff.k, doff.v, swave, (t + 1) * kPfBN * row_bytes, kn, vn);
+        if (t + 1 < n_tiles) dma_tile<D, NW>(k_head, v_head, kv_bytes, doff.k, doff.v, swave, (t + 1) * kPfBN * row_bytes, kn, vn);
 
         if (t < wave_tiles) {
             const uint32_t n0 = t * kPfBN;
@@ -453,7 +461,10 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(PrefillProblem p
             __builtin_amdgcn_sched_group_barrier(0x008, P::DBLK, 0);
         }
 
-        __syncthreads();  // (waits for this wave's tile loads, then for every wave)
+        // This wave's tile loads, then every wave.  The wait is explicit: the
+        // compiler's tracking of loads that write LDS is not relied on.
+        __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+        __syncthreads();
     };
     for (uint32_t t = 0; t < n_tiles; t += 2) {
         step(t, s_k0, s_v0, s_k1, s_v1);
@@ -472,7 +483,8 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_kernel(PrefillProblem p
     {
         constexpr int CPR = D / 8;
         const float inv = 1.0f / l_tot;  // (rows past S: not stored)
-        uint16_t* so = (wave < 2 ? s_k0 : s_k1) + (wave & 1) * 32 * D;
+        uint16_t* so = ((wave >> 1) == 0 ? s_k0 : (wave >> 1) == 1 ? s_k1 : (wave >> 1) == 2 ? s_v0 : s_v1) +
+                       (wave & 1) * 32 * D;
 #pragma unroll
         for (int db = 0; db < P::DBLK; ++db)
 #pragma unroll
@@ -1141,8 +1153,20 @@ hipError_t launch_t(const PrefillProblem& p, hipStream_t st) {
         hipLaunchKernelGGL((prefill_splitkv_kernel<D, FUSED>), grid, dim3(kPfThreads), 0, st, p,
                            sl2, items);
     } else {
-        const dim3 grid(n_qtiles * p.hq);
-        hipLaunchKernelGGL((prefill_kernel<D, FUSED>), grid, dim3(kPfThreads), 0, st, p, sl2);
+        // Head pairs per workgroup when the GQA group is even and the pair
+        // grid is at least two rounds of the device (measured on MI355X,
+        // 32/8 heads: S = 8192 490 -> 479 us, S = 4096 150 -> 143 us, but
+        // S = 2048, one round, 50 -> 58 us).
+        static int cache[64];
+        const uint32_t pair_wgs = n_qtiles * (p.hq / 2);
+        const bool even = (p.hq / p.hkv) % 2 == 0;
+        if (even && (p.variant == 4 ||
+                     (p.variant == 0 && pair_wgs >= 2 * resident_slots(prefill_kernel<D, FUSED, true>, 512, 1, cache)))) {
+            hipLaunchKernelGGL((prefill_kernel<D, FUSED, true>), dim3(pair_wgs), dim3(512), 0, st, p, sl2);
+        } else {
+            hipLaunchKernelGGL((prefill_kernel<D, FUSED, false>), dim3(n_qtiles * p.hq), dim3(kPfThreads), 0,
+                               st, p, sl2);
+        }
     }
     return hipGetLastError();
 }

@@ -74,7 +74,7 @@ def traffic_bytes(workload):
     return int(round((r * FETCH_SCALE + w * WRITE_SCALE) * 1024))
 WORKLOADS = ("all", "prefill", "prefill_fused", "decode_b8_l4096", "decode_b1_l32768",
              "decode_step", "decode_contract", "decode_engine_lean", "proj_gemv", "proj_gemm", "qwen3_e2e",
-             "sample", "copy_calibration")
+             "sample", "copy_calibration", "torch_sdpa")
 
 
 def causal_flops(s, hq, d):
@@ -186,6 +186,39 @@ def bench_prefill(dev, stream, steps, warmup, s=1371, hq=16, hkv=8, d=128):
             "ms_per_step": round(ms, 5), "value": round(tflops, 2), "unit": "TFLOP/s",
             "roofline": roofline("mfma", tflops, PEAK_BF16_TFLOPS, "TFLOP/s",
                                  traffic_bytes("prefill"))}
+
+
+def bench_torch_sdpa(dev, stream, steps, warmup):
+    """For scale, not a measurement of this library: PyTorch's own causal
+    attention on this GPU (torch.nn.functional.scaled_dot_product_attention,
+    is_causal, enable_gqa; its ROCm flash kernel) on the attention of
+    configs[3] (S=8192, 32/8 heads, no QK-norm/RoPE) and configs[1]
+    (S=1371, 16/8), with this library's row-tile and auto kernels on the same
+    inputs beside it."""
+    import torch
+    import torch.nn.functional as F
+
+    from toyinfer_amd import attn
+
+    out = {"workload": "torch_sdpa_causal_gqa_d128",
+           "entry": "torch.nn.functional.scaled_dot_product_attention (for scale)"}
+    for (s, hq, hkv) in ((8192, 32, 8), (1371, 16, 8)):
+        _, (q, k, v) = prefill_inputs(s, hq, hkv, 128, dev)
+        qt, kt, vt = (x.permute(1, 0, 2).unsqueeze(0).contiguous() for x in (q, k, v))
+        ms_t = time_steps(lambda i: F.scaled_dot_product_attention(qt, kt, vt, is_causal=True,
+                                                                   enable_gqa=True),
+                          steps, warmup, stream)
+        o = torch.empty((s, hq, 128), dtype=torch.bfloat16, device=dev)
+        ms_o = time_steps(lambda i: attn.flash_attention_v1_bf16(q, k, v, o, hq, hkv, 128, s, stream),
+                          steps, warmup, stream)
+        fl = causal_flops(s, hq, 128)
+        out[f"s{s}_hq{hq}_hkv{hkv}"] = {
+            "torch_sdpa_us": round(ms_t * 1e3, 2), "torch_sdpa_tflops": round(fl / (ms_t * 1e-3) / 1e12, 1),
+            "this_library_us": round(ms_o * 1e3, 2),
+            "this_library_tflops": round(fl / (ms_o * 1e-3) / 1e12, 1)}
+    out["value"] = out["s8192_hq32_hkv8"]["torch_sdpa_tflops"]
+    out["unit"] = "TFLOP/s"
+    return out
 
 
 FUSED = dict(s=8192, hq=32, hkv=8, d=128, eps=1e-6, theta=1e6)
@@ -646,6 +679,7 @@ def main():
         "proj_gemm": lambda: bench_proj_gemm(dev, stream, max(200, args.steps), 50),
         "sample": lambda: bench_sample(dev, stream, max(200, args.steps), 50),
         "qwen3_e2e": lambda: bench_qwen3_e2e(dev),
+        "torch_sdpa": lambda: bench_torch_sdpa(dev, stream, 20, 3),
         "copy_calibration": lambda: bench_copy(dev, stream, args.steps, args.warmup),
     }
     if args.workload != "all":
@@ -688,7 +722,7 @@ def main():
                               ("prefill", "decode_b8_l4096", "decode_b1_l32768", "decode_step",
                                "decode_contract", "decode_engine_lean", "proj_gemv",
                                "proj_gemm", "sample",
-                               "qwen3_e2e")]
+                               "qwen3_e2e", "torch_sdpa")]
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(host, gpu_out, args.cpu_seconds)
     print(json.dumps(line), flush=True)

@@ -178,7 +178,8 @@ def test_algos_agree_at_long_s(dev, s, hq, hkv, d):
 
 
 @pytest.mark.parametrize("s,hq,hkv,d", [(700, 8, 2, 128), (1000, 32, 8, 128), (333, 16, 4, 64),
-                                         (129, 4, 2, 128), (4096, 32, 8, 128)])
+                                         (129, 4, 2, 128), (4096, 32, 8, 128), (4100, 32, 8, 128),
+                                         (2049, 16, 4, 64)])
 def test_row_pairs_equal_row_tiles_bitwise(dev, s, hq, hkv, d):
     """The 128-row kernel with a GQA head pair per workgroup computes every
     row as the single-head kernel does (same tiles in the same order): the

@@ -177,6 +177,21 @@ def test_fused_equals_unfused_composition(dev):
     H.check_bar(a, b, "fused vs unfused", max_abs=1e-2, mean_abs=2e-4)
 
 
+def test_fused_prefill_head_pairs_ragged_rows(dev):
+    """The fused entry at a length where the head-pair 128-row kernel is
+    chosen (S = 4100, 32/8: 33 query tiles x 16 pairs, two rounds of the
+    device) with a partial last query tile: first and last rows and every
+    37th against the oracle."""
+    s, hq, hkv, d = 4100, 32, 8, 128
+    print("[fused] S=4100 32/8 head pairs, row subset", flush=True)
+    qb, kb, vb, gq, gk = config4_inputs(s, hq, hkv, d, seed=7)
+    got, k_out, _ = fused_prefill(qb, kb, vb, gq, gk, 1e-6, 1e6, dev)
+    rows = sorted(set(range(40)) | set(range(s - 40, s)) | set(range(0, s, 37)))
+    exp, kn = oracle_fused(qb, kb, vb, gq, gk, 1e-6, 1e6, rows=rows)
+    H.check_bar(H.bf16_bits_to_f32(k_out), kn, "K_out")
+    H.check_bar(H.bf16_bits_to_f32(got[rows]), oracle.round_bf16(exp[rows]), "fused O rows")
+
+
 def test_config4_row_subset(dev):
     """Config 4 (S=8192, 32/8, D=128): rows 0-63, 8128-8191 and every 61st
     against the oracle (the full fp64 reference is minutes of CPU)."""

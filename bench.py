@@ -189,12 +189,12 @@ def bench_prefill(dev, stream, steps, warmup, s=1371, hq=16, hkv=8, d=128):
 
 
 def bench_torch_sdpa(dev, stream, steps, warmup):
-    """For scale, not a measurement of this library: PyTorch's own causal
-    attention on this GPU (torch.nn.functional.scaled_dot_product_attention,
-    is_causal, enable_gqa; its ROCm flash kernel) on the attention of
-    configs[3] (S=8192, 32/8 heads, no QK-norm/RoPE) and configs[1]
-    (S=1371, 16/8), with this library's row-tile and auto kernels on the same
-    inputs beside it."""
+    """For scale, not a measurement of this library: PyTorch's own attention
+    on this GPU (torch.nn.functional.scaled_dot_product_attention, is_causal,
+    enable_gqa; its ROCm flash kernel) on the attention of configs[3]
+    (S=8192, 32/8 heads, no QK-norm/RoPE) and configs[1] (S=1371, 16/8), with
+    this library's prefill on the same inputs beside it, and on the decode
+    shapes of configs[2] and the north-star decode."""
     import torch
     import torch.nn.functional as F
 
@@ -216,6 +216,19 @@ def bench_torch_sdpa(dev, stream, steps, warmup):
             "torch_sdpa_us": round(ms_t * 1e3, 2), "torch_sdpa_tflops": round(fl / (ms_t * 1e-3) / 1e12, 1),
             "this_library_us": round(ms_o * 1e3, 2),
             "this_library_tflops": round(fl / (ms_o * 1e-3) / 1e12, 1)}
+    # Decode shapes (one query row per sequence; the same KV set every call,
+    # so the Infinity Cache may hold it, unlike the decode components above).
+    for (b, L) in ((8, 4096), (1, 32768)):
+        g = torch.Generator(device=dev).manual_seed(SEED + 61)
+        qd = torch.randn((b, 32, 1, 128), generator=g, device=dev).to(torch.bfloat16)
+        kd = torch.randn((b, 8, L, 128), generator=g, device=dev).to(torch.bfloat16)
+        vd = torch.randn((b, 8, L, 128), generator=g, device=dev).to(torch.bfloat16)
+        ms_t = time_steps(lambda i: F.scaled_dot_product_attention(qd, kd, vd, enable_gqa=True),
+                          steps, warmup, stream)
+        out[f"decode_b{b}_l{L}_hq32_hkv8"] = {
+            "torch_sdpa_us": round(ms_t * 1e3, 2),
+            "torch_sdpa_gbps": round(2.0 * b * L * 8 * 128 * 2 / (ms_t * 1e-3) / 1e9, 1)}
+        del qd, kd, vd
     out["value"] = out["s8192_hq32_hkv8"]["torch_sdpa_tflops"]
     out["unit"] = "TFLOP/s"
     return out

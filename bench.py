@@ -16,7 +16,8 @@ kernels run on.
 
 The same line carries, under "components", the other hot-path workloads,
 each with its own roofline block:
-  * prefill_s1371: configs[1], S=1371, 16/8 (toyinfer_flash_attention_v1_bf16);
+  * prefill_s1371: configs[1], S=1371, 16/8 (toyinfer_flash_attention_v1_bf16), after
+    0.1 s of the same call untimed;
   * decode_b8_l4096: configs[2], split-K decode over 128 MiB of KV, HBM-bound;
   * decode_b1_l32768: the north-star 32k-token decode, 128 MiB of KV;
   * decode_step / decode_contract: the decode-step pre-pass and the
@@ -170,19 +171,25 @@ def prefill_inputs(s, hq, hkv, d, dev, seed=SEED):
     return (qb, kb, vb), (to_dev(qb, dev), to_dev(kb, dev), to_dev(vb, dev))
 
 
-def bench_prefill(dev, stream, steps, warmup, s=1371, hq=16, hkv=8, d=128):
-    """causal GQA prefill through toyinfer_flash_attention_v1_bf16."""
+def bench_prefill(dev, stream, steps, warmup, s=1371, hq=16, hkv=8, d=128, settle_s=0.1):
+    """causal GQA prefill through toyinfer_flash_attention_v1_bf16.
+    The call first runs untimed for `settle_s` seconds (see settle()): the
+    component follows host-side input generation that leaves the GPU idle,
+    and its 100 timed launches (about 2 ms) would otherwise fall inside the
+    power controller's transient."""
     import torch
 
     from toyinfer_amd import attn
 
     _, (q, k, v) = prefill_inputs(s, hq, hkv, d, dev)
     o = torch.empty((s, hq, d), dtype=torch.bfloat16, device=dev)
-    ms = time_steps(lambda i: attn.flash_attention_v1_bf16(q, k, v, o, hq, hkv, d, s, stream),
-                    steps, warmup, stream)
+    fn = lambda i: attn.flash_attention_v1_bf16(q, k, v, o, hq, hkv, d, s, stream)
+    n_settle = settle(fn, stream, settle_s) if settle_s > 0 else 0
+    ms = time_steps(fn, steps, warmup, stream)
     tflops = causal_flops(s, hq, d) / (ms * 1e-3) / 1e12
     return {"workload": f"prefill_causal_gqa_s{s}_hq{hq}_hkv{hkv}_d{d}",
             "entry": "toyinfer_flash_attention_v1_bf16", "steps": steps,
+            "settle_s": settle_s, "settle_launches": n_settle,
             "ms_per_step": round(ms, 5), "value": round(tflops, 2), "unit": "TFLOP/s",
             "roofline": roofline("mfma", tflops, PEAK_BF16_TFLOPS, "TFLOP/s",
                                  traffic_bytes("prefill"))}

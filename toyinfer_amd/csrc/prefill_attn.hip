@@ -799,9 +799,10 @@ __global__ __launch_bounds__(kPfThreads, 2) void prefill_splitkv_kernel(PrefillP
 // A stream's 32-key K and V tiles reach LDS by buffer loads that write LDS
 // (each of its two waves fills half), double-buffered, so one fetch serves
 // both heads, no registers stage a tile and no ds_write is issued; one
-// barrier per step of four tiles.  After the last step the partials merge in
-// LDS in two rounds (streams 2, 3 into 0, 1, then 1 into 0) while the next
-// item's first tiles and Q are already in flight.
+// barrier per step of four tiles.  After the last step the four streams'
+// partials merge in LDS in two exchange rounds in which every wave takes part
+// (each then writes a quarter of its head's output), while the next item's
+// first tiles and Q are already in flight.
 constexpr int kSpThreads = 512;
 
 template <int D>
@@ -858,6 +859,192 @@ __device__ __forceinline__ void lds_ops_barrier() {
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
+// A partner's N float4 (1 KiB apart: lane l at src + 16 l) and its (m, l)
+// pair, read from LDS in one asm block that also waits for them.  In asm
+// the reads are not LDS accesses to the compiler, which would otherwise make
+// them wait for every buffer load writing LDS (the next item's tiles and Q,
+// in flight into other buffers).
+template <int N>
+__device__ __forceinline__ float2 sp_read(float4 (&x)[N], const float4* src, const float2* ml, int lane) {
+    const uint32_t a = (uint32_t)(size_t)(const __attribute__((address_space(3))) void*)(src + lane);
+    const uint32_t b = (uint32_t)(size_t)(const __attribute__((address_space(3))) void*)(ml + lane);
+    f32x4_t v[N];
+    float2 r;
+    typedef float f32x2_t __attribute__((ext_vector_type(2)));
+    f32x2_t m;
+    static_assert(N == 2 || N == 4 || N == 8, "read count");
+    if constexpr (N == 2) {
+        asm volatile(
+            "ds_read_b128 %0, %3\n\t"
+            "ds_read_b128 %1, %3 offset:1024\n\t"
+            "ds_read_b64 %2, %4\n\t"
+            "s_waitcnt lgkmcnt(0)"
+            : "=&v"(v[0]), "=&v"(v[1]), "=&v"(m)
+            : "v"(a), "v"(b)
+            : "memory");
+    } else if constexpr (N == 4) {
+        asm volatile(
+            "ds_read_b128 %0, %5\n\t"
+            "ds_read_b128 %1, %5 offset:1024\n\t"
+            "ds_read_b128 %2, %5 offset:2048\n\t"
+            "ds_read_b128 %3, %5 offset:3072\n\t"
+            "ds_read_b64 %4, %6\n\t"
+            "s_waitcnt lgkmcnt(0)"
+            : "=&v"(v[0]), "=&v"(v[1]), "=&v"(v[2]), "=&v"(v[3]), "=&v"(m)
+            : "v"(a), "v"(b)
+            : "memory");
+    } else {
+        asm volatile(
+            "ds_read_b128 %0, %9\n\t"
+            "ds_read_b128 %1, %9 offset:1024\n\t"
+            "ds_read_b128 %2, %9 offset:2048\n\t"
+            "ds_read_b128 %3, %9 offset:3072\n\t"
+            "ds_read_b128 %4, %9 offset:4096\n\t"
+            "ds_read_b128 %5, %9 offset:5120\n\t"
+            "ds_read_b128 %6, %9 offset:6144\n\t"
+            "ds_read_b128 %7, %9 offset:7168\n\t"
+            "ds_read_b64 %8, %10\n\t"
+            "s_waitcnt lgkmcnt(0)"
+            : "=&v"(v[0]), "=&v"(v[1]), "=&v"(v[2]), "=&v"(v[3]), "=&v"(v[4]), "=&v"(v[5]), "=&v"(v[6]),
+              "=&v"(v[7]), "=&v"(m)
+            : "v"(a), "v"(b)
+            : "memory");
+    }
+#pragma unroll
+    for (int i = 0; i < N; ++i) x[i] = make_float4(v[i].x, v[i].y, v[i].z, v[i].w);
+    r = make_float2(m.x, m.y);
+    return r;
+}
+// This wave's N float4 (lane l at dst + 16 l, 1 KiB apart) and its (m, l)
+// pair, written to LDS in asm for the same reason as sp_read (the barrier
+// that follows waits for them).
+template <int N>
+__device__ __forceinline__ void sp_write(float4* dst, float2* ml, int lane, const float4 (&x)[N], float2 mlv) {
+    const uint32_t a = (uint32_t)(size_t)(__attribute__((address_space(3))) void*)(dst + lane);
+    const uint32_t b = (uint32_t)(size_t)(__attribute__((address_space(3))) void*)(ml + lane);
+    typedef float f32x2_t __attribute__((ext_vector_type(2)));
+    f32x4_t v[N];
+#pragma unroll
+    for (int i = 0; i < N; ++i) v[i] = f32x4_t{x[i].x, x[i].y, x[i].z, x[i].w};
+    const f32x2_t m = f32x2_t{mlv.x, mlv.y};
+    static_assert(N == 2 || N == 4 || N == 8, "write count");
+    if constexpr (N == 2) {
+        asm volatile(
+            "ds_write_b128 %0, %2\n\t"
+            "ds_write_b128 %0, %3 offset:1024\n\t"
+            "ds_write_b64 %1, %4"
+            :
+            : "v"(a), "v"(b), "v"(v[0]), "v"(v[1]), "v"(m)
+            : "memory");
+    } else if constexpr (N == 4) {
+        asm volatile(
+            "ds_write_b128 %0, %2\n\t"
+            "ds_write_b128 %0, %3 offset:1024\n\t"
+            "ds_write_b128 %0, %4 offset:2048\n\t"
+            "ds_write_b128 %0, %5 offset:3072\n\t"
+            "ds_write_b64 %1, %6"
+            :
+            : "v"(a), "v"(b), "v"(v[0]), "v"(v[1]), "v"(v[2]), "v"(v[3]), "v"(m)
+            : "memory");
+    } else {
+        asm volatile(
+            "ds_write_b128 %0, %2\n\t"
+            "ds_write_b128 %0, %3 offset:1024\n\t"
+            "ds_write_b128 %0, %4 offset:2048\n\t"
+            "ds_write_b128 %0, %5 offset:3072\n\t"
+            "ds_write_b128 %0, %6 offset:4096\n\t"
+            "ds_write_b128 %0, %7 offset:5120\n\t"
+            "ds_write_b128 %0, %8 offset:6144\n\t"
+            "ds_write_b128 %0, %9 offset:7168\n\t"
+            "ds_write_b64 %1, %10"
+            :
+            : "v"(a), "v"(b), "v"(v[0]), "v"(v[1]), "v"(v[2]), "v"(v[3]), "v"(v[4]), "v"(v[5]), "v"(v[6]),
+              "v"(v[7]), "v"(m)
+            : "memory");
+    }
+}
+// Weights of two partials with running maxima ma, mb (log2 units) in their
+// merge: exp2(m - max(ma, mb)), 0 for a partial that saw no key.
+__device__ __forceinline__ void sp_weights(float ma, float mb, float& wa, float& wb) {
+    const float M = fmaxf(ma, mb);
+    wa = ma == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(ma - M);
+    wb = mb == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mb - M);
+}
+// The two exchange rounds of an item's merge for the waves of stream K (all
+// indices compile-time): give half GIVE_H of the float4 to the partner k ^ 2
+// and fold its copy of half KEEP_H in, then give quarter K ^ 1 to partner
+// k ^ 1 (through slot sw ^ 2, which only this wave read in the first round)
+// and fold its copy of quarter K in.  On return `part` holds quarter K of
+// the merged O and m_run / l_tot the merged statistics.
+template <int K, int DB>
+__device__ __forceinline__ void sp_merge_stream(f32x16_t (&o)[DB], float4* area, float2 (*s_ml)[64], int sw,
+                                                int lane, float& m_run, float& l_tot, float4 (&part)[DB]) {
+    constexpr int NF = DB * 4, HALF = NF / 2, QTR = NF / 4;
+    constexpr int KEEP_H = (K & 2) ? HALF : 0, GIVE_H = HALF - KEEP_H;
+    constexpr int KEEP_Q = K * QTR, GIVE_Q = (K ^ 1) * QTR;
+    {
+        float4 g[HALF];
+#pragma unroll
+        for (int i = 0; i < HALF; ++i) {
+            const int f = GIVE_H + i;
+            g[i] = make_float4(o[f / 4][4 * (f % 4)], o[f / 4][4 * (f % 4) + 1], o[f / 4][4 * (f % 4) + 2],
+                               o[f / 4][4 * (f % 4) + 3]);
+        }
+        sp_write<HALF>(area + sw * HALF * 64, s_ml[sw], lane, g, make_float2(m_run, l_tot));
+    }
+    lds_ops_barrier();
+    {
+        float4 x[HALF];
+        const float2 ml = sp_read<HALF>(x, area + (sw ^ 2) * HALF * 64, s_ml[sw ^ 2], lane);
+        float wa, wb;
+        sp_weights(m_run, ml.x, wa, wb);
+#pragma unroll
+        for (int i = 0; i < HALF; ++i) {
+            const int f = KEEP_H + i;
+            o[f / 4][4 * (f % 4)] = fmaf(wb, x[i].x, wa * o[f / 4][4 * (f % 4)]);
+            o[f / 4][4 * (f % 4) + 1] = fmaf(wb, x[i].y, wa * o[f / 4][4 * (f % 4) + 1]);
+            o[f / 4][4 * (f % 4) + 2] = fmaf(wb, x[i].z, wa * o[f / 4][4 * (f % 4) + 2]);
+            o[f / 4][4 * (f % 4) + 3] = fmaf(wb, x[i].w, wa * o[f / 4][4 * (f % 4) + 3]);
+        }
+        l_tot = fmaf(wb, ml.y, wa * l_tot);
+        m_run = fmaxf(m_run, ml.x);
+    }
+    {
+        float4 g[QTR];
+#pragma unroll
+        for (int i = 0; i < QTR; ++i) {
+            const int f = GIVE_Q + i;
+            g[i] = make_float4(o[f / 4][4 * (f % 4)], o[f / 4][4 * (f % 4) + 1], o[f / 4][4 * (f % 4) + 2],
+                               o[f / 4][4 * (f % 4) + 3]);
+        }
+        sp_write<QTR>(area + (sw ^ 2) * HALF * 64, s_ml[sw ^ 2], lane, g, make_float2(m_run, l_tot));
+    }
+    lds_ops_barrier();
+    {
+        float4 x[QTR];
+        const float2 ml = sp_read<QTR>(x, area + (sw ^ 3) * HALF * 64, s_ml[sw ^ 3], lane);
+        float wa, wb;
+        sp_weights(m_run, ml.x, wa, wb);
+#pragma unroll
+        for (int i = 0; i < QTR; ++i) {
+            const int f = KEEP_Q + i;
+            part[i] = make_float4(fmaf(wb, x[i].x, wa * o[f / 4][4 * (f % 4)]),
+                                  fmaf(wb, x[i].y, wa * o[f / 4][4 * (f % 4) + 1]),
+                                  fmaf(wb, x[i].z, wa * o[f / 4][4 * (f % 4) + 2]),
+                                  fmaf(wb, x[i].w, wa * o[f / 4][4 * (f % 4) + 3]));
+        }
+        l_tot = fmaf(wb, ml.y, wa * l_tot);
+        m_run = fmaxf(m_run, ml.x);
+    }
+    // A distinct instruction closing each stream's copy, so that the
+    // compiler does not merge the four copies into one indexed by stream
+    // (which would put the accumulators in scratch memory).
+    if constexpr (K == 0) asm volatile("; merge, stream 0");
+    else if constexpr (K == 1) asm volatile("; merge, stream 1");
+    else if constexpr (K == 2) asm volatile("; merge, stream 2");
+    else asm volatile("; merge, stream 3");
+}
+
 template <int D, bool FUSED>
 __global__ __launch_bounds__(kSpThreads, 1) void prefill_splitkv_pair_kernel(PrefillProblem p,
                                                                              float scale_log2,
@@ -865,11 +1052,11 @@ __global__ __launch_bounds__(kSpThreads, 1) void prefill_splitkv_pair_kernel(Pre
     using P = SpShape<D>;
     // Two buffers as separate arrays, so that the compiler can tell the one
     // being read from the one the loads are filling.  The merge reuses the
-    // second (s_b): 4 waves x 64 lanes x D/2 floats = one buffer exactly.
+    // second (s_b): 8 waves x 64 lanes x D/4 floats = one buffer exactly.
     __shared__ __align__(1024) uint16_t s_a[P::STAGE];
     __shared__ __align__(1024) uint16_t s_b[P::STAGE];
-    __shared__ float2 s_ml[4][64];
-    static_assert(4 * 64 * (D / 2) * 4 == P::STAGE * 2, "merge area is one buffer");
+    __shared__ float2 s_ml8[8][64];
+    static_assert(8 * 64 * (D / 4) * 4 == P::STAGE * 2, "merge area is one buffer");
 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int ql = lane & 31, kg = lane >> 5;
@@ -1034,57 +1221,28 @@ __global__ __launch_bounds__(kSpThreads, 1) void prefill_splitkv_pair_kernel(Pre
             load_q<D, FUSED>(qf, p, it.q0 + ql, it.h0 + sub, kg);
         }
 
-        // Merge: (m, l, O) of this wave's rows with a partner wave's, element
-        // by element (lanes hold the same rows and dims in every wave).
+        // Merge: the four streams' partials of each head in two exchange
+        // rounds in which every wave takes part (streams k and k ^ 2 swap
+        // halves of their O values, then k and k ^ 1 quarters of the kept
+        // half), in s_b; stream k then writes quarter k of its head's output.
         float l_tot = xor32_sum(l_run);
-        float4* const s_mrg = reinterpret_cast<float4*>(s_b);
-        auto put = [&](int slot) __attribute__((always_inline)) {
+        float4 part[P::DBLK];
+        float4* const area = reinterpret_cast<float4*>(s_b);
+        switch (stream) {
+            case 0: sp_merge_stream<0>(oacc, area, s_ml8, sw, lane, m_run, l_tot, part); break;
+            case 1: sp_merge_stream<1>(oacc, area, s_ml8, sw, lane, m_run, l_tot, part); break;
+            case 2: sp_merge_stream<2>(oacc, area, s_ml8, sw, lane, m_run, l_tot, part); break;
+            default: sp_merge_stream<3>(oacc, area, s_ml8, sw, lane, m_run, l_tot, part); break;
+        }
+        if (qq < p.s) {
+            const float inv = 1.0f / l_tot;
+            uint16_t* orow = p.o + ((int64_t)qq * p.hq + h) * D + 4 * kg;
 #pragma unroll
-            for (int db = 0; db < P::DBLK; ++db)
-#pragma unroll
-                for (int g = 0; g < 4; ++g)
-                    s_mrg[(slot * P::DBLK * 4 + db * 4 + g) * 64 + lane] =
-                        make_float4(oacc[db][4 * g], oacc[db][4 * g + 1], oacc[db][4 * g + 2], oacc[db][4 * g + 3]);
-            s_ml[slot][lane] = make_float2(m_run, l_tot);
-        };
-        auto take = [&](int slot) __attribute__((always_inline)) {
-            const float2 ml = s_ml[slot][lane];
-            const float M = fmaxf(m_run, ml.x);
-            const float wa = m_run == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m_run - M);
-            const float wb = ml.x == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(ml.x - M);
-#pragma unroll
-            for (int db = 0; db < P::DBLK; ++db)
-#pragma unroll
-                for (int g = 0; g < 4; ++g) {
-                    const float4 x = s_mrg[(slot * P::DBLK * 4 + db * 4 + g) * 64 + lane];
-                    oacc[db][4 * g] = fmaf(wb, x.x, wa * oacc[db][4 * g]);
-                    oacc[db][4 * g + 1] = fmaf(wb, x.y, wa * oacc[db][4 * g + 1]);
-                    oacc[db][4 * g + 2] = fmaf(wb, x.z, wa * oacc[db][4 * g + 2]);
-                    oacc[db][4 * g + 3] = fmaf(wb, x.w, wa * oacc[db][4 * g + 3]);
-                }
-            l_tot = fmaf(wb, ml.y, wa * l_tot);
-            m_run = M;
-        };
-        // The merge's barriers wait for LDS operations only (a release fence
-        // on LDS would also wait for the next item's tile loads into s_a).
-        if (stream >= 2) put(2 * sub + (stream & 1));
-        lds_ops_barrier();
-        if (stream < 2) take(2 * sub + stream);
-        lds_ops_barrier();
-        if (stream == 1) put(sub);
-        lds_ops_barrier();
-        if (stream == 0) {
-            take(sub);
-            if (qq < p.s) {
-                const float inv = 1.0f / l_tot;
-                uint16_t* orow = p.o + ((int64_t)qq * p.hq + h) * D + 4 * kg;
-#pragma unroll
-                for (int db = 0; db < P::DBLK; ++db)
-#pragma unroll
-                    for (int g = 0; g < 4; ++g)
-                        *reinterpret_cast<uint2*>(orow + 32 * db + 8 * g) =
-                            make_uint2(pack_bf16x2(oacc[db][4 * g] * inv, oacc[db][4 * g + 1] * inv),
-                                       pack_bf16x2(oacc[db][4 * g + 2] * inv, oacc[db][4 * g + 3] * inv));
+            for (int i = 0; i < P::DBLK; ++i) {
+                const int f = P::DBLK * stream + i;  // wave-uniform
+                *reinterpret_cast<uint2*>(orow + 32 * (f / 4) + 8 * (f % 4)) =
+                    make_uint2(pack_bf16x2(part[i].x * inv, part[i].y * inv),
+                               pack_bf16x2(part[i].z * inv, part[i].w * inv));
             }
         }
         if (!more) break;

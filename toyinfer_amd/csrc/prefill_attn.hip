@@ -478,13 +478,20 @@ __global__ __launch_bounds__(PAIR ? 512 : kPfThreads, PAIR ? 1 : 2) void prefill
     // re-read.  The tile buffers are free: every wave passed the last
     // step's barrier.  Each wave uses its own 32 x D region (16-byte chunk c
     // of row r at c ^ (r mod D/8)) and reads back only what it wrote (LDS
-    // operations of a wave complete in order).
+    // operations of a wave complete in order).  The 8-byte stores go to the
+    // banks 16 lanes at a time (128 bytes, 32 banks): lanes whose chunk
+    // positions differ by 8 (D = 128) or whose rows differ by 8 (D = 64)
+    // would meet on the same banks, so those with bit 3 of the position
+    // (D = 128) or of the row (D = 64) set store the two 8-byte halves of
+    // the chunk swapped, and the read-back swaps them again.
     const float l_tot = xor32_sum(l_run);  // all lanes take part in the exchange
     {
         constexpr int CPR = D / 8;
         const float inv = 1.0f / l_tot;  // (rows past S: not stored)
         uint16_t* so = ((wave >> 1) == 0 ? s_k0 : (wave >> 1) == 1 ? s_k1 : (wave >> 1) == 2 ? s_v0 : s_v1) +
                        (wave & 1) * 32 * D;
+        // Whether row r keeps the halves of the chunk at position pos swapped.
+        auto swapped = [](int r, int pos) { return ((D == 128 ? pos : r) >> 3) & 1; };
 #pragma unroll
         for (int db = 0; db < P::DBLK; ++db)
 #pragma unroll
@@ -492,13 +499,15 @@ __global__ __launch_bounds__(PAIR ? 512 : kPfThreads, PAIR ? 1 : 2) void prefill
                 uint2 w;
                 w.x = pack_bf16x2(oacc[db][4 * i4] * inv, oacc[db][4 * i4 + 1] * inv);
                 w.y = pack_bf16x2(oacc[db][4 * i4 + 2] * inv, oacc[db][4 * i4 + 3] * inv);
-                const int c = 4 * db + i4;
-                *reinterpret_cast<uint2*>(so + ql * D + 8 * (c ^ (ql & (CPR - 1))) + 4 * kg) = w;
+                const int pos = (4 * db + i4) ^ (ql & (CPR - 1));
+                *reinterpret_cast<uint2*>(so + ql * D + 8 * pos + 4 * (kg ^ swapped(ql, pos))) = w;
             }
 #pragma unroll
         for (int j = 0; j < 32 * CPR / 64; ++j) {
             const int f = 64 * j + lane, row = f / CPR, c = f % CPR;
-            const uint4 v = *reinterpret_cast<const uint4*>(so + row * D + 8 * (c ^ (row & (CPR - 1))));
+            const int pos = c ^ (row & (CPR - 1));
+            uint4 v = *reinterpret_cast<const uint4*>(so + row * D + 8 * pos);
+            if (swapped(row, pos)) v = make_uint4(v.z, v.w, v.x, v.y);
             const uint32_t q = q0 + row;
             if (q < p.s) stg16_nt(p.o + ((int64_t)q * p.hq + h) * D + 8 * c, v);
         }

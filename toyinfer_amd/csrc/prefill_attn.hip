@@ -871,8 +871,8 @@ __device__ __forceinline__ void lds_ops_barrier() {
 // A partner's N float4 (1 KiB apart: lane l at src + 16 l) and its (m, l)
 // pair, read from LDS in one asm block that also waits for them.  In asm
 // the reads are not LDS accesses to the compiler, which would otherwise make
-// them wait for every buffer load writing LDS (the next item's tiles and Q,
-// in flight into other buffers).
+// them wait for every buffer load writing LDS (the next item's first tiles,
+// in flight into the other buffer).
 template <int N>
 __device__ __forceinline__ float2 sp_read(float4 (&x)[N], const float4* src, const float2* ml, int lane) {
     const uint32_t a = (uint32_t)(size_t)(const __attribute__((address_space(3))) void*)(src + lane);

@@ -234,10 +234,12 @@ def test_gemm_segments_equal_separate_projections(dev, T, hid, rows):
         assert torch.equal(y.view(torch.int16), ref.view(torch.int16)), f"rows {r}"
 
 
-def test_gemm_residual_epilogue_equals_projection_then_add(dev):
+@pytest.mark.parametrize("T,H,M", [(700, 2048, 1024), (129, 512, 130)])
+def test_gemm_residual_epilogue_equals_projection_then_add(dev, T, H, M):
     """residual != 0: y = bf16(y + bf16(x W^T)), bit for bit the projection
-    followed by residual_add_bf16."""
-    T, H, M = 700, 2048, 1024
+    followed by residual_add_bf16 (M = 130: rows not 16-byte aligned, so the
+    epilogue's element stores)."""
+    print(f"[step] gemm residual T={T} H={H} M={M}", flush=True)
     g = torch.Generator(device=dev).manual_seed(38)
     x = torch.randn((T, H), generator=g, device=dev).to(torch.bfloat16)
     w = (torch.randn((M, H), generator=g, device=dev) * 0.05).to(torch.bfloat16)
@@ -254,11 +256,12 @@ def test_gemm_residual_epilogue_equals_projection_then_add(dev):
 
 
 @pytest.mark.parametrize("T,hid,M", [(1371, 1024, 3072), (4096, 1024, 3072), (300, 512, 3072),
-                                     (17, 256, 200)])
+                                     (17, 256, 200), (33, 256, 204)])
 def test_gemm_swiglu_equals_projections_then_swiglu(dev, T, hid, M):
     """Gate/up with SwiGLU in the GEMM epilogue (192 x 128, 256 x 256 and
-    128 x 128 tiles by grid size; a ragged last tile at M = 200) equals the
-    two projections followed by batch_swiglu_bf16x2, bit for bit."""
+    128 x 128 tiles by grid size; a ragged last tile at M = 200; M = 204:
+    rows not 16-byte aligned) equals the two projections followed by
+    batch_swiglu_bf16x2, bit for bit."""
     print(f"[step] gemm swiglu T={T} hid={hid} M={M}", flush=True)
     g = torch.Generator(device=dev).manual_seed(39)
     x = torch.randn((T, hid), generator=g, device=dev).to(torch.bfloat16)

@@ -62,11 +62,11 @@ SETTLE_S = 0.3
 # 256 MiB device-to-device copy (reads x2.0, writes x1.0); the summaries are
 # under profiles/.  (read KiB, write KiB) as the counters report them.
 PMC_KIB = {"prefill": (5566.0, 5484.0),            # prefill_splitkv_pair_kernel<128,false>
-           "prefill_fused": (83210.8, 65536.0),    # prefill_kernel<128,true,true>
-           "decode_b8_l4096": (65845.1, 1632.0),   # decode_split_kernel<128>
-           "decode_b1_l32768": (65622.0, 1632.0),  # decode_split_kernel<128>
+           "prefill_fused": (83509.4, 65536.0),    # prefill_kernel<128,true,true>
+           "decode_b8_l4096": (65844.9, 1632.0),   # decode_split_kernel<128>
+           "decode_b1_l32768": (65621.3, 1632.0),  # decode_split_kernel<128>
            "proj_gemv": (607798.8, 593.5),         # gemv_kernel<8,8,1,float>
-           "proj_gemm": (98482.0, 32768.0)}        # gemm_kernel<GmCfg<256,256,2,4,1,64>>
+           "proj_gemm": (98404.0, 32768.0)}        # gemm_kernel<GmCfg<256,256,2,4,1,64>>
 FETCH_SCALE, WRITE_SCALE = 2.0, 1.0
 
 

@@ -250,15 +250,23 @@ __device__ __host__ __forceinline__ uint32_t gm_out_tiles(const GemmArgs& g) {
 }
 
 // Epilogue staging: chunk c of staged row t (CR 16-byte chunks per row)
-// sits at ep_chunk<CR>(c, t), its two 8-byte halves swapped when bit 4 of t
-// is set.  The 8-byte writes (32 lanes per cycle over 64 banks) put 32
-// consecutive rows at one logical half chunk; rows whose starts share
-// their bank group (t & 1 with 128-byte rows, t & 3 with 64- or 192-byte
-// rows) get different chunks, and rows t and t + 16 different halves.  The
-// 16-byte read-back of consecutive chunks stays a permutation per row.
+// sits at ep_chunk<CR>(c, t), its two 8-byte halves swapped when
+// ep_swap<CR>(t).  An 8-byte LDS write serves 16 lanes per cycle from 32
+// banks (128 bytes), and the staging writes put 16 consecutive rows on 16
+// lanes at one logical half chunk, so those 16 (chunk, half) positions must
+// differ modulo 128 bytes: with 128-byte rows (CR 8) every row starts on the
+// same banks, the chunk takes bits 1-3 of t and the half bit 0; with 64- or
+// 192-byte rows (CR 4, 12) bit 0 of t picks the 64-byte half of the bank
+// line, the chunk takes bits 1-2 (within its aligned group of four) and the
+// half bit 3.  The 16-byte read-back (16 lanes per cycle from 64 banks) of
+// consecutive chunks of a row stays a permutation of the row's banks.
 template <int CR>
 __device__ __forceinline__ int ep_chunk(int c, int t) {
-    return CR == 8 ? c ^ ((t >> 1) & 7) : c ^ ((t >> 2) & 3);
+    return CR == 8 ? c ^ ((t >> 1) & 7) : c ^ ((t >> 1) & 3);
+}
+template <int CR>
+__device__ __forceinline__ int ep_swap(int t) {
+    return CR == 8 ? t & 1 : (t >> 3) & 1;
 }
 
 // Epilogue LDS accesses in asm: to the compiler they are not LDS accesses,
@@ -496,7 +504,7 @@ __global__ __launch_bounds__(C::THREADS, C::MINB) void gemm_kernel(GemmArgs g) {
                         else
                             e[u] = acc[i][j][4 * q + u];
                     }
-                    const int pc = ep_chunk<CR>(4 * j + q, t), h = (lane >> 5) ^ ((t >> 4) & 1);
+                    const int pc = ep_chunk<CR>(4 * j + q, t), h = (lane >> 5) ^ ep_swap<CR>(t);
                     ep_write(area + t * OUTC + 8 * pc + 4 * h, pack_bf16x2(e[0], e[1]),
                              pack_bf16x2(e[2], e[3]));
                 }
@@ -515,7 +523,7 @@ __global__ __launch_bounds__(C::THREADS, C::MINB) void gemm_kernel(GemmArgs g) {
         }
 #pragma unroll
         for (int k = 0; k < PER_LANE; ++k)
-            if ((lane + 64 * k) / CR & 16) stg[k] = make_uint4(stg[k].z, stg[k].w, stg[k].x, stg[k].y);
+            if (ep_swap<CR>((lane + 64 * k) / CR)) stg[k] = make_uint4(stg[k].z, stg[k].w, stg[k].x, stg[k].y);
         if (vec) {
 #pragma unroll
             for (int k = 0; k < PER_LANE; ++k) {

@@ -73,9 +73,10 @@ struct PfShape {
 //   K rows (A operand reads): chunk c at c ^ (row mod D/8).
 //   V rows (transposing reads, 4 rows x 64 bytes per half-wave at D = 128):
 //   chunk c at c ^ 4*(row & 3) (D = 128), c ^ 2*(row & 3) (D = 64).
-// With these maps SQ_LDS_BANK_CONFLICT reads 524288 cycles per launch at
-// S=8192, 32/8 heads (256 per workgroup, about 2 % of the LDS-active
-// cycles; the earlier c ^ (row & 7) / c ^ 2*(row & 3) gave 6.8e7).
+// With these maps, and the O staging described at the output stores,
+// SQ_LDS_BANK_CONFLICT reads 0 per launch for the 128-row kernels at
+// S=8192, 32/8 heads (the earlier c ^ (row & 7) / c ^ 2*(row & 3) gave
+// 6.8e7 cycles).
 template <int D, int NW = kPfThreads / 64>
 struct DmaShape {
     static constexpr int CPR = D / 8;

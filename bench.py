@@ -74,6 +74,7 @@ def traffic_bytes(workload):
     r, w = PMC_KIB[workload]
     return int(round((r * FETCH_SCALE + w * WRITE_SCALE) * 1024))
 WORKLOADS = ("all", "prefill", "prefill_fused", "decode_b8_l4096", "decode_b1_l32768",
+             "stream_128mib",
              "decode_step", "decode_contract", "decode_engine_lean", "proj_gemv", "proj_gemm", "qwen3_e2e",
              "sample", "copy_calibration", "torch_sdpa")
 
@@ -435,6 +436,33 @@ def bench_proj_gemv(dev, stream, steps, warmup, M=151936, N=4096):
             "roofline": roofline("hbm", gbs, PEAK_HBM_GBS, "GB/s", traffic_bytes("proj_gemv"))}
 
 
+def bench_stream_128mib(dev, stream, steps, warmup, sets=4, M=16384, N=4096):
+    """For scale beside the decode workloads: this library's most efficient
+    streaming kernel, the lm-head GEMV (gemv_proj_bf162float), over exactly
+    the decode step's 128 MiB (M x N bf16 weights, as many bytes as the K/V
+    of configs[2]), rotating `sets` weight sets as the decode bench rotates
+    its K/V sets.  It reads the same bytes and does almost nothing else, so
+    its step time bounds what a one-pass decode over 128 MiB can reach on
+    this GPU."""
+    import torch
+
+    from toyinfer_amd import attn
+
+    g = torch.Generator(device=dev).manual_seed(SEED + 41)
+    ws = [torch.randn((M, N), generator=g, device=dev).to(torch.bfloat16) for _ in range(sets)]
+    x = torch.randn((N,), generator=g, device=dev).to(torch.bfloat16)
+    y = torch.empty((M,), dtype=torch.float32, device=dev)
+    ms = time_steps(lambda i: attn.gemv_proj_bf162float(ws[i % sets], x, y, M, N, stream), steps,
+                    warmup, stream)
+    nbytes = 2.0 * M * N
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    return {"workload": f"stream_128MiB_gemv_m{M}_n{N}", "entry": "toyinfer_gemv_proj_bf162float",
+            "steps": steps, "ms_per_step": round(ms, 5), "value": round(gbs, 1), "unit": "GB/s",
+            "note": "for scale: 128 MiB of weights streamed once per call (the decode step's K/V "
+                    f"bytes), {sets} rotating sets; weight bytes / call time",
+            "roofline": roofline("hbm", gbs, PEAK_HBM_GBS, "GB/s")}
+
+
 def bench_proj_gemm(dev, stream, steps, warmup, T=4096, M=4096, N=4096):
     """A prefill projection (batch_gemv_proj_bf16, src/transformer.cpp:370-378)
     over 4096 tokens of Qwen3-8B's hidden size: the MFMA GEMM.  The note
@@ -697,6 +725,7 @@ def main():
                                                             2, lean=True),
         "proj_gemv": lambda: bench_proj_gemv(dev, stream, max(50, args.steps), 10),
         "proj_gemm": lambda: bench_proj_gemm(dev, stream, max(200, args.steps), 50),
+        "stream_128mib": lambda: bench_stream_128mib(dev, stream, max(50, args.steps * 2), 10),
         "sample": lambda: bench_sample(dev, stream, max(200, args.steps), 50),
         "qwen3_e2e": lambda: bench_qwen3_e2e(dev),
         "torch_sdpa": lambda: bench_torch_sdpa(dev, stream, 20, 3),
@@ -739,7 +768,8 @@ def main():
     }
     if not args.no_components:
         line["components"] = [comp[n]() for n in
-                              ("prefill", "decode_b8_l4096", "decode_b1_l32768", "decode_step",
+                              ("prefill", "decode_b8_l4096", "decode_b1_l32768", "stream_128mib",
+                               "decode_step",
                                "decode_contract", "decode_engine_lean", "proj_gemv",
                                "proj_gemm", "sample",
                                "qwen3_e2e", "torch_sdpa")]
